@@ -1,0 +1,770 @@
+// C-ABI implementation of include/aexq.h: contexts, library-owned weights, the
+// strict plan (kernel selection with diagnostics, never a fallback) and the
+// launches.  Reference citations use the aliases listed in include/aexq.h.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/aexq.h"
+#include "aexq_internal.hpp"
+
+using namespace aexq;
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+static thread_local std::string g_last_error;
+
+static aexq_status fail(aexq_status st, const char* op, const char* fmt, ...) {
+  char buf[768];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = std::string("aexq: ") + op + " failed | " + buf;
+  return st;
+}
+
+static aexq_status hip_fail(hipError_t e, const char* op, const char* what) {
+  return fail(e == hipErrorOutOfMemory ? AEXQ_ERR_OUT_OF_MEMORY : AEXQ_ERR_DEVICE, op,
+              "%s | hip=%s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(op, expr)                                   \
+  do {                                                      \
+    hipError_t _e = (expr);                                 \
+    if (_e != hipSuccess) return hip_fail(_e, op, #expr);   \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// objects
+// ---------------------------------------------------------------------------
+struct aexq_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  // argmax partial buffers, grown on demand
+  float* part_best = nullptr;
+  int* part_index = nullptr;
+  float* part_second = nullptr;
+  long long part_cap = 0;
+  float* logits_scratch = nullptr;
+  long long logits_cap = 0;
+};
+
+struct aexq_weight {
+  aexq_ctx* ctx = nullptr;
+  int bits = 8;
+  int n = 0, k = 0;
+  int block = 0;        // scale block in flat elements (k for per-row)
+  int scale_dtype = AEXQ_DTYPE_F32;
+  int nibble_code = AEXQ_NIBBLE_TWOS;
+  int batch = 1;
+  uint32_t* codes = nullptr;
+  void* scales = nullptr;
+  long long code_bytes = 0;    // per copy, unpadded
+  long long scale_count = 0;   // per copy
+  long long code_stride = 0;   // bytes between copies
+  long long scale_stride = 0;  // bytes between copies
+  bool owns = true;
+};
+
+static long long round_up(long long v, long long a) { return (v + a - 1) / a * a; }
+static int scale_bytes(int dtype) { return dtype == AEXQ_DTYPE_F16 ? 2 : 4; }
+
+extern "C" int aexq_abi_version(void) { return AEXQ_ABI_VERSION; }
+extern "C" const char* aexq_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" aexq_status aexq_create(int device, void* hip_stream, aexq_ctx** out) {
+  if (!out) return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_create", "out is NULL");
+  int count = 0;
+  HIP_TRY("aexq_create", hipGetDeviceCount(&count));
+  if (device < 0 || device >= count)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_create", "device=%d of %d", device, count);
+  HIP_TRY("aexq_create", hipSetDevice(device));
+  aexq_ctx* c = new aexq_ctx();
+  c->device = device;
+  c->stream = (hipStream_t)hip_stream;
+  *out = c;
+  return AEXQ_OK;
+}
+
+extern "C" void aexq_destroy(aexq_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipFree(ctx->part_best);
+  (void)hipFree(ctx->part_index);
+  (void)hipFree(ctx->part_second);
+  (void)hipFree(ctx->logits_scratch);
+  delete ctx;
+}
+
+extern "C" aexq_status aexq_set_stream(aexq_ctx* ctx, void* hip_stream) {
+  if (!ctx) return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_set_stream", "ctx is NULL");
+  ctx->stream = (hipStream_t)hip_stream;
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_synchronize(aexq_ctx* ctx) {
+  if (!ctx) return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_synchronize", "ctx is NULL");
+  HIP_TRY("aexq_synchronize", hipSetDevice(ctx->device));
+  HIP_TRY("aexq_synchronize", hipStreamSynchronize(ctx->stream));
+  return AEXQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// weights
+// ---------------------------------------------------------------------------
+static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const void* packed,
+                                 const void* scales, int scale_dtype, int n, int k, int block,
+                                 int nibble_code, aexq_weight** out) {
+  aexq_weight* w = new aexq_weight();
+  w->ctx = ctx;
+  w->bits = bits;
+  w->n = n;
+  w->k = k;
+  w->block = block;
+  w->scale_dtype = scale_dtype;
+  w->nibble_code = nibble_code;
+  const long long count = (long long)n * k;
+  const long long words = bits == 8 ? (count + 3) / 4 : (count + 7) / 8;
+  w->code_bytes = (words < 1 ? 1 : words) * 4;
+  w->scale_count = count / block;
+  w->code_stride = round_up(w->code_bytes, 256);
+  w->scale_stride = round_up(w->scale_count * scale_bytes(scale_dtype), 256);
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = hipMalloc((void**)&w->codes, w->code_stride);
+  if (e == hipSuccess) e = hipMalloc(&w->scales, w->scale_stride);
+  if (e == hipSuccess) e = hipMemset(w->codes, 0, w->code_stride);
+  if (e == hipSuccess) e = hipMemcpy(w->codes, packed, w->code_bytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess)
+    e = hipMemcpy(w->scales, scales, w->scale_count * scale_bytes(scale_dtype),
+                  hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(w->codes);
+    (void)hipFree(w->scales);
+    delete w;
+    return hip_fail(e, op, "weight upload");
+  }
+  *out = w;
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_weight_q8(aexq_ctx* ctx, const uint32_t* packed, const void* scales,
+                                      int scale_dtype, int n, int k, int block,
+                                      aexq_weight** out) {
+  const char* op = "aexq_weight_q8";
+  if (!ctx || !packed || !scales || !out)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (n <= 0 || k <= 0)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "n=%d k=%d must be positive", n, k);
+  if (scale_dtype != AEXQ_DTYPE_F16 && scale_dtype != AEXQ_DTYPE_F32)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "scale_dtype=%d", scale_dtype);
+  if (block == 0) block = k;
+  // GL:65-67 / GS:12893-12894: the direct Q8 path needs one scale per output row
+  if (block != k)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op,
+                "Direct Q8 upload must contain one scale per output channel | block=%d k=%d",
+                block, k);
+  return upload_weight(ctx, op, 8, packed, scales, scale_dtype, n, k, k, AEXQ_NIBBLE_TWOS, out);
+}
+
+extern "C" aexq_status aexq_weight_q4(aexq_ctx* ctx, const uint32_t* packed, const void* scales,
+                                      int scale_dtype, int n, int k, int block, int nibble_code,
+                                      aexq_weight** out) {
+  const char* op = "aexq_weight_q4";
+  if (!ctx || !packed || !scales || !out)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (n <= 0 || k <= 0)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "n=%d k=%d must be positive", n, k);
+  if (scale_dtype != AEXQ_DTYPE_F16 && scale_dtype != AEXQ_DTYPE_F32)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "scale_dtype=%d", scale_dtype);
+  if (nibble_code != AEXQ_NIBBLE_TWOS && nibble_code != AEXQ_NIBBLE_OFFSET8)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "nibble_code=%d", nibble_code);
+  // GS:12979-12980: the group must divide K
+  if (block <= 0 || k % block != 0)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op,
+                "Direct Q4 group size must divide the Gemm K dimension | block=%d k=%d", block, k);
+  return upload_weight(ctx, op, 4, packed, scales, scale_dtype, n, k, block, nibble_code, out);
+}
+
+// Unity Mathf.RoundToInt: ties to even; NaN / out of range -> int.MinValue (x64 CLR).
+static int round_to_int(float v) {
+  const double r = nearbyint((double)v);
+  if (isnan(r) || r >= 2147483648.0 || r < -2147483648.0) return INT32_MIN;
+  return (int)r;
+}
+static float unity_max(float a, float b) { return a > b ? a : b; }
+
+// GS:12838-12885 / GS:12912-12964: per output channel symmetric quantization.
+// The device copy is always [n][k] (transB); a [k][n] source is transposed
+// while packing, which keeps every code and scale identical.
+static aexq_status weight_from_f32(aexq_ctx* ctx, const char* op, int bits, const float* data,
+                                   int n, int k, int trans_b, aexq_weight** out) {
+  if (!ctx || !data || !out) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (n <= 0 || k <= 0)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "n=%d k=%d must be positive", n, k);
+  const long long count = (long long)n * k;
+  const int qmax = bits == 8 ? 127 : 7;
+  std::vector<uint32_t> packed(bits == 8 ? (count + 3) / 4 : (count + 7) / 8, 0u);
+  std::vector<float> scales(n);
+  for (int oc = 0; oc < n; ++oc) {
+    float max_abs = 0.0f;
+    for (int vi = 0; vi < k; ++vi) {
+      const long long src = trans_b ? (long long)oc * k + vi : (long long)vi * n + oc;
+      max_abs = unity_max(max_abs, fabsf(data[src]));
+    }
+    const float scale = max_abs > 0.0f ? max_abs / (float)qmax : 1.0f;
+    scales[oc] = scale;
+    for (int vi = 0; vi < k; ++vi) {
+      const long long src = trans_b ? (long long)oc * k + vi : (long long)vi * n + oc;
+      int q = round_to_int(data[src] / scale);
+      q = q < -qmax ? -qmax : (q > qmax ? qmax : q);
+      const long long dst = (long long)oc * k + vi;
+      if (bits == 8)
+        packed[dst >> 2] |= (uint32_t)(uint8_t)(int8_t)q << ((dst & 3) * 8);
+      else
+        packed[dst >> 3] |= ((uint32_t)q & 0xfu) << ((dst & 7) * 4);
+    }
+  }
+  return upload_weight(ctx, op, bits, packed.data(), scales.data(), AEXQ_DTYPE_F32, n, k, k,
+                       AEXQ_NIBBLE_TWOS, out);
+}
+
+extern "C" aexq_status aexq_weight_q8_from_f32(aexq_ctx* ctx, const float* data, int n, int k,
+                                               int trans_b, aexq_weight** out) {
+  return weight_from_f32(ctx, "aexq_weight_q8_from_f32", 8, data, n, k, trans_b, out);
+}
+
+extern "C" aexq_status aexq_weight_q4_from_f32(aexq_ctx* ctx, const float* data, int n, int k,
+                                               int trans_b, aexq_weight** out) {
+  return weight_from_f32(ctx, "aexq_weight_q4_from_f32", 4, data, n, k, trans_b, out);
+}
+
+extern "C" aexq_status aexq_weight_replicate(aexq_ctx* ctx, const aexq_weight* src, int batch,
+                                             aexq_weight** out) {
+  const char* op = "aexq_weight_replicate";
+  if (!ctx || !src || !out) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (batch <= 0) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "batch=%d", batch);
+  aexq_weight* w = new aexq_weight(*src);
+  w->ctx = ctx;
+  w->batch = batch;
+  w->owns = true;
+  w->codes = nullptr;
+  w->scales = nullptr;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = hipMalloc((void**)&w->codes, w->code_stride * batch);
+  if (e == hipSuccess) e = hipMalloc(&w->scales, w->scale_stride * batch);
+  for (int b = 0; b < batch && e == hipSuccess; ++b) {
+    e = hipMemcpy((char*)w->codes + b * w->code_stride, src->codes, src->code_stride,
+                  hipMemcpyDeviceToDevice);
+    if (e == hipSuccess)
+      e = hipMemcpy((char*)w->scales + b * w->scale_stride, src->scales, src->scale_stride,
+                    hipMemcpyDeviceToDevice);
+  }
+  if (e != hipSuccess) {
+    (void)hipFree(w->codes);
+    (void)hipFree(w->scales);
+    delete w;
+    return hip_fail(e, op, "replicate");
+  }
+  *out = w;
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_weight_alias(aexq_ctx* ctx, const aexq_weight* shared,
+                                         aexq_weight** out) {
+  if (!ctx || !shared || !out)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_weight_alias", "NULL argument");
+  aexq_weight* w = new aexq_weight(*shared);
+  w->ctx = ctx;
+  w->owns = false;
+  *out = w;
+  return AEXQ_OK;
+}
+
+extern "C" void aexq_weight_release(aexq_weight* w) {
+  if (!w) return;
+  if (w->owns) {
+    (void)hipSetDevice(w->ctx->device);
+    (void)hipFree(w->codes);
+    (void)hipFree(w->scales);
+  }
+  delete w;
+}
+
+extern "C" aexq_status aexq_weight_get_info(const aexq_weight* w, aexq_weight_info* out) {
+  if (!w || !out) return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_weight_get_info", "NULL argument");
+  out->bits = w->bits;
+  out->n = w->n;
+  out->k = w->k;
+  out->block = w->block;
+  out->scale_dtype = w->scale_dtype;
+  out->nibble_code = w->nibble_code;
+  out->batch = w->batch;
+  out->code_bytes = w->code_bytes;
+  out->scale_bytes = w->scale_count * scale_bytes(w->scale_dtype);
+  return AEXQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// tensors
+// ---------------------------------------------------------------------------
+struct TensorView {
+  int rows = 0;          // logical M
+  int width = 0;         // logical W
+  long long rstride = 0; // elements between rows
+  int padded = 0;        // row elements the layout stores (zero-filled tail)
+  int batch = 1;
+  long long bstride = 0;
+  int dtype = AEXQ_DTYPE_F16;
+  void* data = nullptr;
+};
+
+static bool same_shape(const aexq_shape& a, int dims, int w, int h, int d, int c) {
+  return a.dims == dims && a.w == w && a.h == h && a.d == d && a.c == c;
+}
+
+// Storage rules of GS:10818-10857 for the three supported layouts.
+static aexq_status view_tensor(const aexq_tensor* t, const char* op, const char* name,
+                               TensorView* v) {
+  if (!t) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "%s is NULL", name);
+  if (!t->data) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "%s.data is NULL", name);
+  if (t->dtype != AEXQ_DTYPE_F16 && t->dtype != AEXQ_DTYPE_F32)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "%s dtype=%d | rejectedFallback=dtype", name, t->dtype);
+  const aexq_shape& L = t->logical;
+  const int W = L.w > 1 ? L.w : 1;
+  const int H = L.dims >= 2 ? (L.h > 1 ? L.h : 1) : 1;
+  v->rows = H;
+  v->width = W;
+  v->dtype = t->dtype;
+  v->data = t->data;
+  v->batch = t->batch > 0 ? t->batch : 1;
+  v->bstride = t->batch_stride;
+  if (L.dims > 2 && (L.d > 1 || L.c > 1))
+    return fail(AEXQ_ERR_SHAPE, op, "%s logical dims=%d d=%d c=%d is not a 2-D matrix", name,
+                L.dims, L.d, L.c);
+  const int packs = (W + 3) / 4;
+  switch (t->layout) {
+    case AEXQ_LAYOUT_LINEAR:
+      if (!(same_shape(t->storage, 2, W, H, 1, 1) || same_shape(t->storage, L.dims, L.w, L.h, L.d, L.c)))
+        return fail(AEXQ_ERR_SHAPE, op, "%s LinearMat storage {%d,%d,%d,%d,%d} != logical [%d][%d]",
+                    name, t->storage.dims, t->storage.w, t->storage.h, t->storage.d,
+                    t->storage.c, H, W);
+      v->rstride = W;
+      v->padded = W;
+      break;
+    case AEXQ_LAYOUT_PACK4_LINEAR:
+      // ResolvePack4LinearMatStorageShape: {3, ceil(w/4), h, 1, 4}
+      if (!same_shape(t->storage, 3, packs, H, 1, 4))
+        return fail(AEXQ_ERR_SHAPE, op,
+                    "%s Pack4 storage {%d,%d,%d,%d,%d} != {3,%d,%d,1,4}", name, t->storage.dims,
+                    t->storage.w, t->storage.h, t->storage.d, t->storage.c, packs, H);
+      v->rstride = (long long)packs * 4;
+      v->padded = packs * 4;
+      break;
+    case AEXQ_LAYOUT_PACK4_TILED: {
+      // ResolvePack4TiledLinearMatStorageShape: {3, tileWidth, h*tileRows, 1, 4}
+      const int tw = t->storage.w;
+      if (t->storage.dims != 3 || t->storage.c != 4 || t->storage.d != 1 || tw <= 0 ||
+          t->storage.h % H != 0)
+        return fail(AEXQ_ERR_SHAPE, op, "%s tiled storage {%d,%d,%d,%d,%d} is not Pack4 tiled",
+                    name, t->storage.dims, t->storage.w, t->storage.h, t->storage.d,
+                    t->storage.c);
+      const int tile_rows = t->storage.h / H;
+      if ((long long)tw * tile_rows < packs || tile_rows != (packs + tw - 1) / tw)
+        return fail(AEXQ_ERR_SHAPE, op, "%s tiled storage %dx%d cannot hold %d packs", name, tw,
+                    tile_rows, packs);
+      v->rstride = (long long)tw * tile_rows * 4;
+      v->padded = packs * 4;
+      break;
+    }
+    case AEXQ_LAYOUT_HEAD_PACKED:
+      return fail(AEXQ_ERR_UNSUPPORTED, op,
+                  "%s layout=HEAD_PACKED | rejectedFallback=attention-head-packed Gemm", name);
+    default:
+      return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "%s layout=%d", name, t->layout);
+  }
+  return AEXQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// strict plan
+// ---------------------------------------------------------------------------
+struct Plan {
+  bool fast = false;
+  QmvConfig cfg{};
+  int rwg = 0;
+  QmvParams p{};
+  int grid = 0;
+};
+
+static const char* kLinearOp = "aexq_linear";
+
+static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const* ws,
+                             const aexq_tensor* x, const aexq_tensor* const* ys,
+                             const aexq_linear_args* args, bool argmax, Plan* plan) {
+  const char* op = argmax ? "aexq_lmhead_argmax" : kLinearOp;
+  if (!ctx) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "ctx is NULL");
+  if (count <= 0 || count > kMaxGroup)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "group count=%d (1..%d)", count, kMaxGroup);
+  aexq_linear_args def{};
+  def.alpha = 1.0f;
+  def.beta = 1.0f;
+  def.broadcast_c = -1;
+  def.rms_eps = 0.001f;
+  const aexq_linear_args& a = args ? *args : def;
+  const unsigned known = AEXQ_EPI_RMSNORM_IN | AEXQ_EPI_SWIGLU_OUT | AEXQ_EPI_RESIDUAL_ADD;
+  if (a.flags & ~known) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "flags=0x%x", a.flags);
+  const aexq_weight* w0 = ws[0];
+  if (!w0) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "weight is NULL");
+  for (int i = 1; i < count; ++i) {
+    if (!ws[i]) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "weight %d is NULL", i);
+    if (ws[i]->bits != w0->bits || ws[i]->k != w0->k || ws[i]->batch != w0->batch ||
+        ws[i]->block != w0->block || ws[i]->scale_dtype != w0->scale_dtype ||
+        ws[i]->nibble_code != w0->nibble_code)
+      return fail(AEXQ_ERR_UNSUPPORTED, op,
+                  "group member %d differs in bits/k/batch/block/scales | rejectedFallback=group", i);
+  }
+  const bool swiglu = (a.flags & AEXQ_EPI_SWIGLU_OUT) != 0;
+  if (swiglu) {
+    if (count != 1) return fail(AEXQ_ERR_UNSUPPORTED, op, "SwiGLU-out takes one gate/up pair");
+    const aexq_weight* up = a.up;
+    if (!up) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "SwiGLU-out without the up weight");
+    if (up->bits != w0->bits || up->n != w0->n || up->k != w0->k || up->batch != w0->batch ||
+        up->block != w0->block || up->scale_dtype != w0->scale_dtype ||
+        up->nibble_code != w0->nibble_code || up->code_stride != w0->code_stride ||
+        up->scale_stride != w0->scale_stride)
+      return fail(AEXQ_ERR_SHAPE, op, "SwiGLU gate/up weights differ in shape or format");
+    if (a.c) return fail(AEXQ_ERR_UNSUPPORTED, op, "SwiGLU-out with a C (bias) term");
+  }
+  if (argmax && (swiglu || (a.flags & AEXQ_EPI_RESIDUAL_ADD)))
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "LM head takes no SwiGLU/residual epilogue");
+
+  TensorView xv;
+  aexq_status st = view_tensor(x, op, "x", &xv);
+  if (st) return st;
+  const int K = w0->k;
+  if (xv.width != K)
+    return fail(AEXQ_ERR_SHAPE, op, "x width=%d != weight K=%d | layer=Gemm", xv.width, K);
+  const int M = xv.rows;
+  if (xv.batch != 1 && xv.batch != w0->batch)
+    return fail(AEXQ_ERR_SHAPE, op, "x batch=%d vs weight batch=%d", xv.batch, w0->batch);
+
+  // output views
+  TensorView yv[kMaxGroup];
+  for (int i = 0; i < count; ++i) {
+    if (!ys[i]) {
+      if (!argmax) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "y %d is NULL", i);
+      yv[i] = TensorView{};
+      yv[i].rows = M;
+      yv[i].width = ws[i]->n;
+      yv[i].rstride = ws[i]->n;
+      yv[i].padded = ws[i]->n;
+      yv[i].dtype = AEXQ_DTYPE_F32;
+      continue;
+    }
+    st = view_tensor(ys[i], op, "y", &yv[i]);
+    if (st) return st;
+    if (yv[i].width != ws[i]->n || yv[i].rows != M)
+      return fail(AEXQ_ERR_SHAPE, op, "y %d is [%d][%d], expected [%d][%d]", i, yv[i].rows,
+                  yv[i].width, M, ws[i]->n);
+    if (yv[i].batch != w0->batch)
+      return fail(AEXQ_ERR_SHAPE, op, "y batch=%d vs weight batch=%d", yv[i].batch, w0->batch);
+    if (yv[i].dtype != yv[0].dtype)
+      return fail(AEXQ_ERR_UNSUPPORTED, op, "group outputs differ in dtype");
+    if (ys[i]->layout != ys[0]->layout)
+      return fail(AEXQ_ERR_UNSUPPORTED, op, "group outputs differ in layout");
+    if (yv[i].rstride != yv[0].rstride)
+      return fail(AEXQ_ERR_UNSUPPORTED, op, "group outputs differ in row stride");
+  }
+  if (argmax && yv[0].dtype != AEXQ_DTYPE_F32)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "LM-head logits must be fp32");
+  TensorView rv;
+  if (a.flags & AEXQ_EPI_RESIDUAL_ADD) {
+    st = view_tensor(a.residual, op, "residual", &rv);
+    if (st) return st;
+    if (rv.rows != M || rv.width != yv[0].width || rv.dtype != yv[0].dtype ||
+        rv.rstride != yv[0].rstride || count != 1)
+      return fail(AEXQ_ERR_SHAPE, op, "residual must match y in shape, layout and dtype");
+  }
+  if (a.c) {
+    if (a.broadcast_c != -1 && a.broadcast_c != 0 && a.broadcast_c != 1 && a.broadcast_c != 2 &&
+        a.broadcast_c != 3 && a.broadcast_c != 4)
+      return fail(AEXQ_ERR_UNSUPPORTED, op, "Gemm broadcast_type_C unsupported: %d",
+                  a.broadcast_c);
+    if (count != 1 && (a.broadcast_c == 3 || a.broadcast_c == 4))
+      return fail(AEXQ_ERR_UNSUPPORTED, op, "per-column C in a grouped launch");
+  }
+  if (a.flags & AEXQ_EPI_RMSNORM_IN) {
+    if (a.rms_gamma && a.rms_gamma_size <= 0)
+      return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "rms_gamma_size=%d", a.rms_gamma_size);
+  }
+
+  // ---- kernel selection (no fallback to anything but another GPU kernel)
+  const int fmt = w0->bits == 8 ? kQ8 : kQ4;
+  const bool chunked = fmt == kQ8 ? (K % 16 == 0) : (K % 32 == 0);
+  const int chunks = chunked ? (fmt == kQ8 ? K / 16 : K / 32) : 0;
+  const bool g16 = fmt == kQ4 && w0->block == 16;
+  const bool group_ok = fmt == kQ8 || g16 || (w0->block % 32 == 0);
+  const bool x_ok = xv.dtype == AEXQ_DTYPE_F16 && xv.rstride % 8 == 0 &&
+                    ((uintptr_t)xv.data % 16) == 0 && (xv.batch == 1 || xv.bstride % 8 == 0);
+  const bool m_ok = M <= 8;
+  const bool fast = chunked && group_ok && x_ok && m_ok && chunks > 0 && chunks <= 256;
+  plan->fast = fast;
+  if (fast) {
+    int lpr, cpl;
+    if (chunks <= 16) {
+      lpr = 16;
+      cpl = 1;
+    } else if (chunks <= 32) {
+      lpr = 32;
+      cpl = 1;
+    } else {
+      lpr = 64;
+      cpl = (chunks + 63) / 64;
+      if (cpl == 3) cpl = 4;
+    }
+    plan->cfg = QmvConfig{fmt, lpr, cpl, M == 1 ? 1 : 8, swiglu, argmax, g16};
+    if (!qmv_has_config(plan->cfg)) {
+      if (argmax) {
+        plan->fast = false;  // logits by the matvec kernel, argmax as a second pass
+        plan->cfg.argmax = false;
+      }
+      if (!qmv_has_config(plan->cfg))
+        return fail(AEXQ_ERR_UNSUPPORTED, op,
+                    "no kernel for bits=%d K=%d M=%d swiglu=%d | rejectedFallback=Gemm", w0->bits,
+                    K, M, (int)swiglu);
+    }
+    plan->rwg = qmv_rows_per_wg(plan->cfg);
+  } else {
+    if (swiglu)
+      return fail(AEXQ_ERR_UNSUPPORTED, op,
+                  "SwiGLU-out needs K aligned to 16-byte code chunks, fp16 x and M<=8 | K=%d M=%d "
+                  "| rejectedFallback=SwiGLU",
+                  K, M);
+    plan->cfg = QmvConfig{fmt, 0, 0, 0, false, false, g16};
+    plan->rwg = generic_rows_per_wg();
+  }
+
+  // ---- parameters
+  QmvParams& p = plan->p;
+  p = QmvParams{};
+  p.nmat = count;
+  p.batch = w0->batch;
+  p.k = K;
+  p.m = M;
+  p.group = w0->block;
+  p.groups_per_row = K / w0->block;
+  p.chunks = chunks;
+  p.xor_mask = (fmt == kQ4 && w0->nibble_code == AEXQ_NIBBLE_TWOS) ? 0x88888888u : 0u;
+  p.x_rstride = xv.rstride;
+  p.y_rstride = yv[0].rstride;
+  p.r_rstride = (a.flags & AEXQ_EPI_RESIDUAL_ADD) ? rv.rstride : 0;
+  p.alpha = a.alpha;
+  p.beta = a.beta;
+  p.c = a.c;
+  p.bcast = a.c ? a.broadcast_c : -1;
+  p.c_rstride = w0->n;
+  p.gamma = (a.flags & AEXQ_EPI_RMSNORM_IN) ? a.rms_gamma : nullptr;
+  p.gamma_size = a.rms_gamma_size;
+  p.eps = a.rms_eps;
+  int flags = 0;
+  if (a.flags & AEXQ_EPI_RMSNORM_IN) flags |= kFlagRms;
+  if (a.flags & AEXQ_EPI_RESIDUAL_ADD) flags |= kFlagResidual;
+  if (yv[0].dtype == AEXQ_DTYPE_F32) flags |= kFlagYf32;
+  // MM:1101 (Pack4 linear / LinearMat) vs MM:2301 (tiled)
+  const int ylayout = ys[0] ? ys[0]->layout : AEXQ_LAYOUT_LINEAR;
+  if (ylayout != AEXQ_LAYOUT_PACK4_TILED) flags |= kFlagAlphaIn;
+  if (w0->scale_dtype == AEXQ_DTYPE_F16) flags |= kFlagScaleF16;
+  if (xv.dtype == AEXQ_DTYPE_F32) flags |= kFlagXf32;
+  p.flags = flags;
+
+  int tiles_total = 0;
+  for (int i = 0; i < count; ++i) {
+    const aexq_weight* w = ws[i];
+    QmvMat& mt = p.mat[i];
+    mt.w = w->codes;
+    mt.s = w->scales;
+    mt.w2 = swiglu ? a.up->codes : nullptr;
+    mt.s2 = swiglu ? a.up->scales : nullptr;
+    mt.x = xv.data;
+    mt.y = ys[i] ? yv[i].data : nullptr;
+    mt.res = (a.flags & AEXQ_EPI_RESIDUAL_ADD) ? rv.data : nullptr;
+    mt.w_bstride = w->code_stride / 4;
+    mt.s_bstride = w->scale_stride / scale_bytes(w->scale_dtype);
+    mt.x_bstride = xv.batch == 1 ? 0 : xv.bstride;
+    mt.y_bstride = ys[i] ? yv[i].bstride : 0;
+    mt.r_bstride = (a.flags & AEXQ_EPI_RESIDUAL_ADD) ? rv.bstride : 0;
+    mt.n = w->n;
+    mt.n_store = ys[i] ? yv[i].padded : w->n;
+    mt.tiles = (mt.n_store + plan->rwg - 1) / plan->rwg;
+    mt.tile_base = tiles_total;
+    const long long add = (long long)mt.tiles * w->batch;
+    if (tiles_total + add > 0x7fffffffLL) return fail(AEXQ_ERR_UNSUPPORTED, op, "grid too large");
+    tiles_total += (int)add;
+  }
+  plan->grid = tiles_total;
+  return AEXQ_OK;
+}
+
+static aexq_status launch_plan(aexq_ctx* ctx, Plan& plan, const char* op) {
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  hipError_t e = plan.fast ? qmv_launch(plan.cfg, plan.p, plan.grid, ctx->stream)
+                           : generic_launch(plan.cfg.fmt, plan.p, plan.grid, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "kernel launch");
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
+                                       const aexq_tensor* y, const aexq_linear_args* args,
+                                       char* diag, size_t diag_len) {
+  Plan plan;
+  const aexq_weight* ws[1] = {w};
+  const aexq_tensor* ys[1] = {y};
+  aexq_status st = make_plan(ctx, 1, ws, x, ys, args, false, &plan);
+  if (diag && diag_len) {
+    if (st)
+      snprintf(diag, diag_len, "%s", g_last_error.c_str());
+    else
+      snprintf(diag, diag_len, "kernel=%s bits=%d lpr=%d cpl=%d mmax=%d swiglu=%d grid=%d",
+               plan.fast ? "qmv" : "generic", w->bits, plan.cfg.lpr, plan.cfg.cpl,
+               plan.cfg.mmax, (int)plan.cfg.pair, plan.grid);
+  }
+  return st;
+}
+
+extern "C" aexq_status aexq_linear(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
+                                   const aexq_tensor* y, const aexq_linear_args* args) {
+  Plan plan;
+  const aexq_weight* ws[1] = {w};
+  const aexq_tensor* ys[1] = {y};
+  aexq_status st = make_plan(ctx, 1, ws, x, ys, args, false, &plan);
+  if (st) return st;
+  return launch_plan(ctx, plan, kLinearOp);
+}
+
+extern "C" aexq_status aexq_linear_group(aexq_ctx* ctx, int count, const aexq_weight* const* w,
+                                         const aexq_tensor* x, const aexq_tensor* const* y,
+                                         const aexq_linear_args* args) {
+  if (!w || !y) return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_linear_group", "NULL arrays");
+  Plan plan;
+  aexq_status st = make_plan(ctx, count, w, x, y, args, false, &plan);
+  if (st) return st;
+  return launch_plan(ctx, plan, "aexq_linear_group");
+}
+
+static aexq_status ensure_parts(aexq_ctx* ctx, long long need, const char* op) {
+  if (need <= ctx->part_cap) return AEXQ_OK;
+  (void)hipFree(ctx->part_best);
+  (void)hipFree(ctx->part_index);
+  (void)hipFree(ctx->part_second);
+  ctx->part_best = nullptr;
+  ctx->part_index = nullptr;
+  ctx->part_second = nullptr;
+  ctx->part_cap = 0;
+  HIP_TRY(op, hipMalloc((void**)&ctx->part_best, need * sizeof(float)));
+  HIP_TRY(op, hipMalloc((void**)&ctx->part_index, need * sizeof(int)));
+  HIP_TRY(op, hipMalloc((void**)&ctx->part_second, need * sizeof(float)));
+  ctx->part_cap = need;
+  return AEXQ_OK;
+}
+
+static aexq_status argmax_over_logits(aexq_ctx* ctx, const float* logits, int m, int n,
+                                      long long rstride, int32_t* argmax, float* gap,
+                                      const char* op) {
+  const int parts = (n + logits_argmax_cols_per_wg() - 1) / logits_argmax_cols_per_wg();
+  aexq_status st = ensure_parts(ctx, (long long)parts * m, op);
+  if (st) return st;
+  hipError_t e = logits_argmax_launch(logits, m, n, rstride, ctx->part_best, ctx->part_index,
+                                      ctx->part_second, parts, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "argmax launch");
+  ArgmaxParams ap{ctx->part_best, ctx->part_index, ctx->part_second, parts, m, argmax, gap};
+  e = argmax_finalize_launch(ap, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
+                                          const aexq_tensor* x, const aexq_tensor* logits,
+                                          int32_t* argmax, float* top2_gap) {
+  const char* op = "aexq_lmhead_argmax";
+  if (!argmax) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "argmax is NULL");
+  if (w && w->batch != 1) return fail(AEXQ_ERR_UNSUPPORTED, op, "stacked LM head");
+  Plan plan;
+  const aexq_weight* ws[1] = {w};
+  const aexq_tensor* ys[1] = {logits};
+  aexq_status st = make_plan(ctx, 1, ws, x, ys, nullptr, true, &plan);
+  if (st) return st;
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  const int M = plan.p.m;
+  if (plan.fast && plan.cfg.argmax) {
+    const int parts = plan.p.mat[0].tiles;
+    st = ensure_parts(ctx, (long long)parts * M, op);
+    if (st) return st;
+    plan.p.part_best = ctx->part_best;
+    plan.p.part_index = ctx->part_index;
+    plan.p.part_second = ctx->part_second;
+    plan.p.parts = parts;
+    hipError_t e = qmv_launch(plan.cfg, plan.p, plan.grid, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, op, "lm head launch");
+    ArgmaxParams ap{ctx->part_best, ctx->part_index, ctx->part_second, parts, M, argmax,
+                    top2_gap};
+    e = argmax_finalize_launch(ap, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
+    return AEXQ_OK;
+  }
+  // logits first (into the caller's tensor or a scratch buffer), then the argmax pass
+  float* lg = nullptr;
+  long long rstride = plan.p.y_rstride;
+  if (logits) {
+    lg = (float*)logits->data;
+  } else {
+    const long long need = (long long)M * w->n;
+    if (need > ctx->logits_cap) {
+      (void)hipFree(ctx->logits_scratch);
+      ctx->logits_scratch = nullptr;
+      ctx->logits_cap = 0;
+      HIP_TRY(op, hipMalloc((void**)&ctx->logits_scratch, need * sizeof(float)));
+      ctx->logits_cap = need;
+    }
+    lg = ctx->logits_scratch;
+    plan.p.mat[0].y = lg;
+    plan.p.y_rstride = w->n;
+    plan.p.flags |= kFlagYf32;
+    rstride = w->n;
+  }
+  st = launch_plan(ctx, plan, op);
+  if (st) return st;
+  return argmax_over_logits(ctx, lg, M, w->n, rstride, argmax, top2_gap, op);
+}
+
+extern "C" aexq_status aexq_argmax(aexq_ctx* ctx, const aexq_tensor* logits, int32_t* argmax,
+                                   float* top2_gap) {
+  const char* op = "aexq_argmax";
+  if (!ctx || !argmax) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  TensorView v;
+  aexq_status st = view_tensor(logits, op, "logits", &v);
+  if (st) return st;
+  if (v.dtype != AEXQ_DTYPE_F32)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "logits dtype must be fp32 | rejectedFallback=dtype");
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  return argmax_over_logits(ctx, (const float*)v.data, v.rows, v.width, v.rstride, argmax,
+                            top2_gap, op);
+}
+
+extern "C" aexq_status aexq_dequant(aexq_ctx* ctx, const aexq_weight* w, float* out) {
+  const char* op = "aexq_dequant";
+  if (!ctx || !w || !out) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  const int fmt = w->bits == 8 ? kQ8 : kQ4;
+  const uint32_t xm = (fmt == kQ4 && w->nibble_code == AEXQ_NIBBLE_TWOS) ? 0x88888888u : 0u;
+  hipError_t e = dequant_launch(fmt, w->codes, w->scales, w->scale_dtype == AEXQ_DTYPE_F16, w->n,
+                                w->k, w->block, xm, out, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "dequant launch");
+  return AEXQ_OK;
+}

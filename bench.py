@@ -1,0 +1,288 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized decode-linear path on one MI355X.
+
+Workload (benchmark config 2, the metric's configuration): one decoder layer's
+seven Q4 linears at M=1 (q 1024->2048, k/v 1024->512, o 2048->1024,
+gate/up 1024->3584, down 3584->1024), symmetric 4-bit offset-8 codes with one
+fp16 scale per 32 K, fp16 activations, fp32 accumulation, fp16 outputs.
+
+"Cold" follows the sustained protocol of the benchmark: COPIES distinct
+device copies of the layer's weights (>= 1 GiB in total, far above the 256 MB
+Infinity Cache and the L2s) are processed in every step, so no weight byte is
+re-read from a cache.  One step = the layer's linears over all copies in four
+launches: RMSNorm-in + q/k/v (one grouped launch), RMSNorm-in + gate/up with
+the SwiGLU-out epilogue, o_proj (input: that copy's q output), down (input:
+that copy's SwiGLU output).
+
+value = COPIES * algorithmic bytes of one layer / wall time of one step, where
+the algorithmic bytes count every code, scale, activation and output once
+(9,142,272 + 46,080 = 9,188,352 B per layer).  The JSON line also carries the
+roofline of the dominant launch (HIP events on the launch stream) and the
+reference CPU path (RunGemmCpu restated in C) timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+METRIC = ("cold-HBM GB/s (% of peak) per quant matvec; decode tokens/s, 0.8B-shape, 1 GPU")
+HBM_PEAK_GBS = 8000.0
+LAYER_WEIGHT_BYTES = 9_142_272
+LAYER_ACT_BYTES = 46_080
+LAYER_BYTES = LAYER_WEIGHT_BYTES + LAYER_ACT_BYTES
+GIB = 1 << 30
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--copies", type=int, default=0,
+                    help="layer copies per step (default: enough for >= 1 GiB)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the per-config extras")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Layer:
+    """One stacked copy set of the seven Q4 linears plus the activation buffers."""
+
+    def __init__(self, ctx, aexq, synth, torch, copies: int, seed: int):
+        self.copies = copies
+        self.aexq = aexq
+        self.ctx = ctx
+        dims = {name: (n, k) for name, n, k in synth.LAYER_LINEARS}
+        self.dims = dims
+        self.w = {}
+        for i, (name, n, k) in enumerate(synth.LAYER_LINEARS):
+            words, scales, _ = synth.q4_weights(n, k, seed + i, group=32, code=synth.NIBBLE_OFFSET8)
+            base = ctx.weight(aexq.QuantizedTensor(n * k, 32, words, scales, bits=4,
+                                                   nibble_code=synth.NIBBLE_OFFSET8), n, k)
+            self.w[name] = base.replicate(copies)
+            base.release()
+        dev = "cuda"
+        x = torch.as_tensor(synth.activations(1, 1024, seed + 100)).to(dev)
+        self.x = x.reshape(-1)
+        self.gamma = torch.as_tensor(synth.rms_gamma(1024, seed + 101)).to(dev)
+        P4 = aexq.LAYOUT_PACK4_LINEAR
+        self.out = {}
+        for name in ("q_proj", "k_proj", "v_proj", "o_proj", "down_proj"):
+            n = dims[name][0]
+            self.out[name] = torch.zeros(copies * n, dtype=torch.float16, device=dev)
+        self.h = torch.zeros(copies * 3584, dtype=torch.float16, device=dev)
+        d = aexq.describe
+        self.xd = d(self.x, 1, 1024)
+        self.yd = {name: d(t, 1, dims[name][0], P4, batch=copies, batch_stride=dims[name][0])
+                   for name, t in self.out.items()}
+        self.hd = d(self.h, 1, 3584, P4, batch=copies, batch_stride=3584)
+        # o_proj reads that copy's q output (2048 wide); down reads the SwiGLU output
+        self.o_in = d(self.out["q_proj"], 1, 2048, P4, batch=copies, batch_stride=2048)
+        self.down_in = d(self.h, 1, 3584, P4, batch=copies, batch_stride=3584)
+        self.eps = 1e-6
+
+    def launch(self, i: int):
+        c, w = self.ctx, self.w
+        if i == 0:
+            c.linear_group([w["q_proj"], w["k_proj"], w["v_proj"]], self.xd,
+                           [self.yd["q_proj"], self.yd["k_proj"], self.yd["v_proj"]],
+                           rmsnorm=True, rms_gamma=self.gamma, rms_eps=self.eps)
+        elif i == 1:
+            c.linear(w["gate_proj"], self.xd, self.hd, rmsnorm=True, rms_gamma=self.gamma,
+                     rms_eps=self.eps, up=w["up_proj"])
+        elif i == 2:
+            c.linear(w["o_proj"], self.o_in, self.yd["o_proj"])
+        else:
+            c.linear(w["down_proj"], self.down_in, self.yd["down_proj"])
+
+    # algorithmic bytes of each launch for ONE copy (codes + scales + activations)
+    def launch_bytes(self, i: int) -> int:
+        def wb(n, k):
+            return n * k // 2 + n * (k // 32) * 2
+        d = self.dims
+        if i == 0:
+            return sum(wb(*d[nm]) + (d[nm][1] + d[nm][0]) * 2 for nm in ("q_proj", "k_proj", "v_proj"))
+        if i == 1:
+            return sum(wb(*d[nm]) + (d[nm][1] + d[nm][0]) * 2 for nm in ("gate_proj", "up_proj"))
+        if i == 2:
+            return wb(*d["o_proj"]) + (2048 + 1024) * 2
+        return wb(*d["down_proj"]) + (3584 + 1024) * 2
+
+    def step(self):
+        for i in range(4):
+            self.launch(i)
+
+
+def time_launches(torch, fn, reps: int):
+    """Average duration (ms) of fn() measured with HIP events on the current stream."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in evs)
+    return sum(ts) / len(ts), ts[len(ts) // 2]
+
+
+def extras(torch, aexq, synth, ctx):
+    """Per-config kernel measurements (sustained cold via rotating copies)."""
+    out = {}
+    # config 1: Q8 M=1 K=1024 N=3584, copies rotated so each launch is cold
+    n, k = 3584, 1024
+    words, scales, _ = synth.q8_weights(n, k, synth.SEED_BASE + 1)
+    base = ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
+    copies = 320
+    stack = base.replicate(copies)
+    base.release()
+    x = torch.as_tensor(synth.activations(1, k, 7)).cuda().reshape(-1)
+    y = torch.zeros(copies * n, dtype=torch.float16, device="cuda")
+    xd = aexq.describe(x, 1, k)
+    yd = aexq.describe(y, 1, n, aexq.LAYOUT_PACK4_LINEAR, batch=copies, batch_stride=n)
+    bytes1 = n * k + n * 2 + k * 2 + n * 2
+    for _ in range(3):
+        ctx.linear(stack, xd, yd)
+    avg, med = time_launches(torch, lambda: ctx.linear(stack, xd, yd), 20)
+    out["config1_q8_m1_sustained"] = {"copies_per_launch": copies, "bytes_per_matvec": bytes1,
+                                      "ms_per_launch": avg,
+                                      "GBps": copies * bytes1 / (avg * 1e-3) / 1e9}
+    stack.release()
+    del y
+    # config 5: LM head Q8 K=1024 N=151936 with fused argmax, M=1 and M=8.
+    n, k = synth.VOCAB, synth.HIDDEN
+    words, scales, _ = synth.q8_weights(n, k, synth.SEED_BASE + 5)
+    heads = [ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
+             for _ in range(8)]         # 8 x 156 MB rotated: each call is cold
+    for m in (1, 8):
+        xm = torch.as_tensor(synth.activations(m, k, 9)).cuda()
+        xmd = aexq.describe(xm, m, k)
+        lay = aexq.LAYOUT_PACK4_TILED
+        logits = aexq.new_activation(m, n, torch.float32, lay)
+        ld = aexq.describe(logits, m, n, lay)
+        am = torch.zeros(m, dtype=torch.int32, device="cuda")
+        it = [0]
+
+        def call():
+            ctx.lmhead_argmax(heads[it[0] % 8], xmd, ld, am)
+            it[0] += 1
+        for _ in range(8):
+            call()
+        avg, med = time_launches(torch, call, 24)
+        b = n * k + n * 2 + m * k * 2 + m * n * 4
+        out[f"config5_lmhead_m{m}"] = {"bytes": b, "ms_per_call": avg,
+                                       "GBps": b / (avg * 1e-3) / 1e9,
+                                       "note": "matvec+argmax partials and the finalize launch"}
+    for h in heads:
+        h.release()
+    return out
+
+
+def cpu_baseline(seconds: float):
+    """RunGemmCpu (GS:13328-13381) restated in C, timed on this host: the seven
+    linears of one layer on dequantized fp32 weights (dequant untimed, as at
+    reference load time), float64 accumulation, single thread."""
+    import numpy as np
+
+    import oracle
+    from aiimage_amd import synth
+    lin = []
+    for i, (name, n, k) in enumerate(synth.LAYER_LINEARS):
+        words, scales, _ = synth.q4_weights(n, k, 1000 + i, group=32, code=synth.NIBBLE_OFFSET8)
+        wf = oracle.dequant_q4(words, scales, n, k, 32, oracle.NIBBLE_OFFSET8, oracle.SCALE_F16)
+        x = synth.activations(1, k, 2000 + i).astype(np.float32)
+        lin.append((x, wf, n))
+    layers = 0
+    t0 = time.perf_counter()
+    while True:
+        for x, wf, n in lin:
+            oracle.gemm_cpu(x, wf, n, True)
+        layers += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per_layer = el / layers
+    return {"value": LAYER_BYTES / per_layer / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{layers} passes of one layer's 7 Q4 linears (M=1) through the C restatement "
+                      f"of RunGemmCpu on dequantized fp32 weights, {el:.1f} s, "
+                      f"{per_layer * 1e3:.2f} ms per layer; rate in algorithmic quantized bytes"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the matvec would shard by output rows; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from aiimage_amd import aexq, synth
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    ctx = aexq.Context(0)
+    copies = args.copies or -(-GIB // LAYER_BYTES)
+    log(f"building {copies} cold copies of the layer ({copies * LAYER_WEIGHT_BYTES / 1e9:.2f} GB)")
+    layer = Layer(ctx, aexq, synth, torch, copies, synth.SEED_BASE + 2)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        layer.step()
+    torch.cuda.synchronize()
+    log(f"warmup done; timing {args.steps} steps")
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(args.steps):
+        layer.step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    value = copies * LAYER_BYTES / (ms_per_step * 1e-3) / 1e9
+    log(f"{ms_per_step:.4f} ms/step -> {value:.1f} GB/s")
+
+    # per-launch durations; the dominant launch carries the roofline
+    per = {}
+    for i, name in enumerate(("qkv_rms", "gate_up_swiglu_rms", "o_proj", "down_proj")):
+        avg, med = time_launches(torch, lambda i=i: layer.launch(i), max(10, args.steps))
+        b = copies * layer.launch_bytes(i)
+        per[name] = {"ms": avg, "ms_median": med, "bytes": b, "GBps": b / (avg * 1e-3) / 1e9}
+    dom = max(per, key=lambda k: per[k]["ms"])
+    ach = per[dom]["GBps"]
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None}
+    result = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "config2: one decoder layer's 7 Q4 linears, M=1, cold (sustained)",
+                   "copies_per_step": copies, "algorithmic_bytes_per_layer": LAYER_BYTES,
+                   "q4": "offset-8, fp16 scale per 32 K", "accumulate": "f32",
+                   "epilogues": "RMSNorm-in (q/k/v, gate/up), SwiGLU-out (gate/up)",
+                   "launches_per_step": 4,
+                   "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "launches": per,
+    }
+    if not args.no_extra:
+        del layer
+        torch.cuda.empty_cache()
+        log("extras: config 1 and config 5")
+        result["extra"] = extras(torch, aexq, synth, ctx)
+    if not args.no_cpu:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,210 @@
+/*
+ * aexq.h -- C ABI of the MI355X (gfx950) quantized decode-linear library.
+ *
+ * The drop-in boundary for Aexis's quantized Gemm path (newzjh/AIImage).  A C#
+ * host P/Invokes these entry points from an AexisBaseLayer subclass in place
+ * of AexisGemmLayer; the binding is shown in INTEGRATION.md.  Paths below are
+ * relative to the reference root; aliases:
+ *   GL  = Packages/com.aexis/Runtime/Execution/Layers/AexisGemmLayer.cs
+ *   GS  = Packages/com.aexis/Runtime/Execution/Graph/AexisGraphSession.cs
+ *   OPS = Packages/com.aexis/Runtime/Execution/Graph/AexisOps.cs
+ *   MM  = Packages/com.aexis/Runtime/Resources/Aexis/Includes/KernelGroups/AexisKernels.Pack4Matmul.hlsl
+ *   TEP = Packages/com.aexis/Runtime/Execution/Graph/AexisTextureExecutionPlanner.cs
+ *   WR  = Packages/com.aexis/Runtime/Execution/Graph/AexisWeightReader.cs
+ *   Q8A = Packages/com.aexis/Runtime/Ncnn/NcnnCompute/NcnnQ8Archive.cs
+ *   DEC = Packages/com.aexis/Samples/AIImageApplicationExample/Runtime/Scripts/Qwen35DecoderSession.cs
+ *
+ * Conventions (the reference's exceptions become status codes):
+ *   - every entry point returns aexq_status; 0 is success.  The message of the
+ *     last failure on the calling thread is aexq_last_error(), in the
+ *     reference's "| layer=... | reason=..." diagnostic style (GL:297-307).
+ *   - weights are library-owned device copies; activations and outputs are
+ *     caller-owned device pointers described by aexq_tensor.
+ *   - work is enqueued on the context's HIP stream and is asynchronous.
+ *   - nothing falls back: a shape, layout or dtype without a kernel returns
+ *     AEXQ_ERR_UNSUPPORTED, as the strict plan does (TEP:389-407).
+ *   - one context per host thread; a context is not thread-safe.
+ */
+#ifndef AEXQ_H
+#define AEXQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AEXQ_ABI_VERSION 1
+
+typedef int aexq_status;
+#define AEXQ_OK 0
+#define AEXQ_ERR_INVALID_ARGUMENT 1 /* ArgumentException (GS:12843-12847, 12893-12896) */
+#define AEXQ_ERR_UNSUPPORTED 2      /* NotSupportedException / strict-plan rejection (GL:297-307, TEP:389-407) */
+#define AEXQ_ERR_SHAPE 3            /* InvalidOperationException: shape/storage mismatch */
+#define AEXQ_ERR_DEVICE 4           /* HIP runtime failure */
+#define AEXQ_ERR_OUT_OF_MEMORY 5
+#define AEXQ_ERR_FORMAT 6           /* InvalidDataException: archive record (Q8A:282-290, 445-469) */
+
+/* element types of activations, outputs and scales */
+#define AEXQ_DTYPE_F16 1 /* ARGBHalf textures; the synthetic format's scales */
+#define AEXQ_DTYPE_F32 2 /* ARGBFloat textures; the reference's scales */
+
+/* Q4 nibble codes (see NcnnQ8Archive.WriteQ4, Q8A:132-135, and MM:715-716) */
+#define AEXQ_NIBBLE_TWOS 0    /* reference: stored q & 0xF, decoded raw >= 8 ? raw - 16 : raw */
+#define AEXQ_NIBBLE_OFFSET8 1 /* zero-point 8: stored q + 8, decoded raw - 8 */
+
+/* storage layouts of an activation or output tensor (GS:10818-10857) */
+#define AEXQ_LAYOUT_LINEAR 0       /* LinearMat: [h][w] row-major */
+#define AEXQ_LAYOUT_PACK4_LINEAR 1 /* Pack4 linear: storage {3, ceil(w/4), h, 1, 4} */
+#define AEXQ_LAYOUT_PACK4_TILED 2  /* Pack4 tiled: storage {3, tileWidth, h*tileRows, 1, 4} */
+#define AEXQ_LAYOUT_HEAD_PACKED 3  /* attention head-packed (MM:1192-1389): no kernel yet */
+
+/* epilogue flags of aexq_linear_args.flags */
+#define AEXQ_EPI_RMSNORM_IN 0x1u   /* x' = fp16(x * rsqrt(max(mean(x^2)+eps,1e-20)) * gamma) (CC:4531-4557) */
+#define AEXQ_EPI_SWIGLU_OUT 0x2u   /* y = swish(x'.Wgate) * (x'.Wup) (MM:106-116, SP:819-831) */
+#define AEXQ_EPI_RESIDUAL_ADD 0x4u /* y += residual (BinaryOp Add after o_proj/down) */
+
+typedef struct aexq_ctx aexq_ctx;
+typedef struct aexq_weight aexq_weight;
+
+/* Mirrors AexisGraphSession.BufferShape(dims, w, h, d, c) (GS:10818-10857). */
+typedef struct aexq_shape {
+  int dims, w, h, d, c;
+} aexq_shape;
+
+/* A device tensor standing in for a Pack4/LinearMat texture: the logical
+ * shape is [h = rows M][w = width], the storage shape follows the layout's
+ * BufferShape rule.  `batch`/`batch_stride` (elements) describe a stack of
+ * independent tensors used with a stacked weight (batch 1 = one tensor). */
+typedef struct aexq_tensor {
+  aexq_shape logical;
+  aexq_shape storage;
+  int layout;
+  int dtype;
+  void* data;
+  int batch;
+  int64_t batch_stride;
+} aexq_tensor;
+
+/* ncnn Gemm parameters and the fused epilogues (GL:23-34 param ids 0..10). */
+typedef struct aexq_linear_args {
+  float alpha;           /* param 0, default 1 */
+  float beta;            /* param 1, default 1 */
+  const float* c;        /* device C (bias), NULL when constantC is off */
+  int broadcast_c;       /* param 10: 0 scalar, 1 per row, 3 full [M][N], 4 per column; -1 none */
+  const float* rms_gamma;/* device fp32 RMSNorm weights (AEXQ_EPI_RMSNORM_IN); NULL = affine off */
+  int rms_gamma_size;
+  float rms_eps;         /* RMSNorm param 1 (reference default 0.001) */
+  const aexq_weight* up; /* SwiGLU partner weight (AEXQ_EPI_SWIGLU_OUT) */
+  const aexq_tensor* residual; /* AEXQ_EPI_RESIDUAL_ADD input, same shape/layout/dtype as y */
+  unsigned flags;
+} aexq_linear_args;
+
+/* Description of a weight (for hosts and tests). */
+typedef struct aexq_weight_info {
+  int bits;         /* 4 or 8 */
+  int n, k;         /* output rows N, reduction K: logical [N][K] (transB) */
+  int block;        /* scale block in elements of the flat [N][K] index (== K for per-row) */
+  int scale_dtype;  /* AEXQ_DTYPE_F16 / AEXQ_DTYPE_F32 */
+  int nibble_code;  /* Q4 only */
+  int batch;        /* stacked copies */
+  int64_t code_bytes;  /* device bytes of codes per copy */
+  int64_t scale_bytes; /* device bytes of scales per copy */
+} aexq_weight_info;
+
+/* ---- library / context ---------------------------------------------------- */
+
+int aexq_abi_version(void);
+/* Thread-local text of the last failure; never NULL. */
+const char* aexq_last_error(void);
+
+/* Creates a context on `device` enqueuing on `hip_stream` (NULL = the null
+ * stream).  Replaces the AexisOps instance that owns dispatch state
+ * (OPS:706-760). */
+aexq_status aexq_create(int device, void* hip_stream, aexq_ctx** out);
+void aexq_destroy(aexq_ctx* ctx);
+aexq_status aexq_set_stream(aexq_ctx* ctx, void* hip_stream);
+aexq_status aexq_synchronize(aexq_ctx* ctx);
+
+/* ---- weights (load time) ------------------------------------------------ */
+
+/* Direct Q8 upload of a packed record (AexisQuantizedTensor, WR:30-44) as
+ * NewInt8WeightOnlyUpload(AexisQuantizedTensor) does (GS:12887-12907):
+ * `packed` holds max(1, ceil(n*k/4)) uint32 words, byte (i & 3) of word i>>2
+ * for flat index i = row*k + col; `scales` holds one scale per output row
+ * (block must equal k, GL:65-67).  Host pointers; the library copies. */
+aexq_status aexq_weight_q8(aexq_ctx* ctx, const uint32_t* packed, const void* scales,
+                           int scale_dtype, int n, int k, int block, aexq_weight** out);
+
+/* Direct Q4 upload (GS:12966-12996): `packed` holds max(1, ceil(n*k/8)) words,
+ * nibble (i & 7) of word i>>3; `scales` holds n*k/block scales indexed by
+ * i / block; block must divide k. */
+aexq_status aexq_weight_q4(aexq_ctx* ctx, const uint32_t* packed, const void* scales,
+                           int scale_dtype, int n, int k, int block, int nibble_code,
+                           aexq_weight** out);
+
+/* Float uploads that quantize per output channel at load time, as the float
+ * overloads of NewInt8/Int4WeightOnlyUpload (GS:12838-12885, 12912-12964).
+ * `data` is [n][k] when trans_b (outputChannelsAreContiguous), else [k][n]. */
+aexq_status aexq_weight_q8_from_f32(aexq_ctx* ctx, const float* data, int n, int k,
+                                    int trans_b, aexq_weight** out);
+aexq_status aexq_weight_q4_from_f32(aexq_ctx* ctx, const float* data, int n, int k,
+                                    int trans_b, aexq_weight** out);
+
+/* A stack of `batch` copies of one packed weight, contiguous on the device.
+ * Used for a layer stack and for cold-HBM measurement; copy 0 holds `packed`,
+ * the others are device-side duplicates. */
+aexq_status aexq_weight_replicate(aexq_ctx* ctx, const aexq_weight* w, int batch,
+                                  aexq_weight** out);
+
+/* Shares the device buffers of `shared` (tied embedding / LM head, GL:91-111,
+ * owns=false).  The alias must be released before the owner. */
+aexq_status aexq_weight_alias(aexq_ctx* ctx, const aexq_weight* shared, aexq_weight** out);
+void aexq_weight_release(aexq_weight* w);
+aexq_status aexq_weight_get_info(const aexq_weight* w, aexq_weight_info* out);
+
+/* ---- execution ---------------------------------------------------------- */
+
+/* Strict preflight of aexq_linear (TEP:252-261, 389-407; GS:3585-3625):
+ * returns AEXQ_OK when a kernel exists for the combination, otherwise the
+ * status aexq_linear would return and a diagnostic in `diag`.  `diag` may be
+ * NULL.  Never touches the device. */
+aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
+                            const aexq_tensor* y, const aexq_linear_args* args, char* diag,
+                            size_t diag_len);
+
+/* y = Gemm(x, W) with constantB=1, transB=1 (GL:471-601 -> OPS:3649-3720 ->
+ * MM:1038-1190 / MM:2245-2302), plus the optional fused epilogues.
+ * Semantics per output layout: LINEAR and PACK4_LINEAR compute
+ * alpha * (beta*C + sum_k x*w) (MM:1054-1057, 1101); PACK4_TILED computes
+ * beta*C + alpha*sum (MM:2301).  x fp16, y fp16 or fp32, fp32 accumulation. */
+aexq_status aexq_linear(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
+                        const aexq_tensor* y, const aexq_linear_args* args);
+
+/* Several linears over one input in one launch (q/k/v share x; also the
+ * layer-stack form where every weight is stacked and x/y are batched).  All
+ * weights must have the same bits, k and batch. */
+aexq_status aexq_linear_group(aexq_ctx* ctx, int count, const aexq_weight* const* w,
+                              const aexq_tensor* x, const aexq_tensor* const* y,
+                              const aexq_linear_args* args);
+
+/* LM head with fused greedy argmax (DEC:734-809 -> tiled Gemm MM:2271-2302
+ * -> ArgMaxPack4LinearMat MM:645-686).  logits (nullable) are fp32 in the
+ * given layout; argmax is a device int32[M] using the first-maximum rule;
+ * top2_gap (nullable) is a device float[M] = best - second best logit. */
+aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
+                               const aexq_tensor* logits, int32_t* argmax, float* top2_gap);
+
+/* Row-wise argmax of an existing logits tensor (OPS:9982-10004, MM:645-686). */
+aexq_status aexq_argmax(aexq_ctx* ctx, const aexq_tensor* logits, int32_t* argmax,
+                        float* top2_gap);
+
+/* Dequantized weights [N][K] fp32 into device memory `out` (the bit-exact
+ * image of MM:707-734 AexisGemm2DReadB for every flat index). */
+aexq_status aexq_dequant(aexq_ctx* ctx, const aexq_weight* w, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
