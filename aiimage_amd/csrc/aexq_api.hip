@@ -479,8 +479,6 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       return fail(AEXQ_ERR_UNSUPPORTED, op, "group outputs differ in dtype");
     if (ys[i]->layout != ys[0]->layout)
       return fail(AEXQ_ERR_UNSUPPORTED, op, "group outputs differ in layout");
-    if (yv[i].rstride != yv[0].rstride)
-      return fail(AEXQ_ERR_UNSUPPORTED, op, "group outputs differ in row stride");
   }
   if (argmax && yv[0].dtype != AEXQ_DTYPE_F32)
     return fail(AEXQ_ERR_UNSUPPORTED, op, "LM-head logits must be fp32");
@@ -563,7 +561,6 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   p.chunks = chunks;
   p.xor_mask = (fmt == kQ4 && w0->nibble_code == AEXQ_NIBBLE_TWOS) ? 0x88888888u : 0u;
   p.x_rstride = xv.rstride;
-  p.y_rstride = yv[0].rstride;
   p.r_rstride = (a.flags & AEXQ_EPI_RESIDUAL_ADD) ? rv.rstride : 0;
   p.alpha = a.alpha;
   p.beta = a.beta;
@@ -600,6 +597,7 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     mt.x_bstride = xv.batch == 1 ? 0 : xv.bstride;
     mt.y_bstride = ys[i] ? yv[i].bstride : 0;
     mt.r_bstride = (a.flags & AEXQ_EPI_RESIDUAL_ADD) ? rv.bstride : 0;
+    mt.y_rstride = yv[i].rstride;
     mt.n = w->n;
     mt.n_store = ys[i] ? yv[i].padded : w->n;
     mt.tiles = (mt.n_store + plan->rwg - 1) / plan->rwg;
@@ -720,7 +718,7 @@ extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
   }
   // logits first (into the caller's tensor or a scratch buffer), then the argmax pass
   float* lg = nullptr;
-  long long rstride = plan.p.y_rstride;
+  long long rstride = plan.p.mat[0].y_rstride;
   if (logits) {
     lg = (float*)logits->data;
   } else {
@@ -734,7 +732,7 @@ extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
     }
     lg = ctx->logits_scratch;
     plan.p.mat[0].y = lg;
-    plan.p.y_rstride = w->n;
+    plan.p.mat[0].y_rstride = w->n;
     plan.p.flags |= kFlagYf32;
     rstride = w->n;
   }

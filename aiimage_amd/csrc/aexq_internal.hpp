@@ -33,6 +33,7 @@ struct QmvMat {
   void* y;             // outputs [m][y_rstride]
   const void* res;     // residual [m][r_rstride] (dtype of y) or null
   long long w_bstride, s_bstride, x_bstride, y_bstride, r_bstride;
+  long long y_rstride; // elements between output rows of this matrix
   int n;               // logical rows (output width N)
   int n_store;         // rows written: n plus zero-filled storage padding
   int tiles;           // row tiles per batch entry
@@ -49,7 +50,7 @@ struct QmvParams {
   int groups_per_row;  // k / group
   int chunks;          // 16-byte code chunks per row
   uint32_t xor_mask;   // 0x88888888 turns two's-complement nibbles into offset-8
-  long long x_rstride, y_rstride, r_rstride;  // elements between activation rows
+  long long x_rstride, r_rstride;  // elements between activation / residual rows
   float alpha, beta;
   const float* c;      // bias (C)
   int bcast;           // -1 none, 0 scalar, 1 per row m, 3 [m][n], 4 per column

@@ -311,7 +311,7 @@ __global__ __launch_bounds__(kThreads) void qmv_kernel(const QmvParams p) {
       outv[u][m] = v;
       // one lane per row stores; lanes of a slot hold identical values
       if (sub == ((u * MMAX + m) & (LPR - 1)) && r < mt.n_store && m < p.m && mt.y) {
-        const long long yi = (long long)m * p.y_rstride + r;
+        const long long yi = (long long)m * mt.y_rstride + r;
         if (yf32)
           ((float*)yb)[yi] = v;
         else
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void generic_kernel(const QmvParams p) {
       } else {
         v = 0.0f;
       }
-      const long long yi = (long long)m * p.y_rstride + r;
+      const long long yi = (long long)m * mt.y_rstride + r;
       if (yf32)
         ((float*)yb)[yi] = v;
       else
