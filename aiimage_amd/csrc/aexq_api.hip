@@ -5,6 +5,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -46,6 +47,7 @@ static aexq_status hip_fail(hipError_t e, const char* op, const char* what) {
 // ---------------------------------------------------------------------------
 struct aexq_ctx {
   int device = 0;
+  int cus = 256;  // compute units of the device
   hipStream_t stream = nullptr;
   // argmax partial buffers, grown on demand
   float* part_best = nullptr;
@@ -86,8 +88,11 @@ extern "C" aexq_status aexq_create(int device, void* hip_stream, aexq_ctx** out)
   if (device < 0 || device >= count)
     return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_create", "device=%d of %d", device, count);
   HIP_TRY("aexq_create", hipSetDevice(device));
+  int cus = 0;
+  HIP_TRY("aexq_create", hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
   aexq_ctx* c = new aexq_ctx();
   c->device = device;
+  c->cus = cus > 0 ? cus : 1;
   c->stream = (hipStream_t)hip_stream;
   *out = c;
   return AEXQ_OK;
@@ -136,11 +141,28 @@ static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const 
   w->scale_count = count / block;
   w->code_stride = round_up(w->code_bytes, 256);
   w->scale_stride = round_up(w->scale_count * scale_bytes(scale_dtype), 256);
+  // Device code layout: Q8 bytes biased by 128 (q + 128), Q4 nibbles offset-8
+  // (q + 8).  Both are one XOR of the reference's two's-complement words; the
+  // synthetic offset-8 Q4 words are already in device form.
+  uint32_t flip = 0u;
+  if (bits == 8) flip = 0x80808080u;
+  if (bits == 4 && nibble_code == AEXQ_NIBBLE_TWOS) flip = 0x88888888u;
+  std::vector<uint32_t> recoded;
+  const void* src = packed;
+  if (flip) {
+    const long long nw = w->code_bytes / 4;
+    recoded.resize((size_t)nw);
+    const uint32_t* in = (const uint32_t*)packed;
+    for (long long i = 0; i < nw; ++i) recoded[(size_t)i] = in[i] ^ flip;
+    src = recoded.data();
+  }
+  // padding decodes to code 0 in device form
+  const int pad_byte = bits == 8 ? 0x80 : 0x88;
   hipError_t e = hipSetDevice(ctx->device);
   if (e == hipSuccess) e = hipMalloc((void**)&w->codes, w->code_stride);
   if (e == hipSuccess) e = hipMalloc(&w->scales, w->scale_stride);
-  if (e == hipSuccess) e = hipMemset(w->codes, 0, w->code_stride);
-  if (e == hipSuccess) e = hipMemcpy(w->codes, packed, w->code_bytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemset(w->codes, pad_byte, w->code_stride);
+  if (e == hipSuccess) e = hipMemcpy(w->codes, src, w->code_bytes, hipMemcpyHostToDevice);
   if (e == hipSuccess)
     e = hipMemcpy(w->scales, scales, w->scale_count * scale_bytes(scale_dtype),
                   hipMemcpyHostToDevice);
@@ -397,11 +419,55 @@ static aexq_status view_tensor(const aexq_tensor* t, const char* op, const char*
 // ---------------------------------------------------------------------------
 struct Plan {
   bool fast = false;
-  QmvConfig cfg{};
-  int rwg = 0;
+  const QmvEntry* entry = nullptr;  // streaming kernel (fast path)
+  int fmt = kQ8;
+  int rows_per_tile = 0;
   QmvParams p{};
   int grid = 0;
 };
+
+// Shape of the streaming kernel for `chunks` 16-byte code chunks per row:
+// the smallest lanes-per-row x chunks-per-lane capacity that covers the row,
+// then the fewest lanes per row whose activation registers (chunks per lane x
+// 8 or 16 dwords per row of M) stay within 32 dwords per activation row.
+// AEXQ_QMV_SHAPE=lpr:cpl overrides the choice (tuning).
+static bool pick_shape(int fmt, int chunks, int mmax, int* lpr, int* cpl) {
+  const int xw = fmt == kQ8 ? 8 : 16;
+  const char* env = getenv("AEXQ_QMV_SHAPE");
+  if (env) {
+    int a = 0, b = 0;
+    if (sscanf(env, "%d:%d", &a, &b) == 2 && a * b >= chunks) {
+      *lpr = a;
+      *cpl = b;
+      return true;
+    }
+  }
+  const int lprs[3] = {16, 32, 64};
+  const int cpls[3] = {1, 2, 4};
+  int best_cap = 0, best_fit = 0, best_l = 0, best_c = 0;
+  for (int li = 0; li < 3; ++li)
+    for (int ci = 0; ci < 3; ++ci) {
+      const int l = lprs[li], c = cpls[ci];
+      // M > 1 shapes: one chunk per lane (Q8 also 64 x 2)
+      if (mmax > 1 && c > 1 && !(fmt == kQ8 && l == 64 && c == 2)) continue;
+      const int cap = l * c;
+      if (cap < chunks) continue;
+      const int fit = c * xw <= 32 ? 0 : 1;
+      // lexicographic: capacity, register fit, lanes per row
+      const bool better = !best_l || cap < best_cap || (cap == best_cap && fit < best_fit) ||
+                          (cap == best_cap && fit == best_fit && l < best_l);
+      if (better) {
+        best_cap = cap;
+        best_fit = fit;
+        best_l = l;
+        best_c = c;
+      }
+    }
+  if (!best_l) return false;
+  *lpr = best_l;
+  *cpl = best_c;
+  return true;
+}
 
 static const char* kLinearOp = "aexq_linear";
 
@@ -507,46 +573,42 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   const int fmt = w0->bits == 8 ? kQ8 : kQ4;
   const bool chunked = fmt == kQ8 ? (K % 16 == 0) : (K % 32 == 0);
   const int chunks = chunked ? (fmt == kQ8 ? K / 16 : K / 32) : 0;
-  const bool g16 = fmt == kQ4 && w0->block == 16;
-  const bool group_ok = fmt == kQ8 || g16 || (w0->block % 32 == 0);
+  const int gmode = fmt == kQ8 ? kGRow : (w0->block == 16 ? kG16 : kG32);
+  const bool group_ok = fmt == kQ8 || w0->block == 16 || (w0->block % 32 == 0);
   const bool x_ok = xv.dtype == AEXQ_DTYPE_F16 && xv.rstride % 8 == 0 &&
                     ((uintptr_t)xv.data % 16) == 0 && (xv.batch == 1 || xv.bstride % 8 == 0);
   const bool m_ok = M <= 8;
-  const bool fast = chunked && group_ok && x_ok && m_ok && chunks > 0 && chunks <= 256;
-  plan->fast = fast;
-  if (fast) {
-    int lpr, cpl;
-    if (chunks <= 16) {
-      lpr = 16;
-      cpl = 1;
-    } else if (chunks <= 32) {
-      lpr = 32;
-      cpl = 1;
-    } else {
-      lpr = 64;
-      cpl = (chunks + 63) / 64;
-      if (cpl == 3) cpl = 4;
-    }
-    plan->cfg = QmvConfig{fmt, lpr, cpl, M == 1 ? 1 : 8, swiglu, argmax, g16};
-    if (!qmv_has_config(plan->cfg)) {
-      if (argmax) {
-        plan->fast = false;  // logits by the matvec kernel, argmax as a second pass
-        plan->cfg.argmax = false;
+  // the streaming kernels read gamma[0..K) directly (no index clamp)
+  const bool rms_ok = !(a.flags & AEXQ_EPI_RMSNORM_IN) || !a.rms_gamma ||
+                      (a.rms_gamma_size >= K && ((uintptr_t)a.rms_gamma % 4) == 0);
+  // 32-bit buffer offsets inside one weight copy
+  const bool size_ok = (long long)w0->n * K * w0->bits / 8 < (1LL << 31);
+  plan->fmt = fmt;
+  plan->fast = false;
+  if (chunked && group_ok && x_ok && m_ok && rms_ok && size_ok && chunks > 0) {
+    const int mmax = M == 1 ? 1 : 8;
+    int lpr = 0, cpl = 0;
+    if (pick_shape(fmt, chunks, mmax, &lpr, &cpl)) {
+      int u = cpl >= 4 ? 1 : (cpl == 2 ? 2 : 4);
+      if (swiglu && u > 1) u /= 2;  // two weights stream per row
+      QmvConfig cfg{fmt, lpr, cpl, mmax == 1 ? u : 1, mmax, swiglu, argmax, gmode};
+      plan->entry = qmv_find(cfg);
+      if (!plan->entry && argmax) {
+        cfg.argmax = false;  // logits by the streaming kernel, argmax as a second pass
+        plan->entry = qmv_find(cfg);
       }
-      if (!qmv_has_config(plan->cfg))
-        return fail(AEXQ_ERR_UNSUPPORTED, op,
-                    "no kernel for bits=%d K=%d M=%d swiglu=%d | rejectedFallback=Gemm", w0->bits,
-                    K, M, (int)swiglu);
+      plan->fast = plan->entry != nullptr;
     }
-    plan->rwg = qmv_rows_per_wg(plan->cfg);
+  }
+  if (plan->fast) {
+    plan->rows_per_tile = plan->entry->rw;
   } else {
     if (swiglu)
       return fail(AEXQ_ERR_UNSUPPORTED, op,
                   "SwiGLU-out needs K aligned to 16-byte code chunks, fp16 x and M<=8 | K=%d M=%d "
                   "| rejectedFallback=SwiGLU",
                   K, M);
-    plan->cfg = QmvConfig{fmt, 0, 0, 0, false, false, g16};
-    plan->rwg = generic_rows_per_wg();
+    plan->rows_per_tile = generic_rows_per_wg();
   }
 
   // ---- parameters
@@ -559,7 +621,6 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   p.group = w0->block;
   p.groups_per_row = K / w0->block;
   p.chunks = chunks;
-  p.xor_mask = (fmt == kQ4 && w0->nibble_code == AEXQ_NIBBLE_TWOS) ? 0x88888888u : 0u;
   p.x_rstride = xv.rstride;
   p.r_rstride = (a.flags & AEXQ_EPI_RESIDUAL_ADD) ? rv.rstride : 0;
   p.alpha = a.alpha;
@@ -600,20 +661,32 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     mt.y_rstride = yv[i].rstride;
     mt.n = w->n;
     mt.n_store = ys[i] ? yv[i].padded : w->n;
-    mt.tiles = (mt.n_store + plan->rwg - 1) / plan->rwg;
+    mt.tiles = (mt.n_store + plan->rows_per_tile - 1) / plan->rows_per_tile;
     mt.tile_base = tiles_total;
     const long long add = (long long)mt.tiles * w->batch;
     if (tiles_total + add > 0x7fffffffLL) return fail(AEXQ_ERR_UNSUPPORTED, op, "grid too large");
     tiles_total += (int)add;
   }
-  plan->grid = tiles_total;
+  p.total_tiles = tiles_total;
+  if (plan->fast) {
+    // persistent grid: every wave resident, each owning a contiguous tile range
+    int per_cu = qmv_blocks_per_cu(plan->entry);
+    const char* env = getenv("AEXQ_QMV_BLOCKS_PER_CU");
+    if (env && atoi(env) > 0) per_cu = atoi(env);
+    const long long need = ((long long)tiles_total + kWaves - 1) / kWaves;
+    const long long cap = (long long)per_cu * ctx->cus;
+    plan->grid = (int)(need < cap ? need : cap);
+    if (plan->grid < 1) plan->grid = 1;
+  } else {
+    plan->grid = tiles_total;
+  }
   return AEXQ_OK;
 }
 
 static aexq_status launch_plan(aexq_ctx* ctx, Plan& plan, const char* op) {
   HIP_TRY(op, hipSetDevice(ctx->device));
-  hipError_t e = plan.fast ? qmv_launch(plan.cfg, plan.p, plan.grid, ctx->stream)
-                           : generic_launch(plan.cfg.fmt, plan.p, plan.grid, ctx->stream);
+  hipError_t e = plan.fast ? qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream)
+                           : generic_launch(plan.fmt, plan.p, plan.grid, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, op, "kernel launch");
   return AEXQ_OK;
 }
@@ -629,9 +702,12 @@ extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, cons
     if (st)
       snprintf(diag, diag_len, "%s", g_last_error.c_str());
     else
-      snprintf(diag, diag_len, "kernel=%s bits=%d lpr=%d cpl=%d mmax=%d swiglu=%d grid=%d",
-               plan.fast ? "qmv" : "generic", w->bits, plan.cfg.lpr, plan.cfg.cpl,
-               plan.cfg.mmax, (int)plan.cfg.pair, plan.grid);
+      snprintf(diag, diag_len,
+               "kernel=%s bits=%d lpr=%d cpl=%d u=%d mmax=%d swiglu=%d tiles=%d grid=%d",
+               plan.fast ? "qmv" : "generic", w->bits, plan.fast ? plan.entry->cfg.lpr : 0,
+               plan.fast ? plan.entry->cfg.cpl : 0, plan.fast ? plan.entry->cfg.u : 0,
+               plan.fast ? plan.entry->cfg.mmax : 0, plan.fast ? (int)plan.entry->cfg.pair : 0,
+               plan.p.total_tiles, plan.grid);
   }
   return st;
 }
@@ -700,15 +776,15 @@ extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
   if (st) return st;
   HIP_TRY(op, hipSetDevice(ctx->device));
   const int M = plan.p.m;
-  if (plan.fast && plan.cfg.argmax) {
-    const int parts = plan.p.mat[0].tiles;
+  if (plan.fast && plan.entry->cfg.argmax) {
+    const int parts = plan.grid * kWaves;  // one partial per wave
     st = ensure_parts(ctx, (long long)parts * M, op);
     if (st) return st;
     plan.p.part_best = ctx->part_best;
     plan.p.part_index = ctx->part_index;
     plan.p.part_second = ctx->part_second;
     plan.p.parts = parts;
-    hipError_t e = qmv_launch(plan.cfg, plan.p, plan.grid, ctx->stream);
+    hipError_t e = qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, op, "lm head launch");
     ArgmaxParams ap{ctx->part_best, ctx->part_index, ctx->part_second, parts, M, argmax,
                     top2_gap};
@@ -760,9 +836,8 @@ extern "C" aexq_status aexq_dequant(aexq_ctx* ctx, const aexq_weight* w, float* 
   if (!ctx || !w || !out) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
   HIP_TRY(op, hipSetDevice(ctx->device));
   const int fmt = w->bits == 8 ? kQ8 : kQ4;
-  const uint32_t xm = (fmt == kQ4 && w->nibble_code == AEXQ_NIBBLE_TWOS) ? 0x88888888u : 0u;
   hipError_t e = dequant_launch(fmt, w->codes, w->scales, w->scale_dtype == AEXQ_DTYPE_F16, w->n,
-                                w->k, w->block, xm, out, ctx->stream);
+                                w->k, w->block, out, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, op, "dequant launch");
   return AEXQ_OK;
 }

@@ -22,27 +22,37 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
 
-// Four int8 codes of one word -> two fp16 pairs holding the exact integers.
-// Biasing by 0x80 gives u = q + 128 in [0, 255]; the fp16 with bits 0x6400|u is
-// 1024 + u exactly, so subtracting 1152 yields q with no rounding.
+// Four Q8 codes of one device word -> two fp16 pairs holding the exact integers.
+// The device copy stores every int8 code biased by 128 (u = q + 128 in [1, 255],
+// applied once at upload), so the fp16 with bits 0x6400|u is 1024 + u exactly
+// and subtracting 1152 yields q with no rounding.
 // lo = (q0, q1), hi = (q2, q3) in element order.
-__device__ __forceinline__ void q8_pairs(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  const uint32_t u = w ^ 0x80808080u;
+__device__ __forceinline__ void q8_pairs(uint32_t u, uint32_t& lo, uint32_t& hi) {
   const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
   lo = as_u(as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
   hi = as_u(as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
 }
 
-// Eight offset-8 nibbles of one word (n0 in bits 0-3) -> four fp16 pairs of the
-// exact codes q = n - 8.  Pair p holds elements (p, p + 4): bits 0x6400|n give
-// 1024 + n, and subtracting 1032 is exact.
+// Eight offset-8 nibbles of one device word (n0 in bits 0-3; the device copy
+// always holds offset-8 codes n = q + 8) -> four fp16 pairs of the exact codes,
+// pair p holding elements (p, p + 4).  Five bit operations and four packed
+// fp16 operations, all exact:
+//   even nibbles: bits 0x6400|n       = 1024 + n    ; + (-1032)         -> n - 8
+//   odd nibbles:  bits 0x6400|(n<<4)  = 1024 + 16n  ; * 1/16 + (-72)    -> n - 8
 __device__ __forceinline__ void q4_pairs(uint32_t w, uint32_t q[4]) {
-  const uint32_t M = 0x000F000Fu, E = 0x64006400u;
-  const f16x2 bias = {(f16)1032.0f, (f16)1032.0f};
-  q[0] = as_u(as_h2((w & M) | E) - bias);
-  q[1] = as_u(as_h2(((w >> 4) & M) | E) - bias);
-  q[2] = as_u(as_h2(((w >> 8) & M) | E) - bias);
-  q[3] = as_u(as_h2(((w >> 12) & M) | E) - bias);
+  const uint32_t E = 0x64006400u;
+  const f16x2 b_even = {(f16)-1032.0f, (f16)-1032.0f};
+  const f16x2 s_odd = {(f16)0.0625f, (f16)0.0625f};
+  const f16x2 b_odd = {(f16)-72.0f, (f16)-72.0f};
+  const uint32_t w8 = w >> 8;
+  const f16x2 a = as_h2((w & 0x000F000Fu) | E);   // (n0, n4)
+  const f16x2 b = as_h2((w & 0x00F000F0u) | E);   // (n1, n5) * 16
+  const f16x2 c = as_h2((w8 & 0x000F000Fu) | E);  // (n2, n6)
+  const f16x2 d = as_h2((w8 & 0x00F000F0u) | E);  // (n3, n7) * 16
+  q[0] = as_u(a + b_even);
+  q[1] = as_u(__builtin_elementwise_fma(b, s_odd, b_odd));
+  q[2] = as_u(c + b_even);
+  q[3] = as_u(__builtin_elementwise_fma(d, s_odd, b_odd));
 }
 
 // Reorders 8 consecutive fp16 activations (a=(x0,x1) b=(x2,x3) c=(x4,x5)
@@ -117,6 +127,48 @@ __device__ __forceinline__ float load_scale(const void* s, long long i, bool f16
   return f16_scale ? (float)((const f16*)s)[i] : ((const float*)s)[i];
 }
 
+// Fourth dword of a raw buffer resource on gfx9-family parts (32-bit data
+// format, no swizzle); loads past num_records return zero.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+// Cache policy of the streamed weight loads: non-temporal.
+constexpr int kStreamAux = 2;
+
+// fp16 or fp32 scale from the aligned dword `dw` loaded at byte offset
+// (off & ~3): an fp16 scale is the half selected by bit 1 of the offset.
+__device__ __forceinline__ float scale_at(uint32_t dw, int off, bool f16_scale) {
+  if (f16_scale) {
+    const uint16_t h = (uint16_t)(dw >> ((off & 2) * 8));
+    return (float)__builtin_bit_cast(f16, h);
+  }
+  return __builtin_bit_cast(float, dw);
+}
+
+// Raw bits of scale i (fp16 in the low half, or fp32); scale_of() widens them
+// exactly (fp16 subnormals included) once the load has landed.
+__device__ __forceinline__ uint32_t load_scale_bits(const void* s, long long i, bool f16_scale) {
+  return f16_scale ? (uint32_t)((const uint16_t*)s)[i] : ((const uint32_t*)s)[i];
+}
+__device__ __forceinline__ float scale_of(uint32_t bits, bool f16_scale) {
+  return f16_scale ? (float)__builtin_bit_cast(f16, (uint16_t)bits) : __builtin_bit_cast(float, bits);
+}
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// Bias, alpha and beta as the reference Gemm resolves them (MM:688-705, 812-820):
+// Pack4-linear output is alpha*(beta*C + sum), tiled output beta*C + alpha*sum.
+__device__ __forceinline__ float gemm_epilogue(const QmvParams& p, int m, int r, float v) {
+  float bias = 0.0f;
+  if (p.c) {
+    switch (p.bcast) {
+      case 0: bias = p.c[0]; break;
+      case 1: bias = p.c[m]; break;
+      case 3: bias = p.c[(long long)m * p.c_rstride + r]; break;
+      case 4: bias = p.c[r]; break;
+      default: bias = 0.0f; break;
+    }
+    bias *= p.beta;
+  }
+  return (p.flags & kFlagAlphaIn) ? p.alpha * (bias + v) : bias + p.alpha * v;
+}
 
 }  // namespace aexq

@@ -22,6 +22,10 @@ enum : int {
   kFlagXf32 = 32,      // activations fp32 (generic kernel only)
 };
 
+// Scale granularity of a streaming kernel: one per row (Q8), per 16 codes
+// (the reference's shipping Q4), or per multiple of 32 codes (incl. per row).
+enum GMode : int { kGRow = 0, kG16 = 1, kG32 = 2 };
+
 // One matrix of a grouped launch; pointers are for batch entry 0 and advance
 // by the *_bstride members (in words / scale elements / tensor elements).
 struct QmvMat {
@@ -49,7 +53,7 @@ struct QmvParams {
   int group;           // scale block (elements); == k for per-row
   int groups_per_row;  // k / group
   int chunks;          // 16-byte code chunks per row
-  uint32_t xor_mask;   // 0x88888888 turns two's-complement nibbles into offset-8
+  int total_tiles;     // wave tiles over all matrices and batch entries
   long long x_rstride, r_rstride;  // elements between activation / residual rows
   float alpha, beta;
   const float* c;      // bias (C)
@@ -76,14 +80,24 @@ struct ArgmaxParams {
   float* out_gap;
 };
 
-// host-side launchers (defined in aexq_qmv.hip)
+// Streaming kernel registry (instantiated in aexq_qmv_q8.hip / aexq_qmv_q4.hip).
 struct QmvConfig {
-  int fmt, lpr, cpl, mmax;
-  bool pair, argmax, g16;
+  int fmt, lpr, cpl, u, mmax;
+  bool pair, argmax;
+  int gmode;
 };
-int qmv_rows_per_wg(const QmvConfig& cfg);
-hipError_t qmv_launch(const QmvConfig& cfg, const QmvParams& p, int grid, hipStream_t stream);
-bool qmv_has_config(const QmvConfig& cfg);
+typedef void (*QmvFn)(const QmvParams);
+struct QmvEntry {
+  QmvConfig cfg;
+  QmvFn fn;
+  int rw;  // rows per wave tile
+};
+const QmvEntry* qmv_table_q8(int* count);
+const QmvEntry* qmv_table_q4(int* count);
+const QmvEntry* qmv_find(const QmvConfig& cfg);
+// resident workgroups of an entry per CU (occupancy query, cached)
+int qmv_blocks_per_cu(const QmvEntry* e);
+hipError_t qmv_launch(const QmvEntry* e, const QmvParams& p, int grid, hipStream_t stream);
 hipError_t generic_launch(int fmt, const QmvParams& p, int grid, hipStream_t stream);
 int generic_rows_per_wg();
 hipError_t argmax_finalize_launch(const ArgmaxParams& a, hipStream_t stream);
@@ -91,7 +105,7 @@ hipError_t logits_argmax_launch(const float* logits, int m, int n, long long rst
                                 int* pi, float* ps, int parts, hipStream_t stream);
 int logits_argmax_cols_per_wg();
 hipError_t dequant_launch(int fmt, const uint32_t* w, const void* s, int scale_f16, int n, int k,
-                          int group, uint32_t xor_mask, float* out, hipStream_t stream);
+                          int group, float* out, hipStream_t stream);
 hipError_t replicate_launch(const void* src, void* dst, long long bytes, int copies,
                             hipStream_t stream);
 

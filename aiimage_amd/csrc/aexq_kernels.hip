@@ -1,0 +1,326 @@
+// Support kernels of the aexq library for gfx950: the element-wise generic
+// Gemm (any K, any scale block, fp32 activations, M > 8), argmax over logits
+// and its partial merge, dequantization, and the streaming-kernel registry.
+//
+// Device code layouts (recoded once at upload from the reference's packed
+// words, MM:707-734): Q8 bytes hold q + 128, Q4 nibbles hold q + 8.
+#include <math.h>
+
+#include "aexq_device.hpp"
+
+namespace aexq {
+
+// ---------------------------------------------------------------------------
+// Generic kernel: any K, any scale block, fp16 or fp32 activations; decodes
+// element by element with the reference formula (MM:707-727).  One wave per
+// output row, lanes stride over K, up to 16 activation rows per launch row.
+// ---------------------------------------------------------------------------
+constexpr int kGenericM = 16;
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void generic_kernel(const QmvParams p) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x;
+  int j = 0;
+  for (int t = 1; t < p.nmat; ++t)
+    if (b >= p.mat[t].tile_base) j = t;
+  const QmvMat& mt = p.mat[j];
+  const int local = b - mt.tile_base;
+  const int bi = local / mt.tiles;
+  const int tile = local - bi * mt.tiles;
+  const int r = tile * kWaves + wave;
+  const int m0 = blockIdx.y * kGenericM;
+  const int mcount = min(kGenericM, p.m - m0);
+
+  const bool scl16 = (p.flags & kFlagScaleF16) != 0;
+  const bool xf32 = (p.flags & kFlagXf32) != 0;
+  const bool yf32 = (p.flags & kFlagYf32) != 0;
+  const uint32_t* w = mt.w + bi * mt.w_bstride;
+  const char* s = (const char*)mt.s + bi * mt.s_bstride * (scl16 ? 2 : 4);
+  const char* xb = (const char*)mt.x + bi * mt.x_bstride * (xf32 ? 4 : 2);
+  const bool rms = (p.flags & kFlagRms) != 0;
+
+  float inv[kGenericM];
+  for (int i = 0; i < kGenericM; ++i) inv[i] = 1.0f;
+  if (rms) {
+    for (int i = 0; i < mcount; ++i) {
+      float ss = 0.0f;
+      for (int kk = lane; kk < p.k; kk += 64) {
+        const long long xi = (long long)(m0 + i) * p.x_rstride + kk;
+        const float a = xf32 ? ((const float*)xb)[xi] : (float)((const f16*)xb)[xi];
+        ss = fmaf(a, a, ss);
+      }
+      ss = wave_sum(ss);
+      inv[i] = rsqrtf(fmaxf(ss / (float)p.k + p.eps, 1e-20f));
+    }
+  }
+
+  float acc[kGenericM];
+  for (int i = 0; i < kGenericM; ++i) acc[i] = 0.0f;
+  if (r < mt.n) {
+    for (int kk = lane; kk < p.k; kk += 64) {
+      const long long idx = (long long)r * p.k + kk;
+      int sv;
+      if constexpr (FMT == kQ8) {
+        sv = (int)((w[idx >> 2] >> ((idx & 3) * 8)) & 0xffu) - 128;
+      } else {
+        sv = (int)((w[idx >> 3] >> ((idx & 7) * 4)) & 0xfu) - 8;
+      }
+      const long long si = FMT == kQ8 ? (long long)r : idx / p.group;
+      const float wval = (float)sv * load_scale(s, si, scl16);
+      for (int i = 0; i < mcount; ++i) {
+        const long long xi = (long long)(m0 + i) * p.x_rstride + kk;
+        float a = xf32 ? ((const float*)xb)[xi] : (float)((const f16*)xb)[xi];
+        if (rms) {
+          a *= inv[i];
+          if (p.gamma) a *= p.gamma[min(kk, p.gamma_size - 1)];
+          if (!xf32) a = (float)(f16)a;
+        }
+        acc[i] = fmaf(a, wval, acc[i]);
+      }
+    }
+  }
+  char* yb = (char*)mt.y + bi * mt.y_bstride * (yf32 ? 4 : 2);
+  const char* rb = mt.res ? (const char*)mt.res + bi * mt.r_bstride * (yf32 ? 4 : 2) : nullptr;
+  for (int i = 0; i < mcount; ++i) {
+    float v = wave_sum(acc[i]);
+    const int m = m0 + i;
+    if (lane == (i & 63) && r < mt.n_store) {
+      if (r < mt.n) {
+        v = gemm_epilogue(p, m, r, v);
+        if (rb && (p.flags & kFlagResidual)) {
+          const long long ri = (long long)m * p.r_rstride + r;
+          v += yf32 ? ((const float*)rb)[ri] : (float)((const f16*)rb)[ri];
+        }
+      } else {
+        v = 0.0f;
+      }
+      const long long yi = (long long)m * mt.y_rstride + r;
+      if (yf32)
+        ((float*)yb)[yi] = v;
+      else
+        ((f16*)yb)[yi] = (f16)v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Argmax over existing fp32 logits rows, and the final merge of partials.
+// ---------------------------------------------------------------------------
+constexpr int kArgmaxCols = 4096;
+
+__global__ __launch_bounds__(kThreads) void logits_argmax_kernel(const float* logits, int n,
+                                                                 long long rstride, float* pv,
+                                                                 int* pi, float* ps, int parts) {
+  const int m = blockIdx.y, part = blockIdx.x;
+  const int c0 = part * kArgmaxCols;
+  const int c1 = min(n, c0 + kArgmaxCols);
+  float bv = __builtin_nanf("");
+  int bix = 0x7fffffff;
+  float bs = -INFINITY;
+  for (int c = c0 + (int)threadIdx.x; c < c1; c += kThreads) {
+    argmax_merge(bv, bix, bs, logits[(long long)m * rstride + c], c, -INFINITY);
+  }
+  argmax_wave_reduce(bv, bix, bs);
+  __shared__ float sv[kWaves], ss[kWaves];
+  __shared__ int si[kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bix;
+    ss[wave] = bs;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWaves; ++w) argmax_merge(bv, bix, bs, sv[w], si[w], ss[w]);
+    const long long o = (long long)m * parts + part;
+    pv[o] = bv;
+    pi[o] = bix;
+    ps[o] = bs;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_finalize_kernel(const ArgmaxParams a) {
+  const int m = blockIdx.x;
+  float bv = __builtin_nanf("");
+  int bix = 0x7fffffff;
+  float bs = -INFINITY;
+  for (int i = threadIdx.x; i < a.parts; i += kThreads) {
+    const long long o = (long long)m * a.parts + i;
+    argmax_merge(bv, bix, bs, a.pv[o], a.pi[o], a.ps[o]);
+  }
+  argmax_wave_reduce(bv, bix, bs);
+  __shared__ float sv[kWaves], ss[kWaves];
+  __shared__ int si[kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bix;
+    ss[wave] = bs;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWaves; ++w) argmax_merge(bv, bix, bs, sv[w], si[w], ss[w]);
+    a.out_index[m] = bix == 0x7fffffff ? 0 : bix;
+    if (a.out_gap) a.out_gap[m] = bs == -INFINITY ? INFINITY : bv - bs;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dequantization to fp32 [N][K].  Chunk-aligned rows use the same code
+// expansion as the matvec kernels; other shapes decode element by element.
+// ---------------------------------------------------------------------------
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void dequant_chunk_kernel(const uint32_t* w, const void* s,
+                                                                 int scl16, int n, int k, int group,
+                                                                 float* out) {
+  const int chunks = FMT == kQ8 ? k / 16 : k / 32;
+  const long long total = (long long)n * chunks;
+  for (long long t = blockIdx.x * (long long)kThreads + threadIdx.x; t < total;
+       t += (long long)gridDim.x * kThreads) {
+    const int r = (int)(t / chunks);
+    const int ci = (int)(t - (long long)r * chunks);
+    const u32x4 v = *(const u32x4*)(w + t * 4);
+    if constexpr (FMT == kQ8) {
+      const float sc = load_scale(s, r, scl16);
+      float* o = out + (long long)r * k + ci * 16;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        uint32_t lo, hi;
+        q8_pairs(v[d], lo, hi);
+        const f16x2 a = as_h2(lo), b = as_h2(hi);
+        o[4 * d + 0] = (float)a[0] * sc;
+        o[4 * d + 1] = (float)a[1] * sc;
+        o[4 * d + 2] = (float)b[0] * sc;
+        o[4 * d + 3] = (float)b[1] * sc;
+      }
+    } else {
+      float* o = out + (long long)r * k + ci * 32;
+      const long long flat0 = (long long)r * k + ci * 32;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        uint32_t q[4];
+        q4_pairs(v[d], q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f16x2 h = as_h2(q[e]);
+          const long long i0 = flat0 + 8 * d + e, i1 = i0 + 4;
+          o[8 * d + e] = (float)h[0] * load_scale(s, i0 / group, scl16);
+          o[8 * d + e + 4] = (float)h[1] * load_scale(s, i1 / group, scl16);
+        }
+      }
+    }
+  }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void dequant_elem_kernel(const uint32_t* w, const void* s,
+                                                                int scl16, int n, int k, int group,
+                                                                float* out) {
+  const long long total = (long long)n * k;
+  for (long long idx = blockIdx.x * (long long)kThreads + threadIdx.x; idx < total;
+       idx += (long long)gridDim.x * kThreads) {
+    int sv;
+    long long si;
+    if constexpr (FMT == kQ8) {
+      sv = (int)((w[idx >> 2] >> ((idx & 3) * 8)) & 0xffu) - 128;
+      si = idx / k;
+    } else {
+      sv = (int)((w[idx >> 3] >> ((idx & 7) * 4)) & 0xfu) - 8;
+      si = idx / group;
+    }
+    out[idx] = (float)sv * load_scale(s, si, scl16);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+const QmvEntry* qmv_find(const QmvConfig& c) {
+  int n = 0;
+  const QmvEntry* t = c.fmt == kQ8 ? qmv_table_q8(&n) : qmv_table_q4(&n);
+  for (int i = 0; i < n; ++i) {
+    const QmvConfig& q = t[i].cfg;
+    if (q.lpr == c.lpr && q.cpl == c.cpl && q.u == c.u && q.mmax == c.mmax && q.pair == c.pair &&
+        q.argmax == c.argmax && q.gmode == c.gmode)
+      return &t[i];
+  }
+  return nullptr;
+}
+
+// Occupancy of each entry, queried once per entry (the device is the same for
+// every context of a process that uses one GPU model).
+int qmv_blocks_per_cu(const QmvEntry* e) {
+  static int cache_q8[512], cache_q4[512];
+  int n8 = 0, n4 = 0;
+  const QmvEntry* t8 = qmv_table_q8(&n8);
+  const QmvEntry* t4 = qmv_table_q4(&n4);
+  int* slot = nullptr;
+  if (e >= t8 && e < t8 + n8 && e - t8 < 512) slot = &cache_q8[e - t8];
+  if (e >= t4 && e < t4 + n4 && e - t4 < 512) slot = &cache_q4[e - t4];
+  if (slot && *slot > 0) return *slot;
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, e->fn, kThreads, 0) != hipSuccess ||
+      blocks <= 0)
+    blocks = 1;
+  if (slot) *slot = blocks;
+  return blocks;
+}
+
+hipError_t qmv_launch(const QmvEntry* e, const QmvParams& p, int grid, hipStream_t stream) {
+  if (!e) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(e->fn, dim3(grid), dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+int generic_rows_per_wg() { return kWaves; }
+
+hipError_t generic_launch(int fmt, const QmvParams& p, int grid, hipStream_t stream) {
+  const dim3 g(grid, (p.m + kGenericM - 1) / kGenericM);
+  if (fmt == kQ8)
+    hipLaunchKernelGGL(generic_kernel<kQ8>, g, dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL(generic_kernel<kQ4>, g, dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+int logits_argmax_cols_per_wg() { return kArgmaxCols; }
+
+hipError_t logits_argmax_launch(const float* logits, int m, int n, long long rstride, float* pv,
+                                int* pi, float* ps, int parts, hipStream_t stream) {
+  hipLaunchKernelGGL(logits_argmax_kernel, dim3(parts, m), dim3(kThreads), 0, stream, logits, n,
+                     rstride, pv, pi, ps, parts);
+  return hipGetLastError();
+}
+
+hipError_t argmax_finalize_launch(const ArgmaxParams& a, hipStream_t stream) {
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(a.m), dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t dequant_launch(int fmt, const uint32_t* w, const void* s, int scale_f16, int n, int k,
+                          int group, float* out, hipStream_t stream) {
+  const bool chunked = fmt == kQ8 ? (k % 16 == 0) : (k % 32 == 0);
+  const long long work = chunked ? (long long)n * (fmt == kQ8 ? k / 16 : k / 32) : (long long)n * k;
+  long long blocks = (work + kThreads - 1) / kThreads;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  if (chunked) {
+    if (fmt == kQ8)
+      hipLaunchKernelGGL(dequant_chunk_kernel<kQ8>, dim3(blocks), dim3(kThreads), 0, stream, w, s,
+                         scale_f16, n, k, group, out);
+    else
+      hipLaunchKernelGGL(dequant_chunk_kernel<kQ4>, dim3(blocks), dim3(kThreads), 0, stream, w, s,
+                         scale_f16, n, k, group, out);
+  } else {
+    if (fmt == kQ8)
+      hipLaunchKernelGGL(dequant_elem_kernel<kQ8>, dim3(blocks), dim3(kThreads), 0, stream, w, s,
+                         scale_f16, n, k, group, out);
+    else
+      hipLaunchKernelGGL(dequant_elem_kernel<kQ4>, dim3(blocks), dim3(kThreads), 0, stream, w, s,
+                         scale_f16, n, k, group, out);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace aexq

@@ -1,0 +1,437 @@
+// Persistent streaming matvec / small-M matmul kernel for gfx950 (M <= 8).
+//
+// The weight is a row-major [N][K] stream of device codes (Q8: int8 biased by
+// 128; Q4: offset-8 nibbles, low nibble first) -- the reference's packed words
+// (MM:707-734) recoded once at upload.  A wave owns a contiguous range of
+// "wave tiles" of RW rows over every (matrix, batch entry, row tile) of the
+// launch and walks it with its next tile's loads in flight (two register
+// buffers), so each wave keeps 2 x U x CPL 16-byte loads outstanding and no
+// barrier ever stops the stream.  Inside a tile, LPR lanes share a row; lane
+// `sub` owns 16-byte code chunks sub, sub+LPR, ... of it.  Codes become exact
+// fp16 integers in registers (q8_pairs / q4_pairs) and meet the fp16
+// activations, which stay in registers while the activation row is unchanged,
+// in v_dot2_f32_f16 with fp32 accumulation.  Scales are applied in fp32: once
+// per row for Q8, once per 16- or 32-code group for Q4.  Rows are reduced
+// across their LPR lanes with DPP.  Epilogues (alpha/beta/C, RMSNorm-in,
+// SwiGLU-out, residual, argmax partials) run before the single store.
+#pragma once
+
+#include <math.h>
+
+#include "aexq_device.hpp"
+
+namespace aexq {
+
+template <int FMT, int LPR, int CPL, int U, int MMAX, bool PAIR, bool ARGMAX, int GM>
+struct Qmv {
+  static constexpr int SLOTS = 64 / LPR;                 // rows sharing one wave at once
+  static constexpr int RW = SLOTS * U;                   // rows per wave tile
+  static constexpr int XW = FMT == kQ8 ? 8 : 16;         // activation dwords per code chunk
+  static constexpr int NW = PAIR ? 2 : 1;                // gate (+ up) weights
+  static constexpr int NS = FMT == kQ8 ? 1 : (GM == kG16 ? 2 * CPL : CPL);  // scales per row
+
+  struct Cursor {
+    int j, b, rt;  // matrix, batch entry, row tile (wave-uniform)
+  };
+
+  struct Buf {
+    u32x4 w[NW][U][CPL];
+    uint32_t s[NW][U][NS];  // raw scale bits, widened when consumed (keeps loads in flight)
+  };
+
+  typedef uint32_t XRegs[MMAX][CPL][XW];
+
+  static __device__ __forceinline__ Cursor locate(const QmvParams& p, int t) {
+    int j = 0;
+    for (int i = 1; i < p.nmat; ++i)
+      if (t >= p.mat[i].tile_base) j = i;
+    const int local = t - p.mat[j].tile_base;
+    Cursor c;
+    c.j = j;
+    c.b = local / p.mat[j].tiles;
+    c.rt = local - c.b * p.mat[j].tiles;
+    return c;
+  }
+
+  static __device__ __forceinline__ Cursor advance(const QmvParams& p, Cursor c) {
+    if (++c.rt == p.mat[c.j].tiles) {
+      c.rt = 0;
+      if (++c.b == p.batch) {
+        c.b = 0;
+        ++c.j;
+      }
+    }
+    return c;
+  }
+
+  // Lane-constant byte offsets of a tile's code chunks and scales, relative to
+  // the tile's first row.
+  struct Offsets {
+    int w[U][CPL];
+    int s[U][NS];
+  };
+
+  static __device__ __forceinline__ Offsets offsets(const QmvParams& p, int sub, int slot) {
+    Offsets o;
+    const int row_bytes = p.chunks * 16;
+    const int sb = (p.flags & kFlagScaleF16) ? 2 : 4;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int rr = u * SLOTS + slot;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) o.w[u][c] = rr * row_bytes + (sub + c * LPR) * 16;
+      if constexpr (FMT == kQ8) {
+        o.s[u][0] = rr * sb;
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          const int ci = sub + c * LPR;
+          const int g0 = rr * p.groups_per_row;
+          if constexpr (GM == kG16) {
+            o.s[u][2 * c] = (g0 + 2 * ci) * sb;
+            o.s[u][2 * c + 1] = (g0 + 2 * ci + 1) * sb;
+          } else {
+            o.s[u][c] = (g0 + (ci * 32) / p.group) * sb;
+          }
+        }
+      }
+    }
+    return o;
+  }
+
+  // Byte offset of a tile's first scale inside its weight copy's scale array.
+  static __device__ __forceinline__ int scale_tile_offset(const QmvParams& p, const Cursor& cu) {
+    const int sb = (p.flags & kFlagScaleF16) ? 2 : 4;
+    const int sper = FMT == kQ8 ? 1 : p.groups_per_row;
+    return cu.rt * RW * sper * sb;
+  }
+
+  // Issues the loads of one tile without a branch.  Codes: buffer loads
+  // against a resource that starts at the tile's first row and ends at row N,
+  // so rows past N read as zero (and are never stored); chunks past K in a
+  // live row read the next row's codes, which meet zero activations.  Scales:
+  // the aligned dword holding each scale, from a resource over the copy's
+  // whole (256-byte aligned, dword-padded) scale array, widened when consumed.
+  static __device__ __forceinline__ void load(const QmvParams& p, const Cursor& cu,
+                                              const Offsets& o, Buf& buf) {
+    const QmvMat& mt = p.mat[cu.j];
+    const int sb = (p.flags & kFlagScaleF16) ? 2 : 4;
+    const long long row_bytes = (long long)p.chunks * 16;
+    const int r0 = cu.rt * RW;
+    // rows of the matrix at or after the tile's first row; a tile inside the
+    // Pack4 padding rows (r0 >= n) gets an empty resource: every load reads 0
+    const int rows = mt.n > r0 ? mt.n - r0 : 0;
+    const int sper = FMT == kQ8 ? 1 : p.groups_per_row;
+    const int sbytes = (mt.n * sper * sb + 3) & ~3;
+    const int toff = scale_tile_offset(p, cu);
+#pragma unroll
+    for (int h = 0; h < NW; ++h) {
+      const char* wb = (const char*)(h == 0 ? mt.w : mt.w2) + (cu.b * mt.w_bstride) * 4 +
+                       (long long)r0 * row_bytes;
+      const char* sbase = (const char*)(h == 0 ? mt.s : mt.s2) + cu.b * mt.s_bstride * sb;
+      const __amdgpu_buffer_rsrc_t wr =
+          __builtin_amdgcn_make_buffer_rsrc((void*)wb, (short)0, (int)(rows * row_bytes),
+                                            kBufferRsrcWord3);
+      const __amdgpu_buffer_rsrc_t sr =
+          __builtin_amdgcn_make_buffer_rsrc((void*)sbase, (short)0, sbytes, kBufferRsrcWord3);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+          buf.w[h][u][c] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o.w[u][c], 0, kStreamAux));
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+          buf.s[h][u][i] =
+              __builtin_amdgcn_raw_buffer_load_b32(sr, (toff + o.s[u][i]) & ~3, 0, 0);
+      }
+    }
+  }
+
+  // Activation rows of one batch entry into registers (RMS-normalised when the
+  // RMSNorm-in epilogue is on: every wave reduces sum(x^2) itself, which keeps
+  // the stream free of workgroup barriers).
+  static __device__ __forceinline__ void load_x(const QmvParams& p, const f16* xb, int lane,
+                                                int sub, XRegs& xr) {
+    const bool rms = (p.flags & kFlagRms) != 0;
+    const __amdgpu_buffer_rsrc_t grsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.gamma, (short)0, p.gamma ? p.k * 4 : 0, kBufferRsrcWord3);
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) {
+      if (m < p.m) {
+        const f16* row = xb + (long long)m * p.x_rstride;
+        float inv = 1.0f;
+        if (rms) {
+          float ss = 0.0f;
+          for (int kk = lane * 8; kk < p.k; kk += 512) {
+            const u32x4 t = *(const u32x4*)(row + kk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const f16x2 h = as_h2(t[i]);
+              const float a = (float)h[0], b = (float)h[1];
+              ss = fmaf(a, a, ss);
+              ss = fmaf(b, b, ss);
+            }
+          }
+          ss = wave_sum(ss);
+          inv = rsqrtf(fmaxf(ss / (float)p.k + p.eps, 1e-20f));
+        }
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          const int ci = sub + c * LPR;
+          uint32_t raw[XW];
+          if (ci < p.chunks) {
+            const u32x4* src = (const u32x4*)(row + (long long)ci * (XW * 2));
+#pragma unroll
+            for (int v = 0; v < XW / 4; ++v) {
+              const u32x4 t = src[v];
+              raw[4 * v + 0] = t[0];
+              raw[4 * v + 1] = t[1];
+              raw[4 * v + 2] = t[2];
+              raw[4 * v + 3] = t[3];
+            }
+            if (rms) {
+              // gamma through a buffer resource: one offset register per chunk,
+              // the rest are immediate offsets (the streaming kernels require
+              // gamma to cover K; shorter affine vectors take the generic path)
+              const int goff = ci * XW * 2 * 4;
+#pragma unroll
+              for (int d = 0; d < XW; d += 2) {
+                float g[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+                if (p.gamma) {
+                  const f32x4 t = __builtin_bit_cast(
+                      f32x4, __builtin_amdgcn_raw_buffer_load_b128(grsrc, goff + d * 8, 0, 0));
+                  g[0] = t[0];
+                  g[1] = t[1];
+                  g[2] = t[2];
+                  g[3] = t[3];
+                }
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                  const f16x2 h = as_h2(raw[d + e]);
+                  const f16x2 o = {(f16)((float)h[0] * inv * g[2 * e]),
+                                   (f16)((float)h[1] * inv * g[2 * e + 1])};
+                  raw[d + e] = as_u(o);
+                }
+              }
+            }
+          } else {
+#pragma unroll
+            for (int d = 0; d < XW; ++d) raw[d] = 0u;
+          }
+          if constexpr (FMT == kQ8) {
+#pragma unroll
+            for (int d = 0; d < XW; ++d) xr[m][c][d] = raw[d];
+          } else {
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+              q4_xpairs(raw[4 * d], raw[4 * d + 1], raw[4 * d + 2], raw[4 * d + 3],
+                        &xr[m][c][4 * d]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+#pragma unroll
+          for (int d = 0; d < XW; ++d) xr[m][c][d] = 0u;
+      }
+    }
+  }
+
+  // Dot products, row reduction, epilogue and store of one tile.
+  static __device__ __forceinline__ void compute(const QmvParams& p, const Cursor& cu,
+                                                 const Offsets& o, const Buf& buf,
+                                                 const XRegs& xr, int sub,
+                                                 int slot, float (&bv)[MMAX], int (&bi)[MMAX],
+                                                 float (&bs)[MMAX]) {
+    const QmvMat& mt = p.mat[cu.j];
+    const bool scl16 = (p.flags & kFlagScaleF16) != 0;
+    const int toff = scale_tile_offset(p, cu);
+    float acc[NW][U][MMAX];
+#pragma unroll
+    for (int h = 0; h < NW; ++h)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int m = 0; m < MMAX; ++m) acc[h][u][m] = 0.0f;
+
+#pragma unroll
+    for (int h = 0; h < NW; ++h)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          if constexpr (FMT == kQ8) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              uint32_t lo, hi;
+              q8_pairs(buf.w[h][u][c][d], lo, hi);
+#pragma unroll
+              for (int m = 0; m < MMAX; ++m)
+                acc[h][u][m] =
+                    dot2(hi, xr[m][c][2 * d + 1], dot2(lo, xr[m][c][2 * d], acc[h][u][m]));
+            }
+          } else {
+            constexpr int SPC = GM == kG16 ? 2 : 1;
+            float part[SPC][MMAX];
+#pragma unroll
+            for (int g = 0; g < SPC; ++g)
+#pragma unroll
+              for (int m = 0; m < MMAX; ++m) part[g][m] = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              uint32_t q[4];
+              q4_pairs(buf.w[h][u][c][d], q);
+              const int g = GM == kG16 ? (d >> 1) : 0;
+#pragma unroll
+              for (int m = 0; m < MMAX; ++m) {
+                float t = part[g][m];
+                t = dot2(q[0], xr[m][c][4 * d + 0], t);
+                t = dot2(q[1], xr[m][c][4 * d + 1], t);
+                t = dot2(q[2], xr[m][c][4 * d + 2], t);
+                t = dot2(q[3], xr[m][c][4 * d + 3], t);
+                part[g][m] = t;
+              }
+            }
+#pragma unroll
+            for (int g = 0; g < SPC; ++g)
+#pragma unroll
+              for (int m = 0; m < MMAX; ++m)
+                acc[h][u][m] = fmaf(part[g][m], scale_at(buf.s[h][u][c * SPC + g],
+                                                          toff + o.s[u][c * SPC + g], scl16),
+                                    acc[h][u][m]);
+          }
+        }
+
+#pragma unroll
+    for (int h = 0; h < NW; ++h)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int m = 0; m < MMAX; ++m) {
+          float v = group_sum<LPR>(acc[h][u][m]);
+          if constexpr (FMT == kQ8) v *= scale_at(buf.s[h][u][0], toff + o.s[u][0], scl16);
+          acc[h][u][m] = v;
+        }
+
+    const bool yf32 = (p.flags & kFlagYf32) != 0;
+    char* yb = (char*)mt.y + cu.b * mt.y_bstride * (yf32 ? 4 : 2);
+    const char* rb =
+        mt.res ? (const char*)mt.res + cu.b * mt.r_bstride * (yf32 ? 4 : 2) : nullptr;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int r = cu.rt * RW + u * SLOTS + slot;
+#pragma unroll
+      for (int m = 0; m < MMAX; ++m) {
+        float v = 0.0f;
+        const bool live = r < mt.n && m < p.m;
+        if (live) {
+          v = gemm_epilogue(p, m, r, acc[0][u][m]);
+          if constexpr (PAIR) v = silu(v) * gemm_epilogue(p, m, r, acc[1][u][m]);
+          if (rb && (p.flags & kFlagResidual)) {
+            const long long ri = (long long)m * p.r_rstride + r;
+            v += yf32 ? ((const float*)rb)[ri] : (float)((const f16*)rb)[ri];
+          }
+        }
+        // one lane per row stores; the lanes of a slot hold identical values
+        if (sub == ((u * MMAX + m) & (LPR - 1)) && r < mt.n_store && m < p.m && mt.y) {
+          const long long yi = (long long)m * mt.y_rstride + r;
+          if (yf32)
+            ((float*)yb)[yi] = v;
+          else
+            ((f16*)yb)[yi] = (f16)v;
+        }
+        if constexpr (ARGMAX) {
+          if (sub == 0 && live) argmax_merge(bv[m], bi[m], bs[m], v, r, -INFINITY);
+        }
+      }
+    }
+  }
+};
+
+template <int FMT, int LPR, int CPL, int U, int MMAX, bool PAIR, bool ARGMAX, int GM>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(MMAX > 1 || (FMT == kQ4 && CPL >= 4) ? 2 : (FMT == kQ4 && GM == kG16 ? 3 : 4))))
+void qmv_kernel(const QmvParams p) {
+  using Q = Qmv<FMT, LPR, CPL, U, MMAX, PAIR, ARGMAX, GM>;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane & (LPR - 1), slot = lane / LPR;
+  const int gw = blockIdx.x * kWaves + wave;
+  const int nw = gridDim.x * kWaves;
+  const int t0 = (int)((long long)gw * p.total_tiles / nw);
+  const int t1 = (int)((long long)(gw + 1) * p.total_tiles / nw);
+
+  float bv[MMAX], bs[MMAX];
+  int bi[MMAX];
+#pragma unroll
+  for (int m = 0; m < MMAX; ++m) {
+    bv[m] = __builtin_nanf("");
+    bi[m] = 0x7fffffff;
+    bs[m] = -INFINITY;
+  }
+
+  if (t0 < t1) {
+    const typename Q::Offsets o = Q::offsets(p, sub, slot);
+    typename Q::Cursor cu = Q::locate(p, t0);
+    typename Q::Buf A, B;
+    typename Q::XRegs xr;
+    const f16* xcur = nullptr;
+    Q::load(p, cu, o, A);
+    int t = t0;
+    while (true) {
+      // Tile t is in A.  The activation rows are (re)loaded first, then tile
+      // t+1's loads are issued into B (the last tile re-reads itself), then A
+      // is consumed while B is in flight.
+      {
+        const f16* xp = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
+        if (xp != xcur) {
+          Q::load_x(p, xp, lane, sub, xr);
+          xcur = xp;
+        }
+      }
+      bool more = t + 1 < t1;
+      typename Q::Cursor nx = more ? Q::advance(p, cu) : cu;
+      Q::load(p, nx, o, B);
+      Q::compute(p, cu, o, A, xr, sub, slot, bv, bi, bs);
+      if (!more) break;
+      ++t;
+      cu = nx;
+      // tile t is in B; tile t+1 goes into A
+      {
+        const f16* xp = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
+        if (xp != xcur) {
+          Q::load_x(p, xp, lane, sub, xr);
+          xcur = xp;
+        }
+      }
+      more = t + 1 < t1;
+      nx = more ? Q::advance(p, cu) : cu;
+      Q::load(p, nx, o, A);
+      Q::compute(p, cu, o, B, xr, sub, slot, bv, bi, bs);
+      if (!more) break;
+      ++t;
+      cu = nx;
+    }
+  }
+
+  if constexpr (ARGMAX) {
+    // every wave (also one without tiles) writes its partial for each row m
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) {
+      if (m < p.m) {
+        float v = bv[m], s = bs[m];
+        int i = bi[m];
+        argmax_wave_reduce(v, i, s);
+        if (lane == 0) {
+          const long long o = (long long)m * p.parts + gw;
+          p.part_best[o] = v;
+          p.part_index[o] = i;
+          p.part_second[o] = s;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace aexq
