@@ -56,6 +56,9 @@ struct aexq_ctx {
   long long part_cap = 0;
   float* logits_scratch = nullptr;
   long long logits_cap = 0;
+  // RMS-normalised activation rows of the MFMA path, grown on demand
+  void* act_scratch = nullptr;
+  long long act_cap = 0;
 };
 
 struct aexq_weight {
@@ -105,6 +108,7 @@ extern "C" void aexq_destroy(aexq_ctx* ctx) {
   (void)hipFree(ctx->part_index);
   (void)hipFree(ctx->part_second);
   (void)hipFree(ctx->logits_scratch);
+  (void)hipFree(ctx->act_scratch);
   delete ctx;
 }
 
@@ -140,7 +144,9 @@ static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const 
   w->code_bytes = (words < 1 ? 1 : words) * 4;
   w->scale_count = count / block;
   w->code_stride = round_up(w->code_bytes, 256);
-  w->scale_stride = round_up(w->scale_count * scale_bytes(scale_dtype), 256);
+  // at least 16 zeroed bytes after each copy's scales: the MFMA kernels' wide
+  // scale loads may run into them
+  w->scale_stride = round_up(w->scale_count * scale_bytes(scale_dtype) + 16, 256);
   // Device code layout: Q8 bytes biased by 128 (q + 128), Q4 nibbles offset-8
   // (q + 8).  Both are one XOR of the reference's two's-complement words; the
   // synthetic offset-8 Q4 words are already in device form.
@@ -162,6 +168,7 @@ static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const 
   if (e == hipSuccess) e = hipMalloc((void**)&w->codes, w->code_stride);
   if (e == hipSuccess) e = hipMalloc(&w->scales, w->scale_stride);
   if (e == hipSuccess) e = hipMemset(w->codes, pad_byte, w->code_stride);
+  if (e == hipSuccess) e = hipMemset(w->scales, 0, w->scale_stride);
   if (e == hipSuccess) e = hipMemcpy(w->codes, src, w->code_bytes, hipMemcpyHostToDevice);
   if (e == hipSuccess)
     e = hipMemcpy(w->scales, scales, w->scale_count * scale_bytes(scale_dtype),
@@ -417,13 +424,26 @@ static aexq_status view_tensor(const aexq_tensor* t, const char* op, const char*
 // ---------------------------------------------------------------------------
 // strict plan
 // ---------------------------------------------------------------------------
+enum PlanKind : int { kPlanGeneric = 0, kPlanStream = 1, kPlanMfma = 2 };
+
 struct Plan {
-  bool fast = false;
-  const QmvEntry* entry = nullptr;  // streaming kernel (fast path)
+  int kind = kPlanGeneric;
+  bool fast = false;                 // streaming matvec kernel
+  const QmvEntry* entry = nullptr;   // streaming kernel
+  const QmmEntry* mentry = nullptr;  // MFMA kernel
   int fmt = kQ8;
   int rows_per_tile = 0;
   QmvParams p{};
   int grid = 0;
+  // MFMA path: RMSNorm-in runs as a row pre-pass into the context's
+  // activation scratch; rows go in blocks of `mblock` per launch
+  bool rms_prepass = false;
+  int mblock = 0;
+  int x_f32 = 0;
+  int x_batch = 1;
+  long long x_rstride_in = 0;
+  long long x_bstride_in = 0;
+  int ysz = 2;
 };
 
 // Shape of the streaming kernel for `chunks` 16-byte code chunks per row:
@@ -578,14 +598,34 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   const bool x_ok = xv.dtype == AEXQ_DTYPE_F16 && xv.rstride % 8 == 0 &&
                     ((uintptr_t)xv.data % 16) == 0 && (xv.batch == 1 || xv.bstride % 8 == 0);
   const bool m_ok = M <= 8;
+  // MFMA path (M >= 2): 128-wide K slices, one scale per row or per 16/32 codes,
+  // fp16 activation rows (RMSNorm-in makes them in a pre-pass)
+  const bool rms_in = (a.flags & AEXQ_EPI_RMSNORM_IN) != 0;
+  const bool mfma_ok = M >= 2 && K % 128 == 0 &&
+                       (fmt == kQ8 || w0->block == 16 || w0->block == 32) &&
+                       (rms_in || (xv.dtype == AEXQ_DTYPE_F16 && xv.rstride % 2 == 0 &&
+                                   ((uintptr_t)xv.data % 4) == 0 &&
+                                   (xv.batch == 1 || xv.bstride % 2 == 0)));
   // the streaming kernels read gamma[0..K) directly (no index clamp)
   const bool rms_ok = !(a.flags & AEXQ_EPI_RMSNORM_IN) || !a.rms_gamma ||
                       (a.rms_gamma_size >= K && ((uintptr_t)a.rms_gamma % 4) == 0);
-  // 32-bit buffer offsets inside one weight copy
-  const bool size_ok = (long long)w0->n * K * w0->bits / 8 < (1LL << 31);
+  // 32-bit buffer offsets inside one weight copy (and below the kernels' no-chunk offset)
+  const bool size_ok = (long long)w0->n * K * w0->bits / 8 < (1LL << 30);
   plan->fmt = fmt;
   plan->fast = false;
-  if (chunked && group_ok && x_ok && m_ok && rms_ok && size_ok && chunks > 0) {
+  if (mfma_ok && size_ok) {
+    const int mt = M <= 16 ? 1 : 2;
+    const int nt = swiglu ? (mt == 1 ? 2 : 1) : (mt == 1 ? 4 : 2);
+    QmmConfig mc{fmt, gmode, mt, nt, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16};
+    plan->mentry = qmm_find(mc);
+    if (plan->mentry) {
+      plan->kind = kPlanMfma;
+      plan->rms_prepass = rms_in;
+      plan->mblock = 16 * mt;
+    }
+  }
+  if (plan->kind != kPlanMfma && chunked && group_ok && x_ok && m_ok && rms_ok && size_ok &&
+      chunks > 0) {
     const int mmax = M == 1 ? 1 : 8;
     int lpr = 0, cpl = 0;
     if (pick_shape(fmt, chunks, mmax, &lpr, &cpl)) {
@@ -598,9 +638,12 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
         plan->entry = qmv_find(cfg);
       }
       plan->fast = plan->entry != nullptr;
+      if (plan->fast) plan->kind = kPlanStream;
     }
   }
-  if (plan->fast) {
+  if (plan->kind == kPlanMfma) {
+    plan->rows_per_tile = plan->mentry->tn;
+  } else if (plan->fast) {
     plan->rows_per_tile = plan->entry->rw;
   } else {
     if (swiglu)
@@ -668,9 +711,31 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     tiles_total += (int)add;
   }
   p.total_tiles = tiles_total;
-  if (plan->fast) {
+  plan->x_f32 = xv.dtype == AEXQ_DTYPE_F32;
+  plan->x_batch = xv.batch;
+  plan->x_rstride_in = xv.rstride;
+  plan->x_bstride_in = xv.batch == 1 ? 0 : xv.bstride;
+  plan->ysz = yv[0].dtype == AEXQ_DTYPE_F32 ? 4 : 2;
+  if (plan->kind == kPlanMfma) {
+    p.flags &= ~kFlagRms;  // normalised by the pre-pass
+    if (plan->rms_prepass) {
+      // the scratch rows: [x batch][M][K] fp16 (pointer bound at launch)
+      p.x_rstride = K;
+      for (int i = 0; i < count; ++i) p.mat[i].x_bstride = xv.batch == 1 ? 0 : (long long)M * K;
+    }
+    int per_cu = qmm_blocks_per_cu(plan->mentry);
+    const char* env = getenv("AEXQ_QMM_BLOCKS_PER_CU");
+    if (env && atoi(env) > 0) per_cu = atoi(env);
+    const long long need = ((long long)tiles_total + kWaves - 1) / kWaves;
+    const long long cap = (long long)per_cu * ctx->cus;
+    plan->grid = (int)(need < cap ? need : cap);
+    if (plan->grid < 1) plan->grid = 1;
+  } else if (plan->fast) {
     // persistent grid: every wave resident, each owning a contiguous tile range
+    // Q4's heavier unpack streams best with twice the resident waves queued
+    // (8 workgroups of 4 waves per CU); Q8 with the resident count
     int per_cu = qmv_blocks_per_cu(plan->entry);
+    if (fmt == kQ4 && per_cu < 8) per_cu = 8;
     const char* env = getenv("AEXQ_QMV_BLOCKS_PER_CU");
     if (env && atoi(env) > 0) per_cu = atoi(env);
     const long long need = ((long long)tiles_total + kWaves - 1) / kWaves;
@@ -683,8 +748,46 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   return AEXQ_OK;
 }
 
+// MFMA path: optional RMSNorm pre-pass, then one launch per block of rows.
+static aexq_status launch_mfma(aexq_ctx* ctx, Plan& plan, const char* op) {
+  QmvParams p = plan.p;
+  const int M = p.m, K = p.k;
+  if (plan.rms_prepass) {
+    const long long need = (long long)plan.x_batch * M * K * 2;
+    if (need > ctx->act_cap) {
+      (void)hipFree(ctx->act_scratch);
+      ctx->act_scratch = nullptr;
+      ctx->act_cap = 0;
+      HIP_TRY(op, hipMalloc(&ctx->act_scratch, need));
+      ctx->act_cap = need;
+    }
+    hipError_t e = rmsnorm_rows_launch(p.mat[0].x, plan.x_f32, plan.x_rstride_in,
+                                       plan.x_bstride_in, plan.x_batch, M, K, plan.p.gamma,
+                                       plan.p.gamma_size, plan.p.eps, ctx->act_scratch,
+                                       ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, op, "rmsnorm pre-pass launch");
+    for (int i = 0; i < p.nmat; ++i) p.mat[i].x = ctx->act_scratch;
+  }
+  const int ysz = plan.ysz;
+  for (int m0 = 0; m0 < M; m0 += plan.mblock) {
+    QmvParams q = p;
+    q.m = M - m0 < plan.mblock ? M - m0 : plan.mblock;
+    q.m_base = m0;
+    for (int i = 0; i < q.nmat; ++i) {
+      QmvMat& mt = q.mat[i];
+      mt.x = (const char*)mt.x + (long long)m0 * q.x_rstride * 2;
+      if (mt.y) mt.y = (char*)mt.y + (long long)m0 * mt.y_rstride * ysz;
+      if (mt.res) mt.res = (const char*)mt.res + (long long)m0 * q.r_rstride * ysz;
+    }
+    hipError_t e = qmm_launch(plan.mentry, q, plan.grid, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, op, "mfma kernel launch");
+  }
+  return AEXQ_OK;
+}
+
 static aexq_status launch_plan(aexq_ctx* ctx, Plan& plan, const char* op) {
   HIP_TRY(op, hipSetDevice(ctx->device));
+  if (plan.kind == kPlanMfma) return launch_mfma(ctx, plan, op);
   hipError_t e = plan.fast ? qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream)
                            : generic_launch(plan.fmt, plan.p, plan.grid, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, op, "kernel launch");
@@ -701,6 +804,11 @@ extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, cons
   if (diag && diag_len) {
     if (st)
       snprintf(diag, diag_len, "%s", g_last_error.c_str());
+    else if (plan.kind == kPlanMfma)
+      snprintf(diag, diag_len, "kernel=qmm bits=%d mt=%d nt=%d swiglu=%d rms_prepass=%d "
+               "tiles=%d grid=%d mblock=%d",
+               w->bits, plan.mentry->cfg.mt, plan.mentry->cfg.nt, (int)plan.mentry->cfg.pair,
+               (int)plan.rms_prepass, plan.p.total_tiles, plan.grid, plan.mblock);
     else
       snprintf(diag, diag_len,
                "kernel=%s bits=%d lpr=%d cpl=%d u=%d mmax=%d swiglu=%d tiles=%d grid=%d",

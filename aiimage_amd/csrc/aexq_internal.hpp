@@ -50,6 +50,7 @@ struct QmvParams {
   int batch;
   int k;               // reduction length (shared)
   int m;               // activation rows
+  int m_base;          // first activation row of this launch (row index of bias C)
   int group;           // scale block (elements); == k for per-row
   int groups_per_row;  // k / group
   int chunks;          // 16-byte code chunks per row
@@ -98,6 +99,25 @@ const QmvEntry* qmv_find(const QmvConfig& cfg);
 // resident workgroups of an entry per CU (occupancy query, cached)
 int qmv_blocks_per_cu(const QmvEntry* e);
 hipError_t qmv_launch(const QmvEntry* e, const QmvParams& p, int grid, hipStream_t stream);
+
+// Small-M MFMA kernel registry (aexq_qmm.hip): rows M <= 64 per launch.
+struct QmmConfig {
+  int fmt, gmode, mt, nt;
+  bool pair, sf16;  // SwiGLU pair; fp16 (else fp32) scales
+};
+struct QmmEntry {
+  QmmConfig cfg;
+  QmvFn fn;
+  int tn;  // weight rows per tile
+};
+const QmmEntry* qmm_find(const QmmConfig& cfg);
+int qmm_blocks_per_cu(const QmmEntry* e);
+hipError_t qmm_launch(const QmmEntry* e, const QmvParams& p, int grid, hipStream_t stream);
+// RMSNorm of activation rows into fp16 rows (the M > 1 form of RMSNorm-in):
+// out[b][m][k] = fp16(x * rsqrt(max(mean(x^2) + eps, 1e-20)) * gamma[min(k, size-1)])
+hipError_t rmsnorm_rows_launch(const void* x, int x_f32, long long x_rstride, long long x_bstride,
+                               int batch, int m, int k, const float* gamma, int gamma_size,
+                               float eps, void* out, hipStream_t stream);
 hipError_t generic_launch(int fmt, const QmvParams& p, int grid, hipStream_t stream);
 int generic_rows_per_wg();
 hipError_t argmax_finalize_launch(const ArgmaxParams& a, hipStream_t stream);

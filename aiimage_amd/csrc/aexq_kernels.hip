@@ -105,6 +105,49 @@ __global__ __launch_bounds__(kThreads) void generic_kernel(const QmvParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// RMSNorm-in for M > 1 (CC:4531-4557): one workgroup per activation row
+// writes the normalised row as fp16, the activation precision the matmul
+// kernels consume.  out[b][m][k] (rows contiguous).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(const void* x, int x_f32,
+                                                                long long x_rstride,
+                                                                long long x_bstride, int m, int k,
+                                                                const float* gamma, int gamma_size,
+                                                                float eps, f16* out) {
+  const int row = blockIdx.x, b = blockIdx.y;
+  const long long base = (long long)b * x_bstride + (long long)row * x_rstride;
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < k; i += kThreads) {
+    const float v = x_f32 ? ((const float*)x)[base + i] : (float)((const f16*)x)[base + i];
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  __shared__ float red[kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) tot += red[w];
+  const float inv = rsqrtf(fmaxf(tot / (float)k + eps, 1e-20f));
+  f16* o = out + ((long long)b * m + row) * k;
+  for (int i = threadIdx.x; i < k; i += kThreads) {
+    const float v = x_f32 ? ((const float*)x)[base + i] : (float)((const f16*)x)[base + i];
+    float y = v * inv;
+    if (gamma) y *= gamma[i < gamma_size - 1 ? i : gamma_size - 1];
+    o[i] = (f16)y;
+  }
+}
+
+hipError_t rmsnorm_rows_launch(const void* x, int x_f32, long long x_rstride, long long x_bstride,
+                               int batch, int m, int k, const float* gamma, int gamma_size,
+                               float eps, void* out, hipStream_t stream) {
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(m, batch), dim3(kThreads), 0, stream, x, x_f32,
+                     x_rstride, x_bstride, m, k, gamma, gamma_size, eps, (f16*)out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Argmax over existing fp32 logits rows, and the final merge of partials.
 // ---------------------------------------------------------------------------
 constexpr int kArgmaxCols = 4096;

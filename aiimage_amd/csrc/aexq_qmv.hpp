@@ -70,6 +70,8 @@ struct Qmv {
     int w[U][CPL];
     int s[U][NS];
   };
+  // byte offset beyond any resource (weight copies are < 2 GiB)
+  static constexpr int kNoChunk = 0x7ffffff0;
 
   static __device__ __forceinline__ Offsets offsets(const QmvParams& p, int sub, int slot) {
     Offsets o;
@@ -79,7 +81,11 @@ struct Qmv {
     for (int u = 0; u < U; ++u) {
       const int rr = u * SLOTS + slot;
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) o.w[u][c] = rr * row_bytes + (sub + c * LPR) * 16;
+      for (int c = 0; c < CPL; ++c) {
+        // a chunk past K points beyond every resource: it reads 0 with no traffic
+        const int ci = sub + c * LPR;
+        o.w[u][c] = ci < p.chunks ? rr * row_bytes + ci * 16 : kNoChunk;
+      }
       if constexpr (FMT == kQ8) {
         o.s[u][0] = rr * sb;
       } else {
@@ -108,8 +114,8 @@ struct Qmv {
 
   // Issues the loads of one tile without a branch.  Codes: buffer loads
   // against a resource that starts at the tile's first row and ends at row N,
-  // so rows past N read as zero (and are never stored); chunks past K in a
-  // live row read the next row's codes, which meet zero activations.  Scales:
+  // so rows past N, and chunks past K, read as zero without memory traffic
+  // (and are never stored / meet zero activations).  Scales:
   // the aligned dword holding each scale, from a resource over the copy's
   // whole (256-byte aligned, dword-padded) scale array, widened when consumed.
   static __device__ __forceinline__ void load(const QmvParams& p, const Cursor& cu,

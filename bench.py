@@ -7,9 +7,11 @@ gate/up 1024->3584, down 3584->1024), symmetric 4-bit offset-8 codes with one
 fp16 scale per 32 K, fp16 activations, fp32 accumulation, fp16 outputs.
 
 "Cold" follows the sustained protocol of the benchmark: COPIES distinct
-device copies of the layer's weights (>= 1 GiB in total, far above the 256 MB
-Infinity Cache and the L2s) are processed in every step, so no weight byte is
-re-read from a cache.  One step = the layer's linears over all copies in four
+device copies of the layer's weights are processed in every step, enough that
+each of the step's launches cycles through >= 1 GiB of distinct weights (the
+smallest launch, o_proj, sets the count: about 900 copies, 8.3 GB), far above
+the 256 MB Infinity Cache and the L2s, so no weight byte is re-read from a
+cache.  One step = the layer's linears over all copies in four
 launches: RMSNorm-in + q/k/v (one grouped launch), RMSNorm-in + gate/up with
 the SwiGLU-out epilogue, o_proj (input: that copy's q output), down (input:
 that copy's SwiGLU output).
@@ -42,7 +44,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--copies", type=int, default=0,
-                    help="layer copies per step (default: enough for >= 1 GiB)")
+                    help="layer copies per step (default: every launch streams >= 1 GiB)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the per-config extras")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -186,6 +188,59 @@ def extras(torch, aexq, synth, ctx):
     return out
 
 
+def config4(torch, aexq, synth, ctx, copies: int = 120):
+    """Benchmark config 4: the layer's linears at M in {16, 64, 512} rows, Q4 and Q8,
+    on the MFMA path.  Every copy reads the same activation rows (x stays in L2)
+    and writes the same outputs (identical replicas), so the stream is the
+    weights plus each copy's algorithmic activation/output bytes; 120 copies
+    (1.1 GB of Q4 weights) per step keep the weights cold."""
+    out = {}
+    P4 = aexq.LAYOUT_PACK4_LINEAR
+    for bits in (4, 8):
+        ws = {}
+        for i, (name, n, k) in enumerate(synth.LAYER_LINEARS):
+            if bits == 4:
+                words, scales, _ = synth.q4_weights(n, k, 700 + i, group=32, code=synth.NIBBLE_OFFSET8)
+                qt = aexq.QuantizedTensor(n * k, 32, words, scales, bits=4, nibble_code=synth.NIBBLE_OFFSET8)
+            else:
+                words, scales, _ = synth.q8_weights(n, k, 700 + i)
+                qt = aexq.QuantizedTensor(n * k, k, words, scales, bits=8)
+            base = ctx.weight(qt, n, k)
+            ws[name] = base.replicate(copies)
+            base.release()
+        wbytes = 9_142_272 if bits == 4 else 16_277_504
+        for m in (16, 64, 512):
+            xs = {k: torch.as_tensor(synth.activations(m, k, 800 + k)).cuda() for k in (1024, 2048, 3584)}
+            gamma = torch.as_tensor(synth.rms_gamma(1024, 801)).cuda()
+            ys = {name: torch.zeros(m * n, dtype=torch.float16, device="cuda")
+                  for name, n, _ in synth.LAYER_LINEARS}
+            d = aexq.describe
+            yd = {name: d(ys[name], m, n, P4, batch=copies, batch_stride=0)
+                  for name, n, _ in synth.LAYER_LINEARS}
+            xd = {k: d(v, m, k) for k, v in xs.items()}
+
+            def step():
+                ctx.linear_group([ws["q_proj"], ws["k_proj"], ws["v_proj"]], xd[1024],
+                                 [yd["q_proj"], yd["k_proj"], yd["v_proj"]],
+                                 rmsnorm=True, rms_gamma=gamma, rms_eps=1e-6)
+                ctx.linear(ws["gate_proj"], xd[1024], yd["gate_proj"], rmsnorm=True,
+                           rms_gamma=gamma, rms_eps=1e-6, up=ws["up_proj"])
+                ctx.linear(ws["o_proj"], xd[2048], yd["o_proj"])
+                ctx.linear(ws["down_proj"], xd[3584], yd["down_proj"])
+            reps = 3 if m == 512 else 10
+            avg, med = time_launches(torch, step, reps)
+            b = copies * (wbytes + m * 46_080)
+            fl = copies * 2 * m * 16_252_928
+            out[f"config4_q{bits}_m{m}"] = {"copies": copies, "ms_per_step": round(med, 4),
+                                            "GBps": round(b / (med * 1e-3) / 1e9, 1),
+                                            "TFLOPs": round(fl / (med * 1e-3) / 1e12, 1)}
+            log(f"config4 q{bits} m={m}: {out[f'config4_q{bits}_m{m}']}")
+            del xs, ys
+        for w in ws.values():
+            w.release()
+    return out
+
+
 def cpu_baseline(seconds: float):
     """RunGemmCpu (GS:13328-13381) restated in C, timed on this host: the seven
     linears of one layer on dequantized fp32 weights (dequant untimed, as at
@@ -229,7 +284,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     ctx = aexq.Context(0)
-    copies = args.copies or -(-GIB // LAYER_BYTES)
+    # the smallest launch (o_proj: 1024 x 2048 Q4 codes + fp16 group scales)
+    o_proj_bytes = 1024 * 2048 // 2 + 1024 * (2048 // 32) * 2
+    copies = args.copies or -(-GIB // o_proj_bytes)
     log(f"building {copies} cold copies of the layer ({copies * LAYER_WEIGHT_BYTES / 1e9:.2f} GB)")
     layer = Layer(ctx, aexq, synth, torch, copies, synth.SEED_BASE + 2)
     torch.cuda.synchronize()
@@ -278,6 +335,7 @@ def main():
         torch.cuda.empty_cache()
         log("extras: config 1 and config 5")
         result["extra"] = extras(torch, aexq, synth, ctx)
+        result["extra"].update(config4(torch, aexq, synth, ctx))
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -482,3 +482,132 @@ def test_linearity_at_full_layer_size(ctx, aexq):
     ctx.linear(w, aexq.describe(dev(2 * x, torch.float16), 1, k), aexq.describe(y2, 1, n, 1))
     torch.cuda.synchronize()
     assert torch.equal(y2, 2 * y1)
+
+
+# ------------------------------------------------------------------ small-M MFMA path (config 4)
+
+def _mm_case(ctx, aexq, orc, fmt, n, k, m, seed, group=32, code=1, scale_f16=True, ydtype=None,
+             **kw):
+    """One linear on the M >= 2 path; returns (y [m][n] float64, ref, plan string)."""
+    from aiimage_amd import synth
+    sdt = np.float16 if scale_f16 else np.float32
+    if fmt == 8:
+        words, scales, _ = synth.q8_weights(n, k, seed, scale_dtype=sdt)
+        w = ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
+        wf = orc.dequant_q8(words, scales, n, k,
+                            scale_dtype=orc.SCALE_F16 if scale_f16 else orc.SCALE_F32)
+    else:
+        w, words, scales = _q4_weight(ctx, aexq, n, k, seed, group=group, code=code,
+                                      scale_f16=scale_f16)
+        wf = orc.dequant_q4(words, scales, n, k, group, nibble_code=code,
+                            scale_dtype=orc.SCALE_F16 if scale_f16 else orc.SCALE_F32)
+    x16 = synth.activations(m, k, seed + 1)
+    ydtype = ydtype or torch.float16
+    y = aexq.new_activation(m, n, ydtype, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    plan = ctx.plan_check(w, xd, yd, **kw)
+    ctx.linear(w, xd, yd, **kw)
+    torch.cuda.synchronize()
+    stride = aexq.storage_elements(aexq.LAYOUT_PACK4_LINEAR, m, n)
+    got = y.cpu().numpy().astype(np.float64).reshape(m, stride)
+    assert np.all(got[:, n:] == 0)
+    return got[:, :n], wf, x16, plan
+
+
+@pytest.mark.parametrize("fmt,n,k,m", [(8, 3584, 1024, 16), (8, 1024, 2048, 64), (8, 1024, 1024, 512),
+                                       (4, 3584, 1024, 16), (4, 1024, 3584, 64), (4, 2048, 1024, 512),
+                                       (4, 512, 1024, 5), (8, 256, 384, 31)])
+def test_small_m_mfma_config4(ctx, aexq, orc, fmt, n, k, m):
+    """Batched decode / short prefill shapes on the MFMA path against the float64 oracle."""
+    _announce(f"mfma q{fmt} n={n} k={k} m={m}")
+    got, wf, x16, plan = _mm_case(ctx, aexq, orc, fmt, n, k, m, seed=n + k + m)
+    assert plan.startswith("kernel=qmm"), plan
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    assert normwise(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("group,scale_f16,code", [(16, False, 0), (16, True, 0), (32, False, 0)])
+def test_small_m_mfma_reference_q4_formats(ctx, aexq, orc, group, scale_f16, code):
+    """The reference's shipping Q4 (two's complement, group 16, fp32 scales) and its
+    neighbours at M > 1, fp32 output for a tight bar."""
+    _announce(f"mfma q4 group={group} f16={scale_f16}")
+    got, wf, x16, plan = _mm_case(ctx, aexq, orc, 4, 1024, 1024, 12, seed=40 + group,
+                                  group=group, code=code, scale_f16=scale_f16,
+                                  ydtype=torch.float32)
+    assert plan.startswith("kernel=qmm"), plan
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    assert normwise(got, ref) <= 1e-5
+
+
+def test_small_m_mfma_swiglu_rmsnorm(ctx, aexq, orc):
+    """M=20 gate/up with RMSNorm-in (row pre-pass) and SwiGLU-out on the MFMA path."""
+    _announce("mfma swiglu rmsnorm m=20")
+    from aiimage_amd import synth
+    n, k, m, eps = 3584, 1024, 20, 1e-6
+    wg, gw, gs = _q4_weight(ctx, aexq, n, k, 61)
+    wu, uw, us = _q4_weight(ctx, aexq, n, k, 62)
+    x16 = synth.activations(m, k, 63)
+    gamma = synth.rms_gamma(k, 64)
+    y = aexq.new_activation(m, n, torch.float16, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    kw = dict(rmsnorm=True, rms_gamma=dev(gamma), rms_eps=eps, up=wu)
+    plan = ctx.plan_check(wg, xd, yd, **kw)
+    assert plan.startswith("kernel=qmm") and "rms_prepass=1" in plan, plan
+    ctx.linear(wg, xd, yd, **kw)
+    torch.cuda.synchronize()
+    xn = orc.rmsnorm(x16.astype(np.float32), eps, gamma).astype(np.float16).astype(np.float32)
+    g = _q4_ref(orc, gw, gs, n, k, 32, 1, True, xn)
+    u = _q4_ref(orc, uw, us, n, k, 32, 1, True, xn)
+    ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32)) for r in range(m)])
+    got = y.cpu().numpy().astype(np.float64).reshape(m, -1)[:, :n]
+    assert normwise(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("bcast", [1, 3])
+def test_small_m_mfma_row_blocks_bias_residual(ctx, aexq, orc, bcast):
+    """M=33 crosses the 32-row launch blocks: row-indexed C and the residual must
+    follow each block's rows."""
+    _announce(f"mfma m=33 bcast={bcast}")
+    from aiimage_amd import synth
+    n, k, m = 512, 1024, 33
+    words, scales, _ = synth.q8_weights(n, k, 71, scale_dtype=np.float32)
+    w = ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
+    x16 = synth.activations(m, k, 72)
+    rng = np.random.default_rng(73)
+    c = rng.standard_normal(m if bcast == 1 else m * n).astype(np.float32)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+    rd = dev(res)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    kw = dict(alpha=0.75, beta=1.5, c=dev(c), broadcast_c=bcast,
+              residual=aexq.describe(rd, m, n, aexq.LAYOUT_PACK4_LINEAR))
+    assert ctx.plan_check(w, xd, yd, **kw).startswith("kernel=qmm")
+    ctx.linear(w, xd, yd, **kw)
+    torch.cuda.synchronize()
+    s = orc.gemm_gpu_semantics(x16.astype(np.float32), orc.dequant_q8(words, scales, n, k))
+    cc = np.repeat(c[:, None], n, 1) if bcast == 1 else c.reshape(m, n)
+    ref = 0.75 * (1.5 * cc + s) + res
+    got = y.cpu().numpy().reshape(m, n)
+    assert normwise(got, ref) <= 1e-5
+
+
+def test_small_m_mfma_stacked_copies_match_single(ctx, aexq):
+    """Size-independent property at M=16: every copy of a replicated weight stack
+    gives exactly the single-weight output."""
+    _announce("mfma stacked copies")
+    from aiimage_amd import synth
+    n, k, m, copies = 2048, 1024, 16, 5
+    w, _, _ = _q4_weight(ctx, aexq, n, k, 81)
+    x = dev(synth.activations(m, k, 82))
+    y1 = aexq.new_activation(m, n, torch.float16, aexq.LAYOUT_PACK4_LINEAR)
+    ctx.linear(w, aexq.describe(x, m, k), aexq.describe(y1, m, n, aexq.LAYOUT_PACK4_LINEAR))
+    st = w.replicate(copies)
+    ys = torch.zeros(copies * m * n, dtype=torch.float16, device="cuda")
+    ctx.linear(st, aexq.describe(x, m, k),
+               aexq.describe(ys, m, n, aexq.LAYOUT_PACK4_LINEAR, batch=copies, batch_stride=m * n))
+    torch.cuda.synchronize()
+    for c in range(copies):
+        assert torch.equal(ys[c * m * n:(c + 1) * m * n], y1)
