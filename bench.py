@@ -32,6 +32,10 @@ import time
 
 METRIC = ("cold-HBM GB/s (% of peak) per quant matvec; decode tokens/s, 0.8B-shape, 1 GPU")
 HBM_PEAK_GBS = 8000.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
+# HBM bytes per dispatch of the dominant kernel, from two rocprofv3 --pmc runs of
+# this bench (FETCH_SIZE, WRITE_SIZE) scaled by the calibration kernel's counts
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmv_q4_layer_config2_traffic.json")
 LAYER_WEIGHT_BYTES = 9_142_272
 LAYER_ACT_BYTES = 46_080
 LAYER_BYTES = LAYER_WEIGHT_BYTES + LAYER_ACT_BYTES
@@ -48,6 +52,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the per-config extras")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calib", action="store_true",
+                    help="also run one 256 MiB fp32 neg kernel (known HBM traffic) to scale "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -284,6 +291,12 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     ctx = aexq.Context(0)
+    if args.calib:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)       # reads 256 MiB, writes 256 MiB
+        torch.cuda.synchronize()
+        del src, dst
     # the smallest launch (o_proj: 1024 x 2048 Q4 codes + fp16 group scales)
     o_proj_bytes = 1024 * 2048 // 2 + 1024 * (2048 // 32) * 2
     copies = args.copies or -(-GIB // o_proj_bytes)
@@ -314,8 +327,14 @@ def main():
         per[name] = {"ms": avg, "ms_median": med, "bytes": b, "GBps": b / (avg * 1e-3) / 1e9}
     dom = max(per, key=lambda k: per[k]["ms"])
     ach = per[dom]["GBps"]
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        rec = json.load(open(TRAFFIC_FILE))
+        if rec.get("launch") == dom and rec.get("copies") == copies:
+            traffic = rec.get("hbm_bytes_per_dispatch")
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None}
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "algorithmic_bytes": per[dom]["bytes"]}
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
