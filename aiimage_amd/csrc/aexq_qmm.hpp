@@ -4,9 +4,11 @@
 // "steps" -- (weight tile of TN = 16 x NT rows, 128-wide K slice) pairs over
 // every matrix and batch entry of the launch -- and keeps the next step's
 // loads in flight while the current one is consumed.  Per step and 16-row
-// weight block a lane loads its B fragments straight from HBM: Q4, one dword
-// (8 codes) from each of the slice's four 32-code groups, so each MFMA covers
-// exactly one scale group; Q8, one 32-code run.  Codes
+// weight block the four 16-lane rows of a wave read 64 contiguous code bytes
+// of each weight row (16 bytes per lane) straight from HBM.  For Q4 a lane's
+// 16 bytes are one 32-code group; a 4x4 dword transpose across the four lane
+// rows (v_permlane32_swap / v_permlane16_swap) turns them into four MFMA B
+// fragments that each cover exactly one scale group.  Codes
 // become exact fp16 integers (q4_pairs / q8_pairs) and meet fp16 activations
 // in v_mfma_f32_16x16x32_f16.  Q4 scales are applied in fp32 to each group's
 // MFMA result (one group = one MFMA K-extent, so the dequantised weight is
@@ -26,6 +28,20 @@
 namespace aexq {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// 4x4 transpose of dwords across the four 16-lane rows of a wave: on return,
+// register q of row R holds what register R of row q held.
+__device__ __forceinline__ void rows_transpose4(uint32_t& c0, uint32_t& c1, uint32_t& c2,
+                                                uint32_t& c3) {
+  const auto s02 = __builtin_amdgcn_permlane32_swap(c0, c2, false, false);
+  const auto s13 = __builtin_amdgcn_permlane32_swap(c1, c3, false, false);
+  const auto t0 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+  const auto t1 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+  c0 = t0[0];
+  c1 = t0[1];
+  c2 = t1[0];
+  c3 = t1[1];
+}
 
 __device__ __forceinline__ f16x8 pack8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
@@ -116,21 +132,19 @@ struct Qmm {
       for (int nt = 0; nt < NT; ++nt) {
         const int rr = 16 * nt + n_l;
         if constexpr (FMT == kQ8) {
-          // 32 codes: k = 32 kb .. 32 kb + 31 of the slice
+          // codes 16 kb .. 16 kb + 15 and 64 + 16 kb .. 64 + 16 kb + 15 of the slice
           buf.w[h][nt][0] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, rr * row_bytes + 32 * kb, 0,
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, rr * row_bytes + 16 * kb, 0,
                                                            kStreamAux));
           buf.w[h][nt][1] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, rr * row_bytes + 32 * kb + 16, 0,
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, rr * row_bytes + 16 * kb + 64, 0,
                                                            kStreamAux));
           buf.s[h][nt][0] = u32x4{0u, 0u, 0u, 0u};
         } else {
-          // word kb (codes 8 kb .. 8 kb + 7) of each group 4 s + q, q < 4
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            buf.w[h][nt][0][q] =
-                __builtin_amdgcn_raw_buffer_load_b32(wr, rr * row_bytes + 16 * q + 4 * kb, 0,
-                                                     kStreamAux);
+          // group 4 s + kb: 32 codes
+          buf.w[h][nt][0] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, rr * row_bytes + 16 * kb, 0,
+                                                           kStreamAux));
 #pragma unroll
           for (int v = 0; v < SV; ++v)
             buf.s[h][nt][v] = __builtin_bit_cast(
@@ -149,8 +163,9 @@ struct Qmm {
       const int off = (16 * m + n_l) * (int)rs2;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        // Q4: group q of the slice, 8 codes at 8 kb; Q8: 8 codes at 32 kb + 8 q
-        const int ko = FMT == kQ8 ? (32 * kb + 8 * q) : (32 * q + 8 * kb);
+        // Q4: group q of the slice, 8 codes at 8 kb; Q8: the lane's B codes of MFMA q,
+        // 8 at 16 kb + 8 q (q < 2) or 64 + 16 kb + 8 (q - 2)
+        const int ko = FMT == kQ8 ? ((q >> 1) * 64 + 16 * kb + 8 * (q & 1)) : (32 * q + 8 * kb);
         buf.x[m][q] =
             __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 2 * ko, 0, 0));
       }
@@ -180,8 +195,13 @@ struct Qmm {
             code[h][nt][q][1] = src[2 * (q & 1) + 1];
           }
         } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) code[h][nt][q][0] = buf.w[h][nt][0][q];
+          uint32_t c0 = buf.w[h][nt][0][0], c1 = buf.w[h][nt][0][1], c2 = buf.w[h][nt][0][2],
+                   c3 = buf.w[h][nt][0][3];
+          rows_transpose4(c0, c1, c2, c3);
+          code[h][nt][0][0] = c0;
+          code[h][nt][1][0] = c1;
+          code[h][nt][2][0] = c2;
+          code[h][nt][3][0] = c3;
         }
       }
 #pragma unroll
@@ -341,6 +361,9 @@ void qmm_kernel(const QmvParams p) {
     bool more = t + 1 < t1;
     typename Q::Cursor nx = more ? Q::advance(p, cu) : cu;
     Q::load(p, nx, lane, B);
+    // keep the prefetch issued ahead of the consumer (the scheduler otherwise
+    // sinks it below the MFMAs and every slice waits for its own loads)
+    __builtin_amdgcn_sched_barrier(0);
     Q::compute(p, lane, A, acc);
     if (cu.s == steps - 1) Q::finish(p, cu, lane, acc);
     if (!more) break;
@@ -349,6 +372,7 @@ void qmm_kernel(const QmvParams p) {
     more = t + 1 < t1;
     nx = more ? Q::advance(p, cu) : cu;
     Q::load(p, nx, lane, A);
+    __builtin_amdgcn_sched_barrier(0);
     Q::compute(p, lane, B, acc);
     if (cu.s == steps - 1) Q::finish(p, cu, lane, acc);
     if (!more) break;
