@@ -152,6 +152,12 @@ def _declare(L):
         "aexq_lmhead_argmax": (i32, [P, P, TP, TP, P, P]),
         "aexq_argmax": (i32, [P, TP, P, P]),
         "aexq_dequant": (i32, [P, P, P]),
+        "aexq_rmsnorm": (i32, [P, TP, TP, P, i32, f32]),
+        "aexq_embed_q8": (i32, [P, P, P, i32, P]),
+        "aexq_rope_kv_append": (i32, [P, P, P, P, P, P, i32, i32, i32, i32, i32, P, P]),
+        "aexq_attention_decode": (i32, [P, P, P, P, i32, i32, i32, i32, i32, f32, P]),
+        "aexq_attention_decode_rope": (i32, [P, P, P, P, P, P, i32, i32, i32, i32, i32, P, P,
+                                             f32, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -159,6 +159,11 @@ class Context:
     def synchronize(self):
         check(self._lib.aexq_synchronize(self.handle), "aexq_synchronize")
 
+    def set_stream(self, stream):
+        """Enqueue subsequent work on `stream` (a torch HIP stream)."""
+        self.stream = stream
+        check(self._lib.aexq_set_stream(self.handle, _stream_handle(stream)), "aexq_set_stream")
+
     # ---- weights
     def weight(self, qt: QuantizedTensor, n: int, k: int) -> "QuantWeight":
         """Direct upload of a packed record (GS:12887-12907 / GS:12966-12996)."""
@@ -235,6 +240,51 @@ class Context:
                                     ctypes.c_void_p(argmax.data_ptr()),
                                     ctypes.c_void_p(top2_gap.data_ptr()) if top2_gap is not None else None),
               "aexq_argmax")
+
+    # ---- decode-step operators around the linears
+    def rmsnorm(self, x: _abi.Tensor, y: _abi.Tensor, gamma: Optional[torch.Tensor] = None,
+                eps: float = 1e-3):
+        """AexisRMSNormLayer (RMS:24-46): y = fp16(x * rsqrt(mean x^2 + eps) * gamma)."""
+        check(self._lib.aexq_rmsnorm(self.handle, ctypes.byref(x), ctypes.byref(y),
+                                     ctypes.c_void_p(gamma.data_ptr()) if gamma is not None else None,
+                                     gamma.numel() if gamma is not None else 0, eps), "aexq_rmsnorm")
+
+    def embed_q8(self, table: "QuantWeight", tokens: torch.Tensor, out: torch.Tensor):
+        """Tied Q8 embedding rows (Qwen35SharedTokenEmbeddingWeights.cs:185-198)."""
+        check(self._lib.aexq_embed_q8(self.handle, table.handle, ctypes.c_void_p(tokens.data_ptr()),
+                                      tokens.numel(), ctypes.c_void_p(out.data_ptr())),
+              "aexq_embed_q8")
+
+    def rope_kv_append(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor, heads_q: int, heads_kv: int,
+                       head_dim: int, capacity: int, position: int, cos_t: torch.Tensor,
+                       sin_t: torch.Tensor):
+        """RoPE (PN:414-473, rotate-half) on q in place and k into the cache; v appended."""
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        check(self._lib.aexq_rope_kv_append(self.handle, P(q), P(k), P(v), P(k_cache), P(v_cache),
+                                            heads_q, heads_kv, head_dim, capacity, position,
+                                            P(cos_t), P(sin_t)), "aexq_rope_kv_append")
+
+    def attention_decode(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                         heads_q: int, heads_kv: int, head_dim: int, capacity: int, length: int,
+                         scale: float, out: torch.Tensor):
+        """GQA decode attention over the cache (MM:420-544)."""
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        check(self._lib.aexq_attention_decode(self.handle, P(q), P(k_cache), P(v_cache), heads_q,
+                                              heads_kv, head_dim, capacity, length, scale, P(out)),
+              "aexq_attention_decode")
+
+    def attention_decode_rope(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              k_cache: torch.Tensor, v_cache: torch.Tensor, heads_q: int,
+                              heads_kv: int, head_dim: int, capacity: int, length: int,
+                              cos_t: torch.Tensor, sin_t: torch.Tensor, scale: float,
+                              out: torch.Tensor):
+        """RoPE + K/V append at position length-1 + decode attention in one pass."""
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        check(self._lib.aexq_attention_decode_rope(self.handle, P(q), P(k), P(v), P(k_cache),
+                                                   P(v_cache), heads_q, heads_kv, head_dim,
+                                                   capacity, length, P(cos_t), P(sin_t), scale,
+                                                   P(out)), "aexq_attention_decode_rope")
 
     def dequant(self, w: "QuantWeight") -> torch.Tensor:
         info = w.info()

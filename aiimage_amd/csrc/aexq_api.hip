@@ -59,6 +59,9 @@ struct aexq_ctx {
   // RMS-normalised activation rows of the MFMA path, grown on demand
   void* act_scratch = nullptr;
   long long act_cap = 0;
+  // decode attention split partials
+  float* attn_part = nullptr;
+  long long attn_cap = 0;
 };
 
 struct aexq_weight {
@@ -109,6 +112,7 @@ extern "C" void aexq_destroy(aexq_ctx* ctx) {
   (void)hipFree(ctx->part_second);
   (void)hipFree(ctx->logits_scratch);
   (void)hipFree(ctx->act_scratch);
+  (void)hipFree(ctx->attn_part);
   delete ctx;
 }
 
@@ -947,5 +951,131 @@ extern "C" aexq_status aexq_dequant(aexq_ctx* ctx, const aexq_weight* w, float* 
   hipError_t e = dequant_launch(fmt, w->codes, w->scales, w->scale_dtype == AEXQ_DTYPE_F16, w->n,
                                 w->k, w->block, out, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, op, "dequant launch");
+  return AEXQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// decode-step operators
+// ---------------------------------------------------------------------------
+extern "C" aexq_status aexq_rmsnorm(aexq_ctx* ctx, const aexq_tensor* x, const aexq_tensor* y,
+                                    const float* gamma, int gamma_size, float eps) {
+  const char* op = "aexq_rmsnorm";
+  if (!ctx) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "ctx is NULL");
+  TensorView xv, yv;
+  aexq_status st = view_tensor(x, op, "x", &xv);
+  if (st) return st;
+  st = view_tensor(y, op, "y", &yv);
+  if (st) return st;
+  if (yv.rows != xv.rows || yv.width != xv.width)
+    return fail(AEXQ_ERR_SHAPE, op, "y [%d][%d] != x [%d][%d] | layer=RMSNorm", yv.rows, yv.width,
+                xv.rows, xv.width);
+  if (yv.dtype != AEXQ_DTYPE_F16 || yv.rstride != yv.width)
+    return fail(AEXQ_ERR_UNSUPPORTED, op,
+                "y must be fp16 rows of exactly W elements | layer=RMSNorm | rejectedFallback=layout");
+  if (xv.batch != yv.batch || (yv.batch > 1 && yv.bstride != (long long)yv.rows * yv.width))
+    return fail(AEXQ_ERR_SHAPE, op, "batched y must be contiguous [batch][rows][W]");
+  if (gamma && gamma_size <= 0)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "gamma_size=%d", gamma_size);
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  hipError_t e = rmsnorm_rows_launch(xv.data, xv.dtype == AEXQ_DTYPE_F32, xv.rstride,
+                                     xv.batch == 1 ? 0 : xv.bstride, xv.batch, xv.rows, xv.width,
+                                     gamma, gamma_size, eps, yv.data, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "rmsnorm launch");
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_embed_q8(aexq_ctx* ctx, const aexq_weight* table,
+                                     const int32_t* tokens, int m, void* out) {
+  const char* op = "aexq_embed_q8";
+  if (!ctx || !table || !tokens || !out) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (table->bits != 8 || table->block != table->k)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "embedding table must be Q8 with one scale per row");
+  if (m <= 0) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "m=%d", m);
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  hipError_t e = embed_q8_launch(table->codes, table->scales, table->scale_dtype == AEXQ_DTYPE_F16,
+                                 table->k, tokens, m, table->n, out, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "embedding launch");
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_rope_kv_append(aexq_ctx* ctx, void* q, const void* k, const void* v,
+                                           void* k_cache, void* v_cache, int heads_q,
+                                           int heads_kv, int head_dim, int capacity, int position,
+                                           const float* cos_table, const float* sin_table) {
+  const char* op = "aexq_rope_kv_append";
+  if (!ctx || !q || !k || !v || !k_cache || !v_cache || !cos_table || !sin_table)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (heads_q <= 0 || heads_kv <= 0 || head_dim <= 0 || (head_dim & 1))
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "heads_q=%d heads_kv=%d head_dim=%d", heads_q,
+                heads_kv, head_dim);
+  if (position < 0 || position >= capacity)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "position=%d outside the cache capacity %d",
+                position, capacity);
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  hipError_t e = rope_kv_launch(q, k, v, k_cache, v_cache, heads_q, heads_kv, head_dim, capacity,
+                                position, cos_table, sin_table, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "rope launch");
+  return AEXQ_OK;
+}
+
+// Shared checks of the decode attention entry points; sizes the split scratch.
+static aexq_status attn_prepare(aexq_ctx* ctx, const char* op, int heads_q, int heads_kv,
+                                int head_dim, int capacity, int length) {
+  if (head_dim != 128)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "head_dim=%d (kernel is built for 128) | layer=SDPA",
+                head_dim);
+  if (heads_kv <= 0 || heads_q <= 0 || heads_q % heads_kv != 0)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "heads_q=%d heads_kv=%d", heads_q, heads_kv);
+  const int group = heads_q / heads_kv;
+  if (group != 1 && group != 2 && group != 4 && group != 8)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "query heads per key head = %d (1, 2, 4 or 8)", group);
+  if (length <= 0 || length > capacity)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "length=%d capacity=%d", length, capacity);
+  const int splits = attn_splits(length, group);
+  if (splits > 1024)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "length=%d needs %d splits (at most 1024)", length,
+                splits);
+  const long long need = (long long)heads_q * splits * (head_dim + 2);
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  if (need > ctx->attn_cap) {
+    (void)hipFree(ctx->attn_part);
+    ctx->attn_part = nullptr;
+    ctx->attn_cap = 0;
+    HIP_TRY(op, hipMalloc((void**)&ctx->attn_part, need * sizeof(float)));
+    ctx->attn_cap = need;
+  }
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_attention_decode(aexq_ctx* ctx, const void* q, const void* k_cache,
+                                             const void* v_cache, int heads_q, int heads_kv,
+                                             int head_dim, int capacity, int length, float scale,
+                                             void* out) {
+  const char* op = "aexq_attention_decode";
+  if (!ctx || !q || !k_cache || !v_cache || !out)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  aexq_status st = attn_prepare(ctx, op, heads_q, heads_kv, head_dim, capacity, length);
+  if (st) return st;
+  hipError_t e = attn_decode_launch(q, k_cache, v_cache, heads_q, heads_kv, capacity, length,
+                                    scale, ctx->attn_part, out, nullptr, nullptr, nullptr, nullptr,
+                                    ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "attention launch");
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_attention_decode_rope(aexq_ctx* ctx, const void* q, const void* k,
+                                                  const void* v, void* k_cache, void* v_cache,
+                                                  int heads_q, int heads_kv, int head_dim,
+                                                  int capacity, int length, const float* cos_table,
+                                                  const float* sin_table, float scale, void* out) {
+  const char* op = "aexq_attention_decode_rope";
+  if (!ctx || !q || !k || !v || !k_cache || !v_cache || !cos_table || !sin_table || !out)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  aexq_status st = attn_prepare(ctx, op, heads_q, heads_kv, head_dim, capacity, length);
+  if (st) return st;
+  hipError_t e = attn_decode_launch(q, k_cache, v_cache, heads_q, heads_kv, capacity, length,
+                                    scale, ctx->attn_part, out, k, v, cos_table, sin_table,
+                                    ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "attention launch");
   return AEXQ_OK;
 }

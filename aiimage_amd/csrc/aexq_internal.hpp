@@ -129,4 +129,18 @@ hipError_t dequant_launch(int fmt, const uint32_t* w, const void* s, int scale_f
 hipError_t replicate_launch(const void* src, void* dst, long long bytes, int copies,
                             hipStream_t stream);
 
+// decode-step kernels (aexq_decode.hip)
+hipError_t embed_q8_launch(const uint32_t* codes, const void* scales, int scale_f16, int k,
+                           const int32_t* tokens, int m, int vocab, void* out, hipStream_t stream);
+hipError_t rope_kv_launch(void* q, const void* k, const void* v, void* kcache, void* vcache,
+                          int hq, int hkv, int d, int cap, int pos, const float* cosv,
+                          const float* sinv, hipStream_t stream);
+int attn_splits(int len, int group);
+// knew/vnew/cosv/sinv non-null: RoPE of q and of the new k row plus the K/V
+// append at position len - 1, fused into the split kernel
+hipError_t attn_decode_launch(const void* q, const void* kcache, const void* vcache, int hq,
+                              int hkv, int cap, int len, float scale, float* part, void* out,
+                              const void* knew, const void* vnew, const float* cosv,
+                              const float* sinv, hipStream_t stream);
+
 }  // namespace aexq

@@ -1,0 +1,203 @@
+"""Synthetic Qwen3.5-0.8B-shaped decode step over the aexq C ABI (benchmark config 3).
+
+Mirrors the per-token work of Qwen35DecoderSession (paths relative to the
+reference root, DEC = Packages/com.aexis/Samples/AIImageApplicationExample/
+Runtime/Scripts/Qwen35DecoderSession.cs): EmbedTokens (DEC:402-428) from the
+tied Q8 table, the decoder layers (DecodeCore, DEC:463-585), the final norm,
+and SelectNextToken's LM head + greedy argmax (DEC:734-809).  Each layer:
+
+    x  -> RMSNorm-in + q/k/v (one grouped launch)
+       -> RoPE on q, k; k/v appended to the fp16 cache; GQA decode attention
+          over the cache (one fused pass + the split combine)
+       -> o_proj + residual
+       -> RMSNorm-in + gate/up + SwiGLU-out
+       -> down + residual
+
+The model is random-init with the benchmark's shapes: hidden 1024, 16 query
+heads of 128, 4 key/value heads (k/v_proj 1024 -> 512), SwiGLU 3584, 24
+layers, Q4 offset-8 linears with fp16 scales per 32, RMSNorm eps 1e-6 with
+weights 1 + N(0, 0.02), RoPE base 1e6, a Q8 per-row LM head 1024 -> 151936
+with fp16 scales (also the embedding), and an fp16 KV cache filled with N(0, 1).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import aexq, synth
+
+
+@dataclass
+class ModelConfig:
+    layers: int = 24
+    hidden: int = 1024
+    heads_q: int = 16
+    heads_kv: int = 4
+    head_dim: int = 128
+    intermediate: int = 3584
+    vocab: int = synth.VOCAB
+    rope_base: float = 1e6
+    eps: float = 1e-6
+    capacity: int = 2048     # KV cache positions
+    group: int = 32          # Q4 scale group
+    seed: int = synth.SEED_BASE + 3
+
+    @property
+    def q_width(self):
+        return self.heads_q * self.head_dim
+
+    @property
+    def kv_width(self):
+        return self.heads_kv * self.head_dim
+
+    def linears(self):
+        h, i = self.hidden, self.intermediate
+        return (("q_proj", self.q_width, h), ("k_proj", self.kv_width, h),
+                ("v_proj", self.kv_width, h), ("o_proj", h, self.q_width),
+                ("gate_proj", i, h), ("up_proj", i, h), ("down_proj", h, i))
+
+    def bytes_per_token(self, length: int) -> dict:
+        """Algorithmic HBM bytes of one decode step attending over `length`
+        positions: every weight code and scale once, each cached K and V row
+        once, and the activations each launch reads and writes."""
+        weights = sum(n * k // 2 + n * (k // self.group) * 2 for _, n, k in self.linears())
+        kv_read = 2 * self.heads_kv * length * self.head_dim * 2
+        h, qw, kw, i = self.hidden, self.q_width, self.kv_width, self.intermediate
+        act = 2 * (h + qw + 2 * kw          # q/k/v: x in, q/k/v out
+                   + qw + 2 * kw + qw + 2 * kw  # RoPE: q in/out, k/v in, k/v appended
+                   + qw + qw                # attention: q in, out
+                   + qw + 2 * h             # o_proj: attention in, residual in, x out
+                   + h + i                  # gate/up: x in, h out
+                   + i + 2 * h)             # down: h in, residual in, x out
+        lm = self.vocab * self.hidden + self.vocab * 2
+        total = self.layers * (weights + kv_read + act) + lm + 2 * h * 3 + 4
+        return {"linear_weights": self.layers * weights, "kv_read": self.layers * kv_read,
+                "activations": self.layers * act + 2 * h * 3 + 4, "lm_head": lm, "total": total}
+
+
+def host_weights(cfg: ModelConfig, layer: int):
+    """Seeded numpy weights of one layer: {name: (words, scales, codes)} and the two norms."""
+    out = {}
+    for i, (name, n, k) in enumerate(cfg.linears()):
+        out[name] = synth.q4_weights(n, k, cfg.seed + 97 * layer + i, group=cfg.group,
+                                     code=synth.NIBBLE_OFFSET8)
+    g_attn = synth.rms_gamma(cfg.hidden, cfg.seed + 97 * layer + 50)
+    g_mlp = synth.rms_gamma(cfg.hidden, cfg.seed + 97 * layer + 51)
+    return out, g_attn, g_mlp
+
+
+def host_lm_head(cfg: ModelConfig):
+    return synth.q8_weights(cfg.vocab, cfg.hidden, cfg.seed + 7)
+
+
+def host_final_gamma(cfg: ModelConfig):
+    return synth.rms_gamma(cfg.hidden, cfg.seed + 8)
+
+
+def host_kv_cache(cfg: ModelConfig, layer: int):
+    """fp16 N(0, 1) K and V caches [heads_kv][capacity][head_dim] of one layer."""
+    g = synth.rng(cfg.seed + 1000 + layer)
+    shape = (cfg.heads_kv, cfg.capacity, cfg.head_dim)
+    return (g.standard_normal(shape).astype(np.float16), g.standard_normal(shape).astype(np.float16))
+
+
+class DecodeSession:
+    """Device state of the synthetic model and one decode step (eager or graph)."""
+
+    def __init__(self, ctx: aexq.Context, cfg: ModelConfig, device: str = "cuda"):
+        self.ctx, self.cfg, self.device = ctx, cfg, device
+        P4 = aexq.LAYOUT_PACK4_LINEAR
+        c = cfg
+        self.layers = []
+        for l in range(c.layers):
+            ws, g_attn, g_mlp = host_weights(c, l)
+            dev_w = {}
+            for name, n, k in c.linears():
+                words, scales, _ = ws[name]
+                dev_w[name] = ctx.weight(aexq.QuantizedTensor(n * k, c.group, words, scales, bits=4,
+                                                              nibble_code=synth.NIBBLE_OFFSET8), n, k)
+            kc, vc = host_kv_cache(c, l)
+            self.layers.append({
+                "w": dev_w,
+                "g_attn": torch.as_tensor(g_attn).to(device),
+                "g_mlp": torch.as_tensor(g_mlp).to(device),
+                "k_cache": torch.as_tensor(kc).to(device).reshape(-1),
+                "v_cache": torch.as_tensor(vc).to(device).reshape(-1),
+            })
+        words, scales, _ = host_lm_head(c)
+        self.lm = ctx.weight(aexq.QuantizedTensor(c.vocab * c.hidden, c.hidden, words, scales, bits=8),
+                             c.vocab, c.hidden)
+        self.g_final = torch.as_tensor(host_final_gamma(c)).to(device)
+        f16 = torch.float16
+        z = lambda n, dt=f16: torch.zeros(n, dtype=dt, device=device)
+        self.token = torch.zeros(1, dtype=torch.int32, device=device)
+        self.next_token = torch.zeros(1, dtype=torch.int32, device=device)
+        self.xa, self.xb, self.xn = z(c.hidden), z(c.hidden), z(c.hidden)
+        self.q, self.k, self.v = z(c.q_width), z(c.kv_width), z(c.kv_width)
+        self.attn = z(c.q_width)
+        self.h = z(c.intermediate)
+        self.cos = z(c.head_dim // 2, torch.float32)
+        self.sin = z(c.head_dim // 2, torch.float32)
+        d = aexq.describe
+        self.d = {
+            "xa": d(self.xa, 1, c.hidden, P4), "xb": d(self.xb, 1, c.hidden, P4),
+            "xn": d(self.xn, 1, c.hidden, P4),
+            "q": d(self.q, 1, c.q_width, P4), "k": d(self.k, 1, c.kv_width, P4),
+            "v": d(self.v, 1, c.kv_width, P4), "attn": d(self.attn, 1, c.q_width, P4),
+            "h": d(self.h, 1, c.intermediate, P4),
+        }
+        self.position = None
+        self.scale = 1.0 / math.sqrt(c.head_dim)
+
+    def set_position(self, position: int):
+        """Uploads the RoPE table of `position` (as the reference uploads its
+        per-step cos/sin textures, DEC:1585-1687)."""
+        c = self.cfg
+        j = np.arange(c.head_dim // 2, dtype=np.float64)
+        ang = position * np.power(c.rope_base, -2.0 * j / c.head_dim)
+        self.cos.copy_(torch.as_tensor(np.cos(ang).astype(np.float32)))
+        self.sin.copy_(torch.as_tensor(np.sin(ang).astype(np.float32)))
+        self.position = position
+
+    def step(self):
+        """One decode step for self.token at self.position -> self.next_token."""
+        c, ctx, d = self.cfg, self.ctx, self.d
+        pos = self.position
+        ctx.embed_q8(self.lm, self.token, self.xa)
+        for L in self.layers:
+            w = L["w"]
+            ctx.linear_group([w["q_proj"], w["k_proj"], w["v_proj"]], d["xa"],
+                             [d["q"], d["k"], d["v"]], rmsnorm=True, rms_gamma=L["g_attn"],
+                             rms_eps=c.eps)
+            ctx.attention_decode_rope(self.q, self.k, self.v, L["k_cache"], L["v_cache"],
+                                      c.heads_q, c.heads_kv, c.head_dim, c.capacity, pos + 1,
+                                      self.cos, self.sin, self.scale, self.attn)
+            ctx.linear(w["o_proj"], d["attn"], d["xb"], residual=d["xa"])
+            ctx.linear(w["gate_proj"], d["xb"], d["h"], rmsnorm=True, rms_gamma=L["g_mlp"],
+                       rms_eps=c.eps, up=w["up_proj"])
+            ctx.linear(w["down_proj"], d["h"], d["xa"], residual=d["xb"])
+        ctx.rmsnorm(d["xa"], d["xn"], self.g_final, c.eps)
+        ctx.lmhead_argmax(self.lm, d["xn"], None, self.next_token)
+
+    def capture(self, warmup: int = 2) -> torch.cuda.CUDAGraph:
+        """Captures step() into a HIP graph on a side stream (scratch buffers are
+        sized by the warm-up steps first, so nothing allocates while capturing)."""
+        stream = torch.cuda.Stream()
+        old = self.ctx.stream
+        self.ctx.set_stream(stream)
+        try:
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                for _ in range(warmup):
+                    self.step()
+            stream.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+                self.step()
+        finally:
+            self.ctx.set_stream(old)
+        torch.cuda.synchronize()
+        return g

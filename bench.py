@@ -248,6 +248,53 @@ def config4(torch, aexq, synth, ctx, copies: int = 120):
     return out
 
 
+def config3(torch, aexq, ctx, steps: int = 30):
+    """Benchmark config 3: one full synthetic Qwen3.5-0.8B-shaped decode step
+    (24 layers, 2048 cached positions, Q8 LM head with argmax), eager and as a
+    replayed HIP graph; tokens/s against the step's algorithmic bytes."""
+    from aiimage_amd import decoder
+    cfg = decoder.ModelConfig()
+    t0 = time.time()
+    sess = decoder.DecodeSession(ctx, cfg)
+    log(f"config3 model built in {time.time() - t0:.1f} s")
+    sess.token.fill_(1)
+    sess.set_position(cfg.capacity - 1)     # attends over all 2048 positions
+    for _ in range(2):
+        sess.step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        sess.step()
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / steps
+    g = sess.capture()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    graph_ms = e0.elapsed_time(e1) / steps
+    b = cfg.bytes_per_token(cfg.capacity)
+    roof = HBM_PEAK_GBS * 1e9 / b["total"]
+    out = {"config3_decode": {
+        "tokens_per_s_graph": round(1000.0 / graph_ms, 1), "ms_per_token_graph": round(graph_ms, 4),
+        "tokens_per_s_eager": round(1000.0 / eager_ms, 1), "ms_per_token_eager": round(eager_ms, 4),
+        "bytes_per_token": b, "roofline_tokens_per_s": round(roof, 1),
+        "frac_of_roofline": round(1000.0 / graph_ms / roof, 4),
+        "GBps_graph": round(b["total"] / (graph_ms * 1e-3) / 1e9, 1),
+        "kv_heads": cfg.heads_kv, "positions": cfg.capacity, "layers": cfg.layers,
+        "launches_per_token": 1 + cfg.layers * 6 + 3}}
+    log(f"config3: {out['config3_decode']}")
+    del g, sess
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(seconds: float):
     """RunGemmCpu (GS:13328-13381) restated in C, timed on this host: the seven
     linears of one layer on dequantized fp32 weights (dequant untimed, as at
@@ -354,6 +401,7 @@ def main():
         torch.cuda.empty_cache()
         log("extras: config 1 and config 5")
         result["extra"] = extras(torch, aexq, synth, ctx)
+        result["extra"].update(config3(torch, aexq, ctx))
         result["extra"].update(config4(torch, aexq, synth, ctx))
     if not args.no_cpu:
         log("cpu baseline")

@@ -204,6 +204,52 @@ aexq_status aexq_argmax(aexq_ctx* ctx, const aexq_tensor* logits, int32_t* argma
  * image of MM:707-734 AexisGemm2DReadB for every flat index). */
 aexq_status aexq_dequant(aexq_ctx* ctx, const aexq_weight* w, float* out);
 
+/* ---- decode-step operators around the linears --------------------------- */
+
+/* RMSNorm of each row of x (AexisRMSNormLayer, RMS:24-46; kernel CC:4531-4557):
+ * y = fp16(x * rsqrt(max(mean(x^2) + eps, 1e-20)) * gamma[min(i, gamma_size-1)]).
+ * x fp16/fp32 in any supported layout; y fp16 with rows of exactly K elements
+ * (LINEAR, or PACK4_LINEAR with K % 4 == 0).  gamma (device fp32) may be NULL. */
+aexq_status aexq_rmsnorm(aexq_ctx* ctx, const aexq_tensor* x, const aexq_tensor* y,
+                         const float* gamma, int gamma_size, float eps);
+
+/* Token embedding rows from a Q8 per-row table (the tied embedding / LM head,
+ * Qwen35SharedTokenEmbeddingWeights.cs:185-198; BT:13-26): out[m][k] =
+ * fp16(q[tokens[m]][k] * scale[tokens[m]]).  tokens: device int32[m], clamped
+ * to the vocabulary; out: device fp16 [m][K]. */
+aexq_status aexq_embed_q8(aexq_ctx* ctx, const aexq_weight* table, const int32_t* tokens, int m,
+                          void* out);
+
+/* RoPE of one decode position (rotate-half pairs (j, j + d/2), the
+ * non-interleaved branch of AexisRotaryEmbedPack4_Impl, PN:414-473) applied in
+ * place to q [heads_q][d] and to k [heads_kv][d], which is written to
+ * k_cache[g][position][:]; v is appended to v_cache the same way.  cos_table /
+ * sin_table are device fp32 [d/2] for this position (the reference uploads the
+ * same tables per step, DEC:1585-1687).  All tensors fp16, rows contiguous. */
+aexq_status aexq_rope_kv_append(aexq_ctx* ctx, void* q, const void* k, const void* v,
+                                void* k_cache, void* v_cache, int heads_q, int heads_kv,
+                                int head_dim, int capacity, int position,
+                                const float* cos_table, const float* sin_table);
+
+/* Decode attention of one query row over the first `length` cached positions
+ * (AexisSdpaAttentionPack4CDHW_Impl, MM:420-544): scores q.k * scale, softmax
+ * with the maximum subtracted and the sum floored at 1e-20, output sum p * v;
+ * query head h reads key/value head h / (heads_q / heads_kv).  q [heads_q][d],
+ * caches [heads_kv][capacity][d], out [heads_q][d]; fp16; d == 128. */
+aexq_status aexq_attention_decode(aexq_ctx* ctx, const void* q, const void* k_cache,
+                                  const void* v_cache, int heads_q, int heads_kv, int head_dim,
+                                  int capacity, int length, float scale, void* out);
+
+/* aexq_rope_kv_append at position length - 1 followed by aexq_attention_decode
+ * over `length` positions, in one pass: q and the new k row are rotated (and
+ * rounded to fp16) inside the attention kernel, the k/v rows are appended to
+ * the caches there, and q itself is left unrotated. */
+aexq_status aexq_attention_decode_rope(aexq_ctx* ctx, const void* q, const void* k, const void* v,
+                                       void* k_cache, void* v_cache, int heads_q, int heads_kv,
+                                       int head_dim, int capacity, int length,
+                                       const float* cos_table, const float* sin_table,
+                                       float scale, void* out);
+
 #ifdef __cplusplus
 }
 #endif

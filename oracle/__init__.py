@@ -71,6 +71,9 @@ def _declare(L):
         "orc_swish": (f32, [f32]),
         "orc_swiglu": (None, [P, P, i32, P]),
         "orc_argmax_rows": (None, [P, i32, i32, i64, P]),
+        "orc_rope_table": (None, [i32, i32, ctypes.c_double, P, P]),
+        "orc_rope_rotate_half": (None, [P, i32, i32, P, P, P]),
+        "orc_sdpa_decode": (None, [P, P, P, i32, i32, i32, i32, f32, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -296,4 +299,36 @@ def argmax_rows(logits, width: int | None = None):
     w = stride if width is None else width
     out = np.empty(rows, np.int32)
     lib().orc_argmax_rows(_p(x), rows, w, stride, _p(out))
+    return out
+
+
+# ---- decode step around the linears -----------------------------------------
+
+def rope_table(position: int, head_dim: int, base: float):
+    """(cos, sin) float32 [head_dim/2] of one position (rotate-half layout)."""
+    c = np.empty(head_dim // 2, np.float32)
+    s = np.empty(head_dim // 2, np.float32)
+    lib().orc_rope_table(position, head_dim, base, _p(c), _p(s))
+    return c, s
+
+
+def rope_rotate_half(x, cos_t, sin_t):
+    """x [heads][head_dim] rotated per PN:414-473 (non-interleaved)."""
+    x = _c(x, np.float32)
+    heads, d = x.shape
+    out = np.empty_like(x)
+    lib().orc_rope_rotate_half(_p(x), heads, d, _p(_c(cos_t, np.float32)), _p(_c(sin_t, np.float32)),
+                               _p(out))
+    return out
+
+
+def sdpa_decode(q, k, v, scale: float):
+    """One query row: q [hq][d], k/v [hkv][length][d] -> float64 [hq][d] (MM:420-544)."""
+    q = _c(q, np.float32)
+    k = _c(k, np.float32)
+    v = _c(v, np.float32)
+    hq, d = q.shape
+    hkv, length, _ = k.shape
+    out = np.empty((hq, d), np.float64)
+    lib().orc_sdpa_decode(_p(q), _p(k), _p(v), hq, hkv, d, length, scale, _p(out))
     return out

@@ -656,3 +656,81 @@ void orc_argmax_rows(const float* logits, int rows, int width, int64_t row_strid
     out_index[r] = best_index;
   }
 }
+
+/* ---------------------------------------------------------------------- */
+/* decode step around the linears                                          */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * RoPE table of one position for the rotate-half layout: angle_j =
+ * position * base^(-2j/d), j < d/2, evaluated in float64 and rounded to
+ * float32 (the reference uploads per-position cos/sin tables of the same
+ * [position][d/2] shape, DEC:1585-1687, and PN:414-473 indexes them by j).
+ */
+void orc_rope_table(int position, int head_dim, double base, float* cos_out, float* sin_out) {
+  int half = head_dim / 2;
+  for (int j = 0; j < half; ++j) {
+    double inv = pow(base, -2.0 * (double)j / (double)head_dim);
+    double a = (double)position * inv;
+    cos_out[j] = (float)cos(a);
+    sin_out[j] = (float)sin(a);
+  }
+}
+
+/*
+ * PN:414-473 AexisRotaryEmbedPack4_Impl, non-interleaved branch: for pair
+ * (j, j + half): first = x0*cos - x1*sin, second = x0*sin + x1*cos, with the
+ * table entry j of the position.  x and out are [heads][head_dim].
+ */
+void orc_rope_rotate_half(const float* x, int heads, int head_dim, const float* cos_t,
+                          const float* sin_t, float* out) {
+  int half = head_dim / 2;
+  for (int h = 0; h < heads; ++h) {
+    const float* r = x + (size_t)h * head_dim;
+    float* o = out + (size_t)h * head_dim;
+    for (int j = 0; j < half; ++j) {
+      float x0 = r[j], x1 = r[j + half];
+      o[j] = x0 * cos_t[j] - x1 * sin_t[j];
+      o[j + half] = x0 * sin_t[j] + x1 * cos_t[j];
+    }
+  }
+}
+
+/*
+ * MM:420-544 AexisSdpaAttentionPack4CDHW_Impl for one query row: query head h
+ * reads key head h / (heads_q / heads_kv); s_j = (q . k_j) * scale; the
+ * softmax subtracts the maximum and divides by max(sum, 1e-20); out = sum_j
+ * p_j v_j.  Evaluated in float64.  q [heads_q][d], k/v [heads_kv][length][d].
+ */
+void orc_sdpa_decode(const float* q, const float* k, const float* v, int heads_q, int heads_kv,
+                     int head_dim, int length, float scale, double* out) {
+  int group = heads_q / heads_kv;
+  if (group < 1) group = 1;
+  double* s = (double*)malloc(sizeof(double) * (size_t)(length > 0 ? length : 1));
+  for (int h = 0; h < heads_q; ++h) {
+    int g = h / group;
+    if (g > heads_kv - 1) g = heads_kv - 1;
+    const float* qh = q + (size_t)h * head_dim;
+    double mx = -1.0e300;
+    for (int j = 0; j < length; ++j) {
+      const float* kj = k + ((size_t)g * length + j) * head_dim;
+      double acc = 0.0;
+      for (int i = 0; i < head_dim; ++i) acc += (double)qh[i] * (double)kj[i];
+      s[j] = acc * (double)scale;
+      if (s[j] > mx) mx = s[j];
+    }
+    double sum = 0.0;
+    for (int j = 0; j < length; ++j) {
+      s[j] = exp(s[j] - mx);
+      sum += s[j];
+    }
+    double inv = 1.0 / (sum > 1e-20 ? sum : 1e-20);
+    for (int i = 0; i < head_dim; ++i) {
+      double acc = 0.0;
+      for (int j = 0; j < length; ++j)
+        acc += s[j] * inv * (double)v[((size_t)g * length + j) * head_dim + i];
+      out[(size_t)h * head_dim + i] = acc;
+    }
+  }
+  free(s);
+}

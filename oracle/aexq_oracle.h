@@ -13,6 +13,7 @@
  *   CC  = Packages/com.aexis/Runtime/Resources/Aexis/AexisCommon.compute
  *   SP  = Packages/com.aexis/Runtime/Resources/Aexis/Includes/KernelGroups/AexisKernels.Pack4Spatial.hlsl
  *   DEC = Packages/com.aexis/Samples/AIImageApplicationExample/Runtime/Scripts/Qwen35DecoderSession.cs
+ *   PN  = Packages/com.aexis/Runtime/Resources/Aexis/Includes/KernelGroups/AexisKernels.Pack4PointwiseNorm.hlsl
  */
 #ifndef AEXQ_ORACLE_H
 #define AEXQ_ORACLE_H
@@ -90,6 +91,13 @@ void orc_swiglu(const float* gate, const float* up, int n, float* out);
 /* ---- LM head argmax ---------------------------------------------------- */
 void orc_argmax_rows(const float* logits, int rows, int width, int64_t row_stride,
                      int32_t* out_index);
+
+/* ---- decode step around the linears ------------------------------------ */
+void orc_rope_table(int position, int head_dim, double base, float* cos_out, float* sin_out);
+void orc_rope_rotate_half(const float* x, int heads, int head_dim, const float* cos_t,
+                          const float* sin_t, float* out);
+void orc_sdpa_decode(const float* q, const float* k, const float* v, int heads_q, int heads_kv,
+                     int head_dim, int length, float scale, double* out);
 
 #ifdef __cplusplus
 }

@@ -419,3 +419,65 @@ def test_q4_from_q8_rows_group16(orc):
     assert np.all(np.abs(q4 - q8f) <= step * 0.5 + 1e-6)
     with pytest.raises(ValueError):
         orc.record_write_q4_from_q8_rows(q8, s8, rows, width, 24)
+
+
+# ---------------------------------------------------------------- decode-step oracle functions
+
+def test_rope_table_and_rotation_properties(orc):
+    """Rotate-half RoPE (PN:414-473): position 0 is the identity, every (j, j+d/2)
+    pair keeps its norm, and <rope(q, a), rope(k, b)> depends only on a - b."""
+    d = 128
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, d)).astype(np.float32)
+    c0, s0 = orc.rope_table(0, d, 1e6)
+    assert np.array_equal(c0, np.ones(d // 2, np.float32)) and np.array_equal(s0, np.zeros(d // 2, np.float32))
+    assert np.array_equal(orc.rope_rotate_half(x, c0, s0), x)
+    c, s = orc.rope_table(1234, d, 1e6)
+    y = orc.rope_rotate_half(x, c, s)
+    half = d // 2
+    np.testing.assert_allclose(x[:, :half] ** 2 + x[:, half:] ** 2, y[:, :half] ** 2 + y[:, half:] ** 2,
+                               rtol=1e-5)
+    # frequency of pair j is base^(-2j/d): pair 0 turns by exactly `position` radians
+    assert abs(float(c[0]) - np.cos(1234.0)) < 1e-6 and abs(float(s[0]) - np.sin(1234.0)) < 1e-6
+    q, k = x[0:1], x[1:2]
+
+    def dot_at(a, b):
+        ca, sa = orc.rope_table(a, d, 1e6)
+        cb, sb = orc.rope_table(b, d, 1e6)
+        return float(np.dot(orc.rope_rotate_half(q, ca, sa)[0].astype(np.float64),
+                            orc.rope_rotate_half(k, cb, sb)[0].astype(np.float64)))
+    assert abs(dot_at(10, 3) - dot_at(107, 100)) < 1e-3 * abs(dot_at(10, 3)) + 1e-3
+
+
+def test_sdpa_decode_properties(orc):
+    """SDPA (MM:420-544) without retyping it: equal keys give the mean of the
+    values, one position gives its value row, a dominant score selects its row,
+    adding a constant to every score changes nothing, and query heads of one
+    key group with equal queries give equal outputs."""
+    rng = np.random.default_rng(6)
+    d, L = 8, 5
+    v = rng.standard_normal((1, L, d)).astype(np.float32)
+    q = rng.standard_normal((2, d)).astype(np.float32)
+    k_eq = np.repeat(rng.standard_normal((1, 1, d)).astype(np.float32), L, axis=1)
+    out = orc.sdpa_decode(q, k_eq, v, 0.7)
+    np.testing.assert_allclose(out, np.repeat(v[0].mean(0, keepdims=True), 2, 0), rtol=1e-6, atol=1e-7)
+    out1 = orc.sdpa_decode(q, k_eq[:, :1], v[:, :1], 0.7)
+    np.testing.assert_allclose(out1, np.repeat(v[0, :1], 2, 0), rtol=1e-6)
+    k = rng.standard_normal((1, L, d)).astype(np.float32) * 0.01
+    k[0, 3] = q[0] * 50.0
+    sel = orc.sdpa_decode(q[:1], k, v, 1.0)
+    np.testing.assert_allclose(sel[0], v[0, 3], rtol=1e-6, atol=1e-6)
+    # shift: a key offset orthogonal... use a constant direction e with q.e = c for every key
+    e = np.zeros(d, np.float32); e[0] = 1.0
+    qq = np.zeros((1, d), np.float32); qq[0, 0] = 2.0; qq[0, 1:] = rng.standard_normal(d - 1)
+    kk = rng.standard_normal((1, L, d)).astype(np.float32); kk[0, :, 0] = 0.0
+    a = orc.sdpa_decode(qq, kk, v, 0.5)
+    b = orc.sdpa_decode(qq, kk + 3.0 * e, v, 0.5)       # every score + 0.5 * 2 * 3
+    np.testing.assert_allclose(a, b, rtol=1e-9)
+    # GQA: heads 0..3 share key head 0, heads 4..7 key head 1
+    q8 = np.repeat(rng.standard_normal((1, d)).astype(np.float32), 8, 0)
+    k2 = rng.standard_normal((2, L, d)).astype(np.float32)
+    v2 = rng.standard_normal((2, L, d)).astype(np.float32)
+    o = orc.sdpa_decode(q8, k2, v2, 0.3)
+    assert np.all(o[:4] == o[0]) and np.all(o[4:] == o[4]) and not np.allclose(o[0], o[4])
+    np.testing.assert_allclose(o[0], orc.sdpa_decode(q8[:1], k2[:1], v2[:1], 0.3)[0], rtol=1e-12)
