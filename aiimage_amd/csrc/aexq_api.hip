@@ -889,7 +889,7 @@ extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
   HIP_TRY(op, hipSetDevice(ctx->device));
   const int M = plan.p.m;
   if (plan.fast && plan.entry->cfg.argmax) {
-    const int parts = plan.grid * kWaves;  // one partial per wave
+    const int parts = plan.grid;  // one partial per workgroup
     st = ensure_parts(ctx, (long long)parts * M, op);
     if (st) return st;
     plan.p.part_best = ctx->part_best;

@@ -188,9 +188,25 @@ __global__ __launch_bounds__(kThreads) void argmax_finalize_kernel(const ArgmaxP
   float bv = __builtin_nanf("");
   int bix = 0x7fffffff;
   float bs = -INFINITY;
-  for (int i = threadIdx.x; i < a.parts; i += kThreads) {
-    const long long o = (long long)m * a.parts + i;
-    argmax_merge(bv, bix, bs, a.pv[o], a.pi[o], a.ps[o]);
+  // kFinalizeBatch partials per thread per pass, all loads issued before the
+  // first merge (the merge order is free: it is a total order plus a max)
+  constexpr int kFinalizeBatch = 8;
+  const float* pv = a.pv + (long long)m * a.parts;
+  const int* pi = a.pi + (long long)m * a.parts;
+  const float* ps = a.ps + (long long)m * a.parts;
+  for (int i0 = threadIdx.x; i0 < a.parts; i0 += kThreads * kFinalizeBatch) {
+    float v[kFinalizeBatch], s[kFinalizeBatch];
+    int ix[kFinalizeBatch];
+#pragma unroll
+    for (int j = 0; j < kFinalizeBatch; ++j) {
+      const int i = i0 + j * kThreads;
+      const bool in = i < a.parts;
+      v[j] = in ? pv[i] : __builtin_nanf("");
+      ix[j] = in ? pi[i] : 0x7fffffff;
+      s[j] = in ? ps[i] : -INFINITY;
+    }
+#pragma unroll
+    for (int j = 0; j < kFinalizeBatch; ++j) argmax_merge(bv, bix, bs, v[j], ix[j], s[j]);
   }
   argmax_wave_reduce(bv, bix, bs);
   __shared__ float sv[kWaves], ss[kWaves];

@@ -29,6 +29,12 @@ struct Qmv {
   static constexpr int XW = FMT == kQ8 ? 8 : 16;         // activation dwords per code chunk
   static constexpr int NW = PAIR ? 2 : 1;                // gate (+ up) weights
   static constexpr int NS = FMT == kQ8 ? 1 : (GM == kG16 ? 2 * CPL : CPL);  // scales per row
+  // vector memory reads of one tile: residual (M = 1), codes, scales
+  static constexpr int kLoadsPerTile = (MMAX == 1 ? U : 0) + NW * U * (CPL + NS);
+#ifndef QMV_VALU_PER_LOAD
+#define QMV_VALU_PER_LOAD 8
+#endif
+  static constexpr int kValuPerLoad = QMV_VALU_PER_LOAD;
 
   struct Cursor {
     int j, b, rt;  // matrix, batch entry, row tile (wave-uniform)
@@ -37,6 +43,7 @@ struct Qmv {
   struct Buf {
     u32x4 w[NW][U][CPL];
     uint32_t s[NW][U][NS];  // raw scale bits, widened when consumed (keeps loads in flight)
+    uint32_t r[U];          // M = 1: the rows' fp16 residual bits, loaded with the tile
   };
 
   typedef uint32_t XRegs[MMAX][CPL][XW];
@@ -64,11 +71,12 @@ struct Qmv {
     return c;
   }
 
-  // Lane-constant byte offsets of a tile's code chunks and scales, relative to
-  // the tile's first row.
+  // Lane-constant byte offsets of the code chunks and scales of a tile's
+  // first row group (u = 0), relative to the tile's first row; row group u
+  // adds the wave-uniform u_code_bytes(u) / u_scale_bytes(u).
   struct Offsets {
-    int w[U][CPL];
-    int s[U][NS];
+    int w[CPL];
+    int s[NS];
   };
   // byte offset beyond any resource (weight copies are < 2 GiB)
   static constexpr int kNoChunk = 0x7ffffff0;
@@ -78,31 +86,37 @@ struct Qmv {
     const int row_bytes = p.chunks * 16;
     const int sb = (p.flags & kFlagScaleF16) ? 2 : 4;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int rr = u * SLOTS + slot;
+    for (int c = 0; c < CPL; ++c) {
+      // a chunk past K points beyond every resource (also after adding a row
+      // group's u_code_bytes): it reads 0 with no traffic
+      const int ci = sub + c * LPR;
+      o.w[c] = ci < p.chunks ? slot * row_bytes + ci * 16 : kNoChunk;
+    }
+    if constexpr (FMT == kQ8) {
+      o.s[0] = slot * sb;
+    } else {
 #pragma unroll
       for (int c = 0; c < CPL; ++c) {
-        // a chunk past K points beyond every resource: it reads 0 with no traffic
         const int ci = sub + c * LPR;
-        o.w[u][c] = ci < p.chunks ? rr * row_bytes + ci * 16 : kNoChunk;
-      }
-      if constexpr (FMT == kQ8) {
-        o.s[u][0] = rr * sb;
-      } else {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          const int ci = sub + c * LPR;
-          const int g0 = rr * p.groups_per_row;
-          if constexpr (GM == kG16) {
-            o.s[u][2 * c] = (g0 + 2 * ci) * sb;
-            o.s[u][2 * c + 1] = (g0 + 2 * ci + 1) * sb;
-          } else {
-            o.s[u][c] = (g0 + (ci * 32) / p.group) * sb;
-          }
+        const int g0 = slot * p.groups_per_row;
+        if constexpr (GM == kG16) {
+          o.s[2 * c] = (g0 + 2 * ci) * sb;
+          o.s[2 * c + 1] = (g0 + 2 * ci + 1) * sb;
+        } else {
+          o.s[c] = (g0 + (ci * 32) / p.group) * sb;
         }
       }
     }
     return o;
+  }
+
+  static __device__ __forceinline__ int u_code_bytes(const QmvParams& p, int u) {
+    return u * SLOTS * p.chunks * 16;
+  }
+  static __device__ __forceinline__ int u_scale_bytes(const QmvParams& p, int u) {
+    const int sb = (p.flags & kFlagScaleF16) ? 2 : 4;
+    const int sper = FMT == kQ8 ? 1 : p.groups_per_row;
+    return u * SLOTS * sper * sb;
   }
 
   // Byte offset of a tile's first scale inside its weight copy's scale array.
@@ -118,17 +132,32 @@ struct Qmv {
   // (and are never stored / meet zero activations).  Scales:
   // the aligned dword holding each scale, from a resource over the copy's
   // whole (256-byte aligned, dword-padded) scale array, widened when consumed.
+  // `live` false issues the same loads against empty resources (the prefetch
+  // after a wave's last tile): they read 0 without memory traffic.
   static __device__ __forceinline__ void load(const QmvParams& p, const Cursor& cu,
-                                              const Offsets& o, Buf& buf) {
+                                              const Offsets& o, Buf& buf, bool live,
+                                              int slot) {
     const QmvMat& mt = p.mat[cu.j];
     const int sb = (p.flags & kFlagScaleF16) ? 2 : 4;
     const long long row_bytes = (long long)p.chunks * 16;
     const int r0 = cu.rt * RW;
     // rows of the matrix at or after the tile's first row; a tile inside the
     // Pack4 padding rows (r0 >= n) gets an empty resource: every load reads 0
-    const int rows = mt.n > r0 ? mt.n - r0 : 0;
+    const int rows = live && mt.n > r0 ? mt.n - r0 : 0;
     const int sper = FMT == kQ8 ? 1 : p.groups_per_row;
-    const int sbytes = (mt.n * sper * sb + 3) & ~3;
+    const int sbytes = live ? (mt.n * sper * sb + 3) & ~3 : 0;
+    if constexpr (MMAX == 1) {
+      // fp16 residual rows of the tile, loaded with it (an empty resource
+      // without one); fp32 outputs read theirs in the epilogue
+      const bool res = mt.res && (p.flags & kFlagResidual) && !(p.flags & kFlagYf32);
+      const char* rb =
+          res ? (const char*)mt.res + (cu.b * mt.r_bstride + r0) * 2 : (const char*)mt.w;
+      const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)rb, (short)0, res ? rows * 2 : 0, kBufferRsrcWord3);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        buf.r[u] = __builtin_amdgcn_raw_buffer_load_b16(rr, (u * SLOTS + slot) * 2, 0, 0);
+    }
     const int toff = scale_tile_offset(p, cu);
 #pragma unroll
     for (int h = 0; h < NW; ++h) {
@@ -145,43 +174,34 @@ struct Qmv {
 #pragma unroll
         for (int c = 0; c < CPL; ++c)
           buf.w[h][u][c] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o.w[u][c], 0, kStreamAux));
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o.w[c], u_code_bytes(p, u),
+                                                           kStreamAux));
 #pragma unroll
         for (int i = 0; i < NS; ++i)
-          buf.s[h][u][i] =
-              __builtin_amdgcn_raw_buffer_load_b32(sr, (toff + o.s[u][i]) & ~3, 0, 0);
+          buf.s[h][u][i] = __builtin_amdgcn_raw_buffer_load_b32(
+              sr, (toff + u_scale_bytes(p, u) + o.s[i]) & ~3, 0, 0);
       }
     }
   }
 
-  // Activation rows of one batch entry into registers (RMS-normalised when the
-  // RMSNorm-in epilogue is on: every wave reduces sum(x^2) itself, which keeps
-  // the stream free of workgroup barriers).
-  static __device__ __forceinline__ void load_x(const QmvParams& p, const f16* xb, int lane,
-                                                int sub, XRegs& xr) {
+  // Activation rows of one batch entry into registers.  With the RMSNorm-in
+  // epilogue the registers hold fp16(x * gamma) and xinv[m] = rsqrt(mean x^2 +
+  // eps), which the epilogue applies to the row's dot product (exact algebra:
+  // the norm is a scalar per activation row).  sum(x^2) comes from the same
+  // registers -- the LPR lanes of a slot hold the whole row -- so x, gamma and
+  // the weight codes are all in flight at once and no wave waits on another
+  // (x * gamma must be fp16-representable, as the normalised row is).
+  static __device__ __forceinline__ void load_x(const QmvParams& p, const f16* xb, int sub,
+                                                XRegs& xr, float (&xinv)[MMAX]) {
     const bool rms = (p.flags & kFlagRms) != 0;
     const __amdgpu_buffer_rsrc_t grsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void*)p.gamma, (short)0, p.gamma ? p.k * 4 : 0, kBufferRsrcWord3);
 #pragma unroll
     for (int m = 0; m < MMAX; ++m) {
+      xinv[m] = 1.0f;
       if (m < p.m) {
         const f16* row = xb + (long long)m * p.x_rstride;
-        float inv = 1.0f;
-        if (rms) {
-          float ss = 0.0f;
-          for (int kk = lane * 8; kk < p.k; kk += 512) {
-            const u32x4 t = *(const u32x4*)(row + kk);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const f16x2 h = as_h2(t[i]);
-              const float a = (float)h[0], b = (float)h[1];
-              ss = fmaf(a, a, ss);
-              ss = fmaf(b, b, ss);
-            }
-          }
-          ss = wave_sum(ss);
-          inv = rsqrtf(fmaxf(ss / (float)p.k + p.eps, 1e-20f));
-        }
+        float ss = 0.0f;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
           const int ci = sub + c * LPR;
@@ -215,8 +235,10 @@ struct Qmv {
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                   const f16x2 h = as_h2(raw[d + e]);
-                  const f16x2 o = {(f16)((float)h[0] * inv * g[2 * e]),
-                                   (f16)((float)h[1] * inv * g[2 * e + 1])};
+                  const float a = (float)h[0], b = (float)h[1];
+                  ss = fmaf(a, a, ss);
+                  ss = fmaf(b, b, ss);
+                  const f16x2 o = {(f16)(a * g[2 * e]), (f16)(b * g[2 * e + 1])};
                   raw[d + e] = as_u(o);
                 }
               }
@@ -235,6 +257,7 @@ struct Qmv {
                         &xr[m][c][4 * d]);
           }
         }
+        if (rms) xinv[m] = rsqrtf(fmaxf(group_sum<LPR>(ss) / (float)p.k + p.eps, 1e-20f));
       } else {
 #pragma unroll
         for (int c = 0; c < CPL; ++c)
@@ -247,8 +270,9 @@ struct Qmv {
   // Dot products, row reduction, epilogue and store of one tile.
   static __device__ __forceinline__ void compute(const QmvParams& p, const Cursor& cu,
                                                  const Offsets& o, const Buf& buf,
-                                                 const XRegs& xr, int sub,
-                                                 int slot, float (&bv)[MMAX], int (&bi)[MMAX],
+                                                 const XRegs& xr, const float (&xinv)[MMAX],
+                                                 int sub, int slot, float (&bv)[MMAX],
+                                                 int (&bi)[MMAX],
                                                  float (&bs)[MMAX]) {
     const QmvMat& mt = p.mat[cu.j];
     const bool scl16 = (p.flags & kFlagScaleF16) != 0;
@@ -303,11 +327,21 @@ struct Qmv {
             for (int g = 0; g < SPC; ++g)
 #pragma unroll
               for (int m = 0; m < MMAX; ++m)
-                acc[h][u][m] = fmaf(part[g][m], scale_at(buf.s[h][u][c * SPC + g],
-                                                          toff + o.s[u][c * SPC + g], scl16),
+                acc[h][u][m] = fmaf(part[g][m],
+                                    scale_at(buf.s[h][u][c * SPC + g],
+                                             toff + u_scale_bytes(p, u) + o.s[c * SPC + g], scl16),
                                     acc[h][u][m]);
           }
         }
+
+    // The next tile's loads, issued just before this call, go out one at a
+    // time between groups of these dot products: a burst of them would hold
+    // the wave at the memory-instruction queue while its VALU work waits.
+#pragma unroll
+    for (int i = 0; i < kLoadsPerTile; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one VMEM read
+      __builtin_amdgcn_sched_group_barrier(0x002, kValuPerLoad, 0);
+    }
 
 #pragma unroll
     for (int h = 0; h < NW; ++h)
@@ -316,8 +350,9 @@ struct Qmv {
 #pragma unroll
         for (int m = 0; m < MMAX; ++m) {
           float v = group_sum<LPR>(acc[h][u][m]);
-          if constexpr (FMT == kQ8) v *= scale_at(buf.s[h][u][0], toff + o.s[u][0], scl16);
-          acc[h][u][m] = v;
+          if constexpr (FMT == kQ8)
+            v *= scale_at(buf.s[h][u][0], toff + u_scale_bytes(p, u) + o.s[0], scl16);
+          acc[h][u][m] = v * xinv[m];
         }
 
     const bool yf32 = (p.flags & kFlagYf32) != 0;
@@ -335,8 +370,12 @@ struct Qmv {
           v = gemm_epilogue(p, m, r, acc[0][u][m]);
           if constexpr (PAIR) v = silu(v) * gemm_epilogue(p, m, r, acc[1][u][m]);
           if (rb && (p.flags & kFlagResidual)) {
-            const long long ri = (long long)m * p.r_rstride + r;
-            v += yf32 ? ((const float*)rb)[ri] : (float)((const f16*)rb)[ri];
+            if (MMAX == 1 && !yf32) {
+              v += (float)as_h2(buf.r[u])[0];
+            } else {
+              const long long ri = (long long)m * p.r_rstride + r;
+              v += yf32 ? ((const float*)rb)[ri] : (float)((const f16*)rb)[ri];
+            }
           }
         }
         // one lane per row stores; the lanes of a slot hold identical values
@@ -355,9 +394,17 @@ struct Qmv {
   }
 };
 
+// Resident waves per SIMD the register budget is sized for: 4 (128 VGPRs)
+// for the lean M = 1 shapes, fewer where the tile's registers need more.
+template <int FMT, int CPL, int MMAX, bool PAIR, int GM>
+constexpr int qmv_waves_per_eu() {
+  if (MMAX > 1 || (FMT == kQ4 && CPL >= 4) || (PAIR && CPL >= 4)) return 2;
+  return FMT == kQ4 && GM == kG16 ? 3 : 4;
+}
+
 template <int FMT, int LPR, int CPL, int U, int MMAX, bool PAIR, bool ARGMAX, int GM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(MMAX > 1 || (FMT == kQ4 && CPL >= 4) ? 2 : (FMT == kQ4 && GM == kG16 ? 3 : 4))))
+__attribute__((amdgpu_waves_per_eu(qmv_waves_per_eu<FMT, CPL, MMAX, PAIR, GM>())))
 void qmv_kernel(const QmvParams p) {
   using Q = Qmv<FMT, LPR, CPL, U, MMAX, PAIR, ARGMAX, GM>;
   const int lane = threadIdx.x & 63;
@@ -382,60 +429,75 @@ void qmv_kernel(const QmvParams p) {
     typename Q::Cursor cu = Q::locate(p, t0);
     typename Q::Buf A, B;
     typename Q::XRegs xr;
-    const f16* xcur = nullptr;
-    Q::load(p, cu, o, A);
+    float xinv[MMAX];
+    Q::load(p, cu, o, A, true, slot);
+    const f16* xcur = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
+    Q::load_x(p, xcur, sub, xr, xinv);
     int t = t0;
     while (true) {
-      // Tile t is in A.  The activation rows are (re)loaded first, then tile
-      // t+1's loads are issued into B (the last tile re-reads itself), then A
-      // is consumed while B is in flight.
-      {
-        const f16* xp = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
-        if (xp != xcur) {
-          Q::load_x(p, xp, lane, sub, xr);
-          xcur = xp;
-        }
-      }
+      // Tile t is in A and its activation rows in xr.  Tile t+1's loads are
+      // issued into B (after the last tile: the same loads against empty
+      // resources), then A is consumed while B is in flight.  Activation rows
+      // change only between batch entries of a batched x (a cold path).
       bool more = t + 1 < t1;
       typename Q::Cursor nx = more ? Q::advance(p, cu) : cu;
-      Q::load(p, nx, o, B);
-      Q::compute(p, cu, o, A, xr, sub, slot, bv, bi, bs);
+      Q::load(p, nx, o, B, more, slot);
+      Q::compute(p, cu, o, A, xr, xinv, sub, slot, bv, bi, bs);
       if (!more) break;
       ++t;
       cu = nx;
-      // tile t is in B; tile t+1 goes into A
       {
         const f16* xp = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
-        if (xp != xcur) {
-          Q::load_x(p, xp, lane, sub, xr);
+        if (__builtin_expect(xp != xcur, 0)) {
+          Q::load_x(p, xp, sub, xr, xinv);
           xcur = xp;
         }
       }
+      // tile t is in B; tile t+1 goes into A
       more = t + 1 < t1;
       nx = more ? Q::advance(p, cu) : cu;
-      Q::load(p, nx, o, A);
-      Q::compute(p, cu, o, B, xr, sub, slot, bv, bi, bs);
+      Q::load(p, nx, o, A, more, slot);
+      Q::compute(p, cu, o, B, xr, xinv, sub, slot, bv, bi, bs);
       if (!more) break;
       ++t;
       cu = nx;
+      {
+        const f16* xp = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
+        if (__builtin_expect(xp != xcur, 0)) {
+          Q::load_x(p, xp, sub, xr, xinv);
+          xcur = xp;
+        }
+      }
     }
   }
 
   if constexpr (ARGMAX) {
-    // every wave (also one without tiles) writes its partial for each row m
+    // every workgroup (also one whose waves had no tiles) writes one partial
+    // per row m: its waves' partials merged through LDS
+    __shared__ float lv[MMAX][kWaves], ls[MMAX][kWaves];
+    __shared__ int li[MMAX][kWaves];
 #pragma unroll
     for (int m = 0; m < MMAX; ++m) {
-      if (m < p.m) {
-        float v = bv[m], s = bs[m];
-        int i = bi[m];
-        argmax_wave_reduce(v, i, s);
-        if (lane == 0) {
-          const long long o = (long long)m * p.parts + gw;
-          p.part_best[o] = v;
-          p.part_index[o] = i;
-          p.part_second[o] = s;
-        }
+      float v = bv[m], s = bs[m];
+      int i = bi[m];
+      argmax_wave_reduce(v, i, s);
+      if (lane == 0) {
+        lv[m][wave] = v;
+        li[m][wave] = i;
+        ls[m][wave] = s;
       }
+    }
+    __syncthreads();
+    if (threadIdx.x < MMAX && (int)threadIdx.x < p.m) {
+      const int m = threadIdx.x;
+      float v = lv[m][0], s = ls[m][0];
+      int i = li[m][0];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) argmax_merge(v, i, s, lv[m][w], li[m][w], ls[m][w]);
+      const long long o = (long long)m * p.parts + blockIdx.x;
+      p.part_best[o] = v;
+      p.part_index[o] = i;
+      p.part_second[o] = s;
     }
   }
 }
