@@ -142,6 +142,9 @@ def _declare(L):
         "aexq_weight_q4": (i32, [P, P, P, i32, i32, i32, i32, i32, PP]),
         "aexq_weight_q8_from_f32": (i32, [P, P, i32, i32, i32, PP]),
         "aexq_weight_q4_from_f32": (i32, [P, P, i32, i32, i32, PP]),
+        "aexq_archive_header": (i32, [P, sz, ctypes.POINTER(i32), ctypes.POINTER(i32),
+                                      ctypes.POINTER(i32)]),
+        "aexq_weight_from_record": (i32, [P, i32, P, sz, i32, i32, PP, ctypes.POINTER(sz)]),
         "aexq_weight_replicate": (i32, [P, P, i32, PP]),
         "aexq_weight_alias": (i32, [P, P, PP]),
         "aexq_weight_release": (None, [P]),

@@ -198,6 +198,18 @@ class Context:
         check(fn(self.handle, d.ctypes.data, n, k, int(trans_b), ctypes.byref(h)), "weight_from_float")
         return QuantWeight(self, h)
 
+    def weight_from_record(self, record: bytes, n: int, k: int, bits: int) -> tuple:
+        """One AQSGET8 Gemm weight record into the device layout, as
+        AexisGemmLayer.LoadLayer reads and uploads it (GL:60-141).  Returns
+        (weight, bytes consumed)."""
+        buf = np.frombuffer(record, np.uint8)
+        h = ctypes.c_void_p()
+        used = ctypes.c_size_t(0)
+        check(self._lib.aexq_weight_from_record(self.handle, bits, buf.ctypes.data, buf.size, n, k,
+                                                ctypes.byref(h), ctypes.byref(used)),
+              "weight_from_record")
+        return QuantWeight(self, h), used.value
+
     # ---- execution
     def linear(self, w: "QuantWeight", x: _abi.Tensor, y: _abi.Tensor, *, alpha: float = 1.0,
                beta: float = 1.0, c: Optional[torch.Tensor] = None, broadcast_c: int = -1,
@@ -292,6 +304,17 @@ class Context:
         check(self._lib.aexq_dequant(self.handle, w.handle, ctypes.c_void_p(out.data_ptr())),
               "aexq_dequant")
         return out
+
+
+def archive_header(buf: bytes) -> tuple:
+    """(quant_bits, default_block, record_count) of an AQSGET8 archive header
+    (Q8A:277-293); raises InvalidDataError for a malformed one."""
+    b = np.frombuffer(buf, np.uint8)
+    bits, blk, rec = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    check(_abi.load().aexq_archive_header(b.ctypes.data, b.size, ctypes.byref(bits),
+                                          ctypes.byref(blk), ctypes.byref(rec)),
+          "archive_header")
+    return bits.value, blk.value, rec.value
 
 
 def make_args(alpha: float = 1.0, beta: float = 1.0, c: Optional[torch.Tensor] = None,

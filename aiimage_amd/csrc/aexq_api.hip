@@ -62,6 +62,8 @@ struct aexq_ctx {
   // decode attention split partials
   float* attn_part = nullptr;
   long long attn_cap = 0;
+  int* attn_count = nullptr;  // per kv head: splits finished in the running launch
+  int attn_count_cap = 0;
 };
 
 struct aexq_weight {
@@ -113,6 +115,7 @@ extern "C" void aexq_destroy(aexq_ctx* ctx) {
   (void)hipFree(ctx->logits_scratch);
   (void)hipFree(ctx->act_scratch);
   (void)hipFree(ctx->attn_part);
+  (void)hipFree(ctx->attn_count);
   delete ctx;
 }
 
@@ -132,9 +135,10 @@ extern "C" aexq_status aexq_synchronize(aexq_ctx* ctx) {
 // ---------------------------------------------------------------------------
 // weights
 // ---------------------------------------------------------------------------
-static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const void* packed,
-                                 const void* scales, int scale_dtype, int n, int k, int block,
-                                 int nibble_code, aexq_weight** out) {
+// A weight's device buffers, codes set to the padding code (0 in device form)
+// and scales to zero; the caller fills them.
+static aexq_status alloc_weight(aexq_ctx* ctx, const char* op, int bits, int scale_dtype, int n,
+                                int k, int block, int nibble_code, aexq_weight** out) {
   aexq_weight* w = new aexq_weight();
   w->ctx = ctx;
   w->bits = bits;
@@ -151,6 +155,34 @@ static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const 
   // at least 16 zeroed bytes after each copy's scales: the MFMA kernels' wide
   // scale loads may run into them
   w->scale_stride = round_up(w->scale_count * scale_bytes(scale_dtype) + 16, 256);
+  const int pad_byte = bits == 8 ? 0x80 : 0x88;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = hipMalloc((void**)&w->codes, w->code_stride);
+  if (e == hipSuccess) e = hipMalloc(&w->scales, w->scale_stride);
+  if (e == hipSuccess) e = hipMemset(w->codes, pad_byte, w->code_stride);
+  if (e == hipSuccess) e = hipMemset(w->scales, 0, w->scale_stride);
+  if (e != hipSuccess) {
+    (void)hipFree(w->codes);
+    (void)hipFree(w->scales);
+    delete w;
+    return hip_fail(e, op, "weight allocation");
+  }
+  *out = w;
+  return AEXQ_OK;
+}
+
+static void free_weight(aexq_weight* w) {
+  (void)hipFree(w->codes);
+  (void)hipFree(w->scales);
+  delete w;
+}
+
+static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const void* packed,
+                                 const void* scales, int scale_dtype, int n, int k, int block,
+                                 int nibble_code, aexq_weight** out) {
+  aexq_weight* w = nullptr;
+  aexq_status st = alloc_weight(ctx, op, bits, scale_dtype, n, k, block, nibble_code, &w);
+  if (st) return st;
   // Device code layout: Q8 bytes biased by 128 (q + 128), Q4 nibbles offset-8
   // (q + 8).  Both are one XOR of the reference's two's-complement words; the
   // synthetic offset-8 Q4 words are already in device form.
@@ -166,21 +198,12 @@ static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const 
     for (long long i = 0; i < nw; ++i) recoded[(size_t)i] = in[i] ^ flip;
     src = recoded.data();
   }
-  // padding decodes to code 0 in device form
-  const int pad_byte = bits == 8 ? 0x80 : 0x88;
-  hipError_t e = hipSetDevice(ctx->device);
-  if (e == hipSuccess) e = hipMalloc((void**)&w->codes, w->code_stride);
-  if (e == hipSuccess) e = hipMalloc(&w->scales, w->scale_stride);
-  if (e == hipSuccess) e = hipMemset(w->codes, pad_byte, w->code_stride);
-  if (e == hipSuccess) e = hipMemset(w->scales, 0, w->scale_stride);
-  if (e == hipSuccess) e = hipMemcpy(w->codes, src, w->code_bytes, hipMemcpyHostToDevice);
+  hipError_t e = hipMemcpy(w->codes, src, w->code_bytes, hipMemcpyHostToDevice);
   if (e == hipSuccess)
     e = hipMemcpy(w->scales, scales, w->scale_count * scale_bytes(scale_dtype),
                   hipMemcpyHostToDevice);
   if (e != hipSuccess) {
-    (void)hipFree(w->codes);
-    (void)hipFree(w->scales);
-    delete w;
+    free_weight(w);
     return hip_fail(e, op, "weight upload");
   }
   *out = w;
@@ -276,6 +299,178 @@ extern "C" aexq_status aexq_weight_q8_from_f32(aexq_ctx* ctx, const float* data,
 extern "C" aexq_status aexq_weight_q4_from_f32(aexq_ctx* ctx, const float* data, int n, int k,
                                                int trans_b, aexq_weight** out) {
   return weight_from_f32(ctx, "aexq_weight_q4_from_f32", 4, data, n, k, trans_b, out);
+}
+
+// ---------------------------------------------------------------------------
+// AQSGET8 archives (Q8A = NcnnQ8Archive.cs): the archive header, and one Gemm
+// weight record straight into the device layout.
+// ---------------------------------------------------------------------------
+static constexpr uint64_t kArchiveMagic = 0x0038544547535141ull;  // Q8A:26 "AQSGET8"
+static constexpr uint32_t kArchiveVersion = 1u;                    // Q8A:27
+static constexpr uint32_t kRecordMagic = 0x31523851u;              // Q8A:28 "Q8R1"
+static constexpr int kRecordQ8 = 1, kRecordRaw = 2, kRecordQ4 = 3;  // Q8A:31-33
+static constexpr size_t kRecordHeaderBytes = 24;                   // Q8A:30, 236-245
+
+static uint32_t get_u32(const uint8_t* p) {
+  uint32_t v;
+  memcpy(&v, p, 4);
+  return v;
+}
+
+extern "C" aexq_status aexq_archive_header(const void* buf, size_t len, int* quant_bits,
+                                           int* default_block, int* record_count) {
+  const char* op = "aexq_archive_header";
+  if (!buf) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "buf is NULL");
+  const uint8_t* b = (const uint8_t*)buf;
+  if (len < 32) return fail(AEXQ_ERR_FORMAT, op, "archive header needs 32 bytes, got %zu", len);
+  uint64_t magic;
+  memcpy(&magic, b, 8);
+  // Q8A:280-290
+  if (magic != kArchiveMagic) return fail(AEXQ_ERR_FORMAT, op, "Invalid AIImage Q8 archive magic.");
+  const uint32_t version = get_u32(b + 8);
+  if (version != kArchiveVersion)
+    return fail(AEXQ_ERR_FORMAT, op, "Unsupported AIImage Q8 archive version: %u", version);
+  const int bits = (int)get_u32(b + 12);
+  const int block = (int)get_u32(b + 16);
+  const int records = (int)get_u32(b + 20);
+  if (block <= 0 || records < 0 || (bits != 0 && bits != 4 && bits != 8))
+    return fail(AEXQ_ERR_FORMAT, op, "Invalid AIImage quantized archive header.");
+  if (quant_bits) *quant_bits = bits == 0 ? 8 : bits;  // Q8A:293
+  if (default_block) *default_block = block;
+  if (record_count) *record_count = records;
+  return AEXQ_OK;
+}
+
+struct RecordHeader {
+  int kind, count, block, payload;
+};
+
+// Q8A:447-463 ReadHeader, plus the bounds of the caller's buffer.
+static aexq_status read_record_header(const char* op, const uint8_t* rec, size_t len,
+                                      long long expected, RecordHeader* h) {
+  if (len < kRecordHeaderBytes)
+    return fail(AEXQ_ERR_FORMAT, op, "record header needs %zu bytes, got %zu",
+                kRecordHeaderBytes, len);
+  if (get_u32(rec) != kRecordMagic) return fail(AEXQ_ERR_FORMAT, op, "Invalid Q8 record magic.");
+  h->kind = (int)get_u32(rec + 4);
+  h->count = (int)get_u32(rec + 8);
+  h->block = (int)get_u32(rec + 12);
+  h->payload = (int)get_u32(rec + 16);
+  if ((long long)h->count != expected)
+    return fail(AEXQ_ERR_FORMAT, op, "Q8 record element count mismatch. expected=%lld actual=%d",
+                expected, h->count);
+  if (h->block <= 0 || h->payload < 0) return fail(AEXQ_ERR_FORMAT, op, "Invalid Q8 record header.");
+  if (len - kRecordHeaderBytes < (size_t)h->payload)
+    return fail(AEXQ_ERR_FORMAT, op, "record payload of %d bytes, %zu available", h->payload,
+                len - kRecordHeaderBytes);
+  return AEXQ_OK;
+}
+
+// Bytes a Q8 / Q4 record of `count` elements in blocks of `block` consumes
+// (Q8A:249-255); the reader requires the header's payload to match (Q8A:465-469).
+static long long quant_payload_bytes(int kind, long long count, int block) {
+  const long long full = count / block, tail = count - full * block;
+  const long long per = kind == kRecordQ8 ? block : (block + 1) / 2;
+  long long bytes = full * (4 + per);
+  if (tail) bytes += 4 + (kind == kRecordQ8 ? tail : (tail + 1) / 2);
+  return bytes;
+}
+
+// Q8A:295-339 ReadArray: the record as float32 (raw copied; Q8 (sbyte)b * scale;
+// Q4 (raw >= 8 ? raw - 16 : raw) * scale).
+static aexq_status record_as_f32(const char* op, const RecordHeader& h, const uint8_t* payload,
+                                 std::vector<float>& out) {
+  const long long count = h.count;
+  out.assign((size_t)count, 0.0f);
+  if (h.kind == kRecordRaw) {
+    if ((long long)h.payload != count * 4)
+      return fail(AEXQ_ERR_FORMAT, op, "Q8 raw float record size mismatch.");
+    memcpy(out.data(), payload, (size_t)count * 4);
+    return AEXQ_OK;
+  }
+  if (h.kind != kRecordQ8 && h.kind != kRecordQ4)
+    return fail(AEXQ_ERR_FORMAT, op, "Expected a quantized array record.");
+  const long long need = quant_payload_bytes(h.kind, count, h.block);
+  if (need != h.payload)
+    return fail(AEXQ_ERR_FORMAT, op, "Q8 payload size mismatch. expected=%d actual=%lld",
+                h.payload, need);
+  long long used = 0;
+  for (long long off = 0; off < count; off += h.block) {
+    const long long len = h.block < count - off ? h.block : count - off;
+    float scale;
+    memcpy(&scale, payload + used, 4);
+    used += 4;
+    if (h.kind == kRecordQ8) {
+      for (long long i = 0; i < len; ++i) out[off + i] = (float)(int8_t)payload[used + i] * scale;
+      used += len;
+    } else {
+      for (long long i = 0; i < len; ++i) {
+        const int raw = (payload[used + (i >> 1)] >> ((i & 1) * 4)) & 0xf;
+        out[off + i] = (float)(raw >= 8 ? raw - 16 : raw) * scale;
+      }
+      used += (len + 1) / 2;
+    }
+  }
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_weight_from_record(aexq_ctx* ctx, int bits, const void* record,
+                                               size_t record_len, int n, int k,
+                                               aexq_weight** out, size_t* consumed) {
+  const char* op = "aexq_weight_from_record";
+  if (!ctx || !record || !out) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (bits != 4 && bits != 8) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "bits=%d (4 or 8)", bits);
+  if (n <= 0 || k <= 0)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "n=%d k=%d must be positive", n, k);
+  const long long count = (long long)n * k;
+  if (count > 0x7fffffffLL)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "n*k=%lld exceeds a record's count", count);
+  const uint8_t* rec = (const uint8_t*)record;
+  RecordHeader h;
+  aexq_status st = read_record_header(op, rec, record_len, count, &h);
+  if (st) return st;
+  const uint8_t* payload = rec + kRecordHeaderBytes;
+  if (consumed) *consumed = kRecordHeaderBytes + (size_t)h.payload;
+  const bool direct = (bits == 4 && h.kind == kRecordQ4) || (bits == 8 && h.kind == kRecordQ8);
+  if (!direct) {
+    // GL:60-68: a record of another kind is read as float32 and quantized per
+    // output row at upload (GL:113-141 -> GS:12838-12885, 12912-12964)
+    std::vector<float> values;
+    st = record_as_f32(op, h, payload, values);
+    if (st) return st;
+    return weight_from_f32(ctx, op, bits, values.data(), n, k, 1, out);
+  }
+  // Q8A:345-346 / GL:67: the direct Q8 path reads with expectedBlockSize = K
+  if (bits == 8 && h.block != k)
+    return fail(AEXQ_ERR_FORMAT, op, "Q8 block size mismatch. expected=%d actual=%d", k, h.block);
+  // GS:12979-12980
+  if (bits == 4 && k % h.block != 0)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op,
+                "Direct Q4 group size must divide the Gemm K dimension. | block=%d k=%d", h.block,
+                k);
+  const long long need = quant_payload_bytes(h.kind, count, h.block);
+  if (need != h.payload)
+    return fail(AEXQ_ERR_FORMAT, op, "Q8 payload size mismatch. expected=%d actual=%lld",
+                h.payload, need);
+  aexq_weight* w = nullptr;
+  st = alloc_weight(ctx, op, bits, AEXQ_DTYPE_F32, n, k, h.block, AEXQ_NIBBLE_TWOS, &w);
+  if (st) return st;
+  // the payload goes to the device as it is and is repacked there; the
+  // allocation's fills and the repack are ordered on the null stream
+  void* staging = nullptr;
+  hipError_t e = hipMalloc(&staging, (size_t)h.payload > 0 ? (size_t)h.payload : 1);
+  if (e == hipSuccess && h.payload > 0)
+    e = hipMemcpy(staging, payload, (size_t)h.payload, hipMemcpyHostToDevice);
+  if (e == hipSuccess)
+    e = record_repack_launch(staging, count, h.block, bits, w->codes, (float*)w->scales, nullptr);
+  if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+  (void)hipFree(staging);
+  if (e != hipSuccess) {
+    free_weight(w);
+    return hip_fail(e, op, "record repack");
+  }
+  *out = w;
+  return AEXQ_OK;
 }
 
 extern "C" aexq_status aexq_weight_replicate(aexq_ctx* ctx, const aexq_weight* src, int batch,
@@ -1031,10 +1226,10 @@ static aexq_status attn_prepare(aexq_ctx* ctx, const char* op, int heads_q, int 
     return fail(AEXQ_ERR_UNSUPPORTED, op, "query heads per key head = %d (1, 2, 4 or 8)", group);
   if (length <= 0 || length > capacity)
     return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "length=%d capacity=%d", length, capacity);
-  const int splits = attn_splits(length, group);
-  if (splits > 1024)
-    return fail(AEXQ_ERR_UNSUPPORTED, op, "length=%d needs %d splits (at most 1024)", length,
-                splits);
+  const int splits = attn_splits(length);
+  if (splits > attn_max_splits())
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "length=%d needs %d splits (at most %d)", length,
+                splits, attn_max_splits());
   const long long need = (long long)heads_q * splits * (head_dim + 2);
   HIP_TRY(op, hipSetDevice(ctx->device));
   if (need > ctx->attn_cap) {
@@ -1043,6 +1238,15 @@ static aexq_status attn_prepare(aexq_ctx* ctx, const char* op, int heads_q, int 
     ctx->attn_cap = 0;
     HIP_TRY(op, hipMalloc((void**)&ctx->attn_part, need * sizeof(float)));
     ctx->attn_cap = need;
+  }
+  if (heads_kv > ctx->attn_count_cap) {
+    // split counters start at zero; every launch leaves them at zero
+    (void)hipFree(ctx->attn_count);
+    ctx->attn_count = nullptr;
+    ctx->attn_count_cap = 0;
+    HIP_TRY(op, hipMalloc((void**)&ctx->attn_count, heads_kv * sizeof(int)));
+    HIP_TRY(op, hipMemset(ctx->attn_count, 0, heads_kv * sizeof(int)));
+    ctx->attn_count_cap = heads_kv;
   }
   return AEXQ_OK;
 }
@@ -1057,8 +1261,8 @@ extern "C" aexq_status aexq_attention_decode(aexq_ctx* ctx, const void* q, const
   aexq_status st = attn_prepare(ctx, op, heads_q, heads_kv, head_dim, capacity, length);
   if (st) return st;
   hipError_t e = attn_decode_launch(q, k_cache, v_cache, heads_q, heads_kv, capacity, length,
-                                    scale, ctx->attn_part, out, nullptr, nullptr, nullptr, nullptr,
-                                    ctx->stream);
+                                    scale, ctx->attn_part, ctx->attn_count, out, nullptr, nullptr,
+                                    nullptr, nullptr, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, op, "attention launch");
   return AEXQ_OK;
 }
@@ -1074,8 +1278,8 @@ extern "C" aexq_status aexq_attention_decode_rope(aexq_ctx* ctx, const void* q, 
   aexq_status st = attn_prepare(ctx, op, heads_q, heads_kv, head_dim, capacity, length);
   if (st) return st;
   hipError_t e = attn_decode_launch(q, k_cache, v_cache, heads_q, heads_kv, capacity, length,
-                                    scale, ctx->attn_part, out, k, v, cos_table, sin_table,
-                                    ctx->stream);
+                                    scale, ctx->attn_part, ctx->attn_count, out, k, v, cos_table,
+                                    sin_table, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, op, "attention launch");
   return AEXQ_OK;
 }

@@ -1,6 +1,7 @@
 // Decode-step kernels around the quantized linears (gfx950): the tied Q8 token
 // embedding, RoPE with KV-cache append, GQA decode attention over an fp16 KV
-// cache (split over positions, then combined), and a standalone RMSNorm.
+// cache (split over positions, the splits merged by the last one to finish),
+// and a standalone RMSNorm.
 //
 // Reference semantics (paths relative to the reference root):
 //   embedding gather   Qwen35SharedTokenEmbeddingWeights.cs:185-198, BT:13-26
@@ -83,185 +84,313 @@ hipError_t rope_kv_launch(void* q, const void* k, const void* v, void* kcache, v
 }
 
 // ---------------------------------------------------------------------------
-// GQA decode attention, split over positions.  Workgroup (kv head g, split c)
-// covers positions [c * kAttnChunk, ...) of length `len` for the G = hq / hkv
-// query heads of g: every cached K and V row is read once.  Thread t scores
-// position t / G for head t % G (the G threads of a position read the same K
-// row); then thread t accumulates output dimension t for every head.  The
-// partial (max, sum, acc[d]) goes to part[h][split]; the combine kernel merges
-// the splits.  d == kAttnDim, G * kAttnChunk == kAttnThreads.
+// GQA decode attention in one launch.  Workgroup (kv head g, split c) covers
+// positions [64 c, 64 c + 64) of the `len` cached ones for the G = hq / hkv
+// query heads of g, so every cached K and V row is read once.  Every load of
+// the workgroup -- q, the RoPE tables and new row, then its K and V rows --
+// is issued before the first wait, and q (rotated here when RoPE is fused)
+// meets K after one barrier:
+//   scores   lanes 4i..4i+3 own position p0 + i, each 32 of its 128 dims, for
+//            all G heads (v_dot2 with fp32 accumulation, quad reduction);
+//   softmax  max / sum per head over the split's positions (wave shuffles,
+//            then LDS across the 4 waves);
+//   P V      wave w owns positions p0 + 16 w + [0, 16), lane l dimensions
+//            2l and 2l + 1; the four waves' sums meet in LDS.
+// The split's (max, sum, acc[128]) per head goes to part[h][split].  The last
+// workgroup of kv head g to finish (a device-scope counter that the same
+// workgroup resets to 0, so the launch needs no clearing and replays inside a
+// graph) merges the splits of its G heads:
+//   M = max m_s, L = sum l_s e^(m_s - M), out = sum acc_s e^(m_s - M) / max(L, 1e-20).
+// head_dim == 128.
 // ---------------------------------------------------------------------------
 constexpr int kAttnDim = 128;
-constexpr int kAttnThreads = 128;
-constexpr int kAttnChunk = 32;  // positions per split for G = 4
+constexpr int kAttnThreads = 256;
+
+// Device-coherent (agent scope) fp32 store / load: written through to, and
+// read from, the level all XCDs share.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int kAttnPos = 64;         // positions per split
+constexpr int kAttnMaxSplits = 512;  // combine staging in LDS
 
 template <int G>
-__global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(
-    const f16* q, const f16* kcache, const f16* vcache, int cap, int len, float scale, int splits,
-    float* part, const f16* knew, const f16* vnew, f16* kcache_w, f16* vcache_w,
-    const float* cosv, const float* sinv) {
-  // knew != nullptr: fused RoPE + append.  q and the new k row are rotated here
-  // (rounded to fp16 as a separate RoPE launch would store them); the split that
-  // covers position len - 1 writes the new K/V rows to the cache and every
-  // split uses the rotated q.
-  constexpr int CH = kAttnThreads / G;  // positions per split
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
+    const f16* q, const f16* kcache, const f16* vcache, int cap, int len, float scale,
+    int splits, float* part, int* counters, f16* out, const f16* knew, const f16* vnew,
+    f16* kcache_w, f16* vcache_w, const float* cosv, const float* sinv) {
   const int g = blockIdx.x, c = blockIdx.y;
-  const int t = threadIdx.x;
-  __shared__ float qs[G][kAttnDim];
-  __shared__ float ps[G][CH];
-  __shared__ float stat[G][2];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int p0 = c * kAttnPos;
+  const int pl = t >> 2, qq = t & 3;  // scores: position p0 + pl, dims 32 qq .. 32 qq + 31
   const bool rope = knew != nullptr;
-  const int half = kAttnDim / 2;
-  if (rope) {
-    for (int i = t; i < G * half; i += kAttnThreads) {
-      const int h = i / half, j = i % half;
-      const f16* qr = q + ((long long)g * G + h) * kAttnDim;
-      const float x0 = (float)qr[j], x1 = (float)qr[j + half];
-      qs[h][j] = (float)(f16)(x0 * cosv[j] - x1 * sinv[j]);
-      qs[h][j + half] = (float)(f16)(x0 * sinv[j] + x1 * cosv[j]);
-    }
-    const int pos = len - 1;
-    if (pos / CH == c) {
-      for (int j = t; j < half; j += kAttnThreads) {
-        const f16* kr = knew + (long long)g * kAttnDim;
-        const float x0 = (float)kr[j], x1 = (float)kr[j + half];
-        f16* kc = kcache_w + ((long long)g * cap + pos) * kAttnDim;
-        kc[j] = (f16)(x0 * cosv[j] - x1 * sinv[j]);
-        kc[j + half] = (f16)(x0 * sinv[j] + x1 * cosv[j]);
-        f16* vc = vcache_w + ((long long)g * cap + pos) * kAttnDim;
-        vc[j] = vnew[(long long)g * kAttnDim + j];
-        vc[j + half] = vnew[(long long)g * kAttnDim + j + half];
-      }
-    }
-  } else {
-    for (int i = t; i < G * kAttnDim; i += kAttnThreads)
-      qs[i / kAttnDim][i % kAttnDim] =
-          (float)q[((long long)g * G + i / kAttnDim) * kAttnDim + i % kAttnDim];
-  }
-  // the appended rows are read back below by other threads of this workgroup
-  __syncthreads();
+  const int pos = len - 1;             // the appended position when RoPE is fused
+  const bool has_new = rope && pos >= p0 && pos < p0 + kAttnPos;
+  constexpr int half = kAttnDim / 2;
+  const long long head_off = (long long)g * cap * kAttnDim;
 
-  const int p0 = c * CH;
-  {
-    const int pl = t / G, h = t % G;
-    const int p = p0 + pl;
-    float s = -INFINITY;
-    if (p < len) {
-      const u32x4* kr = (const u32x4*)(kcache + ((long long)g * cap + p) * kAttnDim);
-      float acc = 0.0f;
-#pragma unroll 4
-      for (int v = 0; v < kAttnDim / 8; ++v) {
-        const u32x4 w = kr[v];
+  // 1. loads, all issued before the first wait; q and the new row first, so
+  // that waiting for them leaves the K/V loads in flight.  Absent tables and
+  // rows come through empty buffer resources (they read 0).
+  constexpr int QI = (G * half + kAttnThreads - 1) / kAttnThreads;  // (head, j) pairs per thread
+  float qa[QI], qb[QI], cs[QI], sn[QI];
+  const __amdgpu_buffer_rsrc_t trs_c = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)cosv, (short)0, rope ? half * 4 : 0, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t trs_s = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)sinv, (short)0, rope ? half * 4 : 0, kBufferRsrcWord3);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const f16x2 kk = as_h2(w[e]);
-          acc = fmaf(qs[h][8 * v + 2 * e], (float)kk[0], acc);
-          acc = fmaf(qs[h][8 * v + 2 * e + 1], (float)kk[1], acc);
-        }
-      }
-      s = acc * scale;
+  for (int r = 0; r < QI; ++r) {
+    const int i = min(t + r * kAttnThreads, G * half - 1);
+    const int h = i / half, j = i % half;
+    const f16* qr = q + ((long long)g * G + h) * kAttnDim;
+    qa[r] = (float)qr[j];
+    qb[r] = (float)qr[j + half];
+    cs[r] = as_f32(__builtin_amdgcn_raw_buffer_load_b32(trs_c, j * 4, 0, 0));
+    sn[r] = as_f32(__builtin_amdgcn_raw_buffer_load_b32(trs_s, j * 4, 0, 0));
+  }
+  const int jn = t & (half - 1);
+  const __amdgpu_buffer_rsrc_t nrs_k = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(rope ? knew + (long long)g * kAttnDim : q), (short)0, has_new ? kAttnDim * 2 : 0,
+      kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t nrs_v = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(rope ? vnew + (long long)g * kAttnDim : q), (short)0, has_new ? kAttnDim * 2 : 0,
+      kBufferRsrcWord3);
+  const uint32_t kn0 = __builtin_amdgcn_raw_buffer_load_b16(nrs_k, jn * 2, 0, 0);
+  const uint32_t kn1 = __builtin_amdgcn_raw_buffer_load_b16(nrs_k, (jn + half) * 2, 0, 0);
+  const uint32_t vn0 = __builtin_amdgcn_raw_buffer_load_b16(nrs_v, jn * 2, 0, 0);
+  const uint32_t vn1 = __builtin_amdgcn_raw_buffer_load_b16(nrs_v, (jn + half) * 2, 0, 0);
+  const float tc = as_f32(__builtin_amdgcn_raw_buffer_load_b32(trs_c, jn * 4, 0, 0));
+  const float ts = as_f32(__builtin_amdgcn_raw_buffer_load_b32(trs_s, jn * 4, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);  // keeps the q-side loads ahead of K and V
+  // K rows of the split (rows >= len read 0): position p0 + pl, 64 bytes per lane
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(kcache + head_off), (short)0, len * kAttnDim * 2, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(vcache + head_off), (short)0, len * kAttnDim * 2, kBufferRsrcWord3);
+  u32x4 kreg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    kreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            krs, (p0 + pl) * 256 + qq * 64 + i * 16, 0, 0));
+  // V rows: wave w owns positions p0 + 16 w + [0, 16), lane l dimensions 2l, 2l + 1
+  uint32_t vreg[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    vreg[i] = __builtin_amdgcn_raw_buffer_load_b32(
+        vrs, ((p0 + 16 * wave + i) * kAttnDim + 2 * lane) * 2, 0, 0);
+
+  // 2. q of the G heads (rotated and rounded to fp16 when RoPE is fused) and,
+  // in the split that holds it, the appended K/V row
+  __shared__ __align__(16) f16 qs[G][kAttnDim];
+  __shared__ __align__(16) f16 kn[kAttnDim];
+  __shared__ __align__(16) f16 vn[kAttnDim];
+#pragma unroll
+  for (int r = 0; r < QI; ++r) {
+    const int i = t + r * kAttnThreads;
+    if (i < G * half) {
+      const int h = i / half, j = i % half;
+      qs[h][j] = rope ? (f16)(qa[r] * cs[r] - qb[r] * sn[r]) : (f16)qa[r];
+      qs[h][j + half] = rope ? (f16)(qa[r] * sn[r] + qb[r] * cs[r]) : (f16)qb[r];
     }
-    ps[h][pl] = s;
+  }
+  if (has_new && t < half) {
+    const float x0 = (float)__builtin_bit_cast(f16, (uint16_t)kn0);
+    const float x1 = (float)__builtin_bit_cast(f16, (uint16_t)kn1);
+    const f16 k0 = (f16)(x0 * tc - x1 * ts), k1 = (f16)(x0 * ts + x1 * tc);
+    const f16 v0 = __builtin_bit_cast(f16, (uint16_t)vn0);
+    const f16 v1 = __builtin_bit_cast(f16, (uint16_t)vn1);
+    kn[t] = k0;
+    kn[t + half] = k1;
+    vn[t] = v0;
+    vn[t + half] = v1;
+    f16* kc = kcache_w + head_off + (long long)pos * kAttnDim;
+    f16* vc = vcache_w + head_off + (long long)pos * kAttnDim;
+    kc[t] = k0;
+    kc[t + half] = k1;
+    vc[t] = v0;
+    vc[t + half] = v1;
   }
   __syncthreads();
-  if (t < G) {
-    float mx = -INFINITY;
-    for (int i = 0; i < CH; ++i) mx = fmaxf(mx, ps[t][i]);
-    float sum = 0.0f;
-    for (int i = 0; i < CH; ++i) {
-      const float e = ps[t][i] == -INFINITY ? 0.0f : __expf(ps[t][i] - mx);
-      ps[t][i] = e;
-      sum += e;
+  if (has_new) {
+    // the cache row at `pos` was loaded before it was written: take the new one
+    if (p0 + pl == pos) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kreg[i] = *(const u32x4*)&kn[qq * 32 + i * 8];
     }
-    stat[t][0] = mx;
-    stat[t][1] = sum;
-  }
-  __syncthreads();
-  // thread t: output dimension t of every head
-  float acc[G];
 #pragma unroll
-  for (int h = 0; h < G; ++h) acc[h] = 0.0f;
-  const int n = len - p0 < CH ? len - p0 : CH;
-  for (int i = 0; i < n; ++i) {
-    const float vv = (float)vcache[((long long)g * cap + p0 + i) * kAttnDim + t];
-#pragma unroll
-    for (int h = 0; h < G; ++h) acc[h] = fmaf(ps[h][i], vv, acc[h]);
+    for (int i = 0; i < 16; ++i)
+      if (p0 + 16 * wave + i == pos) vreg[i] = *(const uint32_t*)&vn[2 * lane];
   }
-  const int stride = kAttnDim + 2;
+
+  // 3. scores of position p0 + pl for every head
+  const bool live = p0 + pl < len;
+  float sc[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    float* o = part + ((long long)(g * G + h) * splits + c) * stride;
-    o[2 + t] = acc[h];
-    if (t == 0) {
-      o[0] = stat[h][0];
-      o[1] = stat[h][1];
+    const u32x4* qv = (const u32x4*)&qs[h][qq * 32];
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 qw = qv[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = dot2(kreg[i][e], qw[e], acc);
+    }
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    sc[h] = live ? acc * scale : -INFINITY;
+  }
+
+  // 4. softmax statistics of the split per head
+  __shared__ float red[kAttnThreads / 64][G];
+  __shared__ float es[G][kAttnPos];
+  float mx[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float m = sc[h];
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    m = fmaxf(m, __shfl_xor(m, 8, 64));
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (lane == 0) red[wave][h] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float m = red[0][h];
+#pragma unroll
+    for (int w = 1; w < kAttnThreads / 64; ++w) m = fmaxf(m, red[w][h]);
+    mx[h] = m;  // finite: every split holds at least one live position
+  }
+  __syncthreads();
+  float sm[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float e = live ? __expf(sc[h] - mx[h]) : 0.0f;
+    if (qq == 0) es[h][pl] = e;
+    float s = e;
+    s += __shfl_xor(s, 4, 64);
+    s += __shfl_xor(s, 8, 64);
+    s += __shfl_xor(s, 16, 64);
+    s += __shfl_xor(s, 32, 64);
+    if (lane == 0) red[wave][h] = s;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnThreads / 64; ++w) s += red[w][h];
+    sm[h] = s;
+  }
+
+  // 5. P V: wave w, dimensions 2 lane and 2 lane + 1 over its 16 positions;
+  // the four waves' sums meet in LDS
+  __shared__ float pv[kAttnThreads / 64][G][kAttnDim];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float e = es[h][16 * wave + i];
+      const f16x2 vv = as_h2(vreg[i]);
+      a0 = fmaf(e, (float)vv[0], a0);
+      a1 = fmaf(e, (float)vv[1], a1);
+    }
+    pv[wave][h][2 * lane] = a0;
+    pv[wave][h][2 * lane + 1] = a1;
+  }
+  __syncthreads();
+  const long long stride = kAttnDim + 2;
+  const int d = t & (kAttnDim - 1), vh = t >> 7;
+  if (vh == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float a = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kAttnThreads / 64; ++w) a += pv[w][h][d];
+      float* o = part + ((long long)(g * G + h) * splits + c) * stride;
+      store_coherent(o + 2 + d, a);
+      if (d == 0) {
+        store_coherent(o, mx[h]);
+        store_coherent(o + 1, sm[h]);
+      }
     }
   }
-}
 
-// Merges the splits of each query head: M = max m_s, L = sum l_s e^(m_s - M),
-// out = sum acc_s e^(m_s - M) / max(L, 1e-20), stored fp16 [hq][d].  The split
-// statistics are staged in LDS with one load per thread, so no thread walks a
-// chain of dependent loads; thread t then sums dimension t over the splits.
-constexpr int kMaxSplits = 1024;
-
-__global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* part, int splits,
-                                                                    f16* out) {
-  const int h = blockIdx.x, t = threadIdx.x;
-  const int stride = kAttnDim + 2;
-  const float* ph = part + (long long)h * splits * stride;
-  __shared__ float wm[kMaxSplits];
-  __shared__ float red[kAttnThreads / 64];
-  float mx = -INFINITY;
-  for (int s = t; s < splits; s += kAttnThreads) {
-    wm[s] = ph[(long long)s * stride];
-    mx = fmaxf(mx, wm[s]);
+  // 6. the last split of kv head g merges all of them.  Partials travel
+  // through device-coherent stores and loads (they bypass the per-XCD L2 that
+  // plain accesses would leave stale), ordered by waiting for the stores
+  // before the counter increment.
+  __shared__ int last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) last = atomicAdd(&counters[g], 1) == splits - 1;
+  __syncthreads();
+  if (!last) return;
+  __shared__ float cm[G * kAttnMaxSplits];  // split maxima, then weights
+  __shared__ float cl[G * kAttnMaxSplits];  // split sums
+  const float* pg = part + (long long)g * G * splits * stride;
+  for (int i = t; i < G * splits; i += kAttnThreads) {
+    cm[i] = load_coherent(pg + (long long)i * stride);
+    cl[i] = load_coherent(pg + (long long)i * stride + 1);
   }
-  mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  if ((t & 63) == 0) red[t >> 6] = mx;
   __syncthreads();
-  mx = red[0];
-#pragma unroll
-  for (int w = 1; w < kAttnThreads / 64; ++w) mx = fmaxf(mx, red[w]);
-  __syncthreads();
-  float lsum = 0.0f;
-  for (int s = t; s < splits; s += kAttnThreads) {
-    const float w = wm[s] == -INFINITY ? 0.0f : __expf(wm[s] - mx);
-    wm[s] = w;
-    lsum = fmaf(ph[(long long)s * stride + 1], w, lsum);
+  // per head: M = max m_s (each wave reduces the heads h == wave mod 4)
+  __shared__ float hm[G], hl[G];
+  for (int h = wave; h < G; h += kAttnThreads / 64) {
+    float m = -INFINITY;
+    for (int s2 = lane; s2 < splits; s2 += 64) m = fmaxf(m, cm[h * splits + s2]);
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    m = fmaxf(m, __shfl_xor(m, 8, 64));
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    float l = 0.0f;
+    for (int s2 = lane; s2 < splits; s2 += 64) {
+      const float w = __expf(cm[h * splits + s2] - m);
+      cm[h * splits + s2] = w;
+      l = fmaf(cl[h * splits + s2], w, l);
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      hm[h] = m;
+      hl[h] = l;
+    }
   }
-  lsum = wave_sum(lsum);
   __syncthreads();
-  if ((t & 63) == 0) red[t >> 6] = lsum;
-  __syncthreads();
-  float l = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kAttnThreads / 64; ++w) l += red[w];
-  float acc = 0.0f;
+  // thread t: dimension d of heads vh, vh + 2, ...
+  for (int h = vh; h < G; h += 2) {
+    const float* ph = pg + (long long)h * splits * stride + 2 + d;
+    const float* wh = cm + h * splits;
+    float a = 0.0f;
 #pragma unroll 8
-  for (int s = 0; s < splits; ++s) acc = fmaf(ph[(long long)s * stride + 2 + t], wm[s], acc);
-  out[(long long)h * kAttnDim + t] = (f16)(acc / fmaxf(l, 1e-20f));
+    for (int s2 = 0; s2 < splits; ++s2)
+      a = fmaf(load_coherent(ph + (long long)s2 * stride), wh[s2], a);
+    out[((long long)g * G + h) * kAttnDim + d] = (f16)(a / fmaxf(hl[h], 1e-20f));
+  }
+  if (t == 0) counters[g] = 0;  // ready for the next launch
 }
 
-int attn_splits(int len, int group) { return (len + kAttnThreads / group - 1) / (kAttnThreads / group); }
+int attn_splits(int len) { return (len + kAttnPos - 1) / kAttnPos; }
+int attn_max_splits() { return kAttnMaxSplits; }
 
 hipError_t attn_decode_launch(const void* q, const void* kcache, const void* vcache, int hq,
-                              int hkv, int cap, int len, float scale, float* part, void* out,
-                              const void* knew, const void* vnew, const float* cosv,
+                              int hkv, int cap, int len, float scale, float* part, int* counters,
+                              void* out, const void* knew, const void* vnew, const float* cosv,
                               const float* sinv, hipStream_t stream) {
   const int group = hq / hkv;
-  const int splits = attn_splits(len, group);
-  if (splits > kMaxSplits) return hipErrorInvalidValue;
+  const int splits = attn_splits(len);
+  if (splits > kAttnMaxSplits) return hipErrorInvalidValue;
   const dim3 grid(hkv, splits);
-#define AEXQ_ATTN(G)                                                                            \
-  hipLaunchKernelGGL(attn_split_kernel<G>, grid, dim3(kAttnThreads), 0, stream, (const f16*)q,  \
-                     (const f16*)kcache, (const f16*)vcache, cap, len, scale, splits, part,     \
-                     (const f16*)knew, (const f16*)vnew, (f16*)kcache, (f16*)vcache, cosv, sinv)
+#define AEXQ_ATTN(G)                                                                             \
+  hipLaunchKernelGGL(attn_decode_kernel<G>, grid, dim3(kAttnThreads), 0, stream, (const f16*)q, \
+                     (const f16*)kcache, (const f16*)vcache, cap, len, scale, splits, part,      \
+                     counters, (f16*)out, (const f16*)knew, (const f16*)vnew, (f16*)kcache,      \
+                     (f16*)vcache, cosv, sinv)
   switch (group) {
     case 1: AEXQ_ATTN(1); break;
     case 2: AEXQ_ATTN(2); break;
@@ -270,10 +399,6 @@ hipError_t attn_decode_launch(const void* q, const void* kcache, const void* vca
     default: return hipErrorInvalidValue;
   }
 #undef AEXQ_ATTN
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(hq), dim3(kAttnThreads), 0, stream, part, splits,
-                     (f16*)out);
   return hipGetLastError();
 }
 

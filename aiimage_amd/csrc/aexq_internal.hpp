@@ -124,6 +124,10 @@ hipError_t argmax_finalize_launch(const ArgmaxParams& a, hipStream_t stream);
 hipError_t logits_argmax_launch(const float* logits, int m, int n, long long rstride, float* pv,
                                 int* pi, float* ps, int parts, hipStream_t stream);
 int logits_argmax_cols_per_wg();
+// AQSGET8 Q8 / Q4 record payload (after its 24-byte header) into the device
+// codes and fp32 scales of a weight with `count` elements.
+hipError_t record_repack_launch(const void* payload, long long count, int block, int bits,
+                                uint32_t* codes, float* scales, hipStream_t stream);
 hipError_t dequant_launch(int fmt, const uint32_t* w, const void* s, int scale_f16, int n, int k,
                           int group, float* out, hipStream_t stream);
 hipError_t replicate_launch(const void* src, void* dst, long long bytes, int copies,
@@ -135,12 +139,15 @@ hipError_t embed_q8_launch(const uint32_t* codes, const void* scales, int scale_
 hipError_t rope_kv_launch(void* q, const void* k, const void* v, void* kcache, void* vcache,
                           int hq, int hkv, int d, int cap, int pos, const float* cosv,
                           const float* sinv, hipStream_t stream);
-int attn_splits(int len, int group);
-// knew/vnew/cosv/sinv non-null: RoPE of q and of the new k row plus the K/V
-// append at position len - 1, fused into the split kernel
+// splits of a decode attention over `len` positions, and the most one launch takes
+int attn_splits(int len);
+int attn_max_splits();
+// part: hq * splits * (128 + 2) floats; counters: hkv ints, zero before the
+// first launch (every launch leaves them zero).  knew/vnew/cosv/sinv non-null:
+// RoPE of q and of the new k row plus the K/V append at position len - 1.
 hipError_t attn_decode_launch(const void* q, const void* kcache, const void* vcache, int hq,
-                              int hkv, int cap, int len, float scale, float* part, void* out,
-                              const void* knew, const void* vnew, const float* cosv,
+                              int hkv, int cap, int len, float scale, float* part, int* counters,
+                              void* out, const void* knew, const void* vnew, const float* cosv,
                               const float* sinv, hipStream_t stream);
 
 }  // namespace aexq

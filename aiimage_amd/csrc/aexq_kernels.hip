@@ -226,6 +226,76 @@ __global__ __launch_bounds__(kThreads) void argmax_finalize_kernel(const ArgmaxP
 }
 
 // ---------------------------------------------------------------------------
+// AQSGET8 record payload -> device layout.  A Q8 (Q4) record's payload is,
+// per block of `block` flat elements, an fp32 scale and then the block's int8
+// codes (two's-complement nibbles, low nibble = even element; Q8A:94-139).
+// Block b starts at byte b * (4 + codes bytes of a full block): every block
+// but the last is full.  Thread per output word: the codes land as the packed
+// words of ReadPackedArray / ReadQ4PackedArray (Q8A:341-431) already recoded
+// to device form (Q8 q + 128, Q4 q + 8; elements past the count are code 0),
+// and one thread per block copies its scale.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void record_repack_kernel(const uint8_t* payload,
+                                                                 long long count, int block,
+                                                                 int bits, uint32_t* codes,
+                                                                 float* scales) {
+  const long long words = bits == 8 ? (count + 3) / 4 : (count + 7) / 8;
+  const long long nblocks = (count + block - 1) / block;
+  const long long bstride = 4 + (bits == 8 ? block : (block + 1) / 2);
+  const long long total = words > nblocks ? words : nblocks;
+  for (long long t = blockIdx.x * (long long)kThreads + threadIdx.x; t < total;
+       t += (long long)gridDim.x * kThreads) {
+    if (t < words) {
+      uint32_t word = 0u;
+      if (bits == 8) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const long long idx = t * 4 + e;
+          uint32_t b = 0x80u;  // code 0
+          if (idx < count) {
+            const long long bi = idx / block, i = idx - bi * block;
+            b = (uint32_t)payload[bi * bstride + 4 + i] ^ 0x80u;
+          }
+          word |= b << (8 * e);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const long long idx = t * 8 + e;
+          uint32_t nib = 0x8u;  // code 0
+          if (idx < count) {
+            const long long bi = idx / block, i = idx - bi * block;
+            const uint32_t byte = payload[bi * bstride + 4 + (i >> 1)];
+            nib = ((byte >> ((i & 1) * 4)) & 0xfu) ^ 0x8u;
+          }
+          word |= nib << (4 * e);
+        }
+      }
+      codes[t] = word;
+    }
+    if (t < nblocks) {
+      const uint8_t* sp = payload + t * bstride;
+      const uint32_t u = (uint32_t)sp[0] | ((uint32_t)sp[1] << 8) | ((uint32_t)sp[2] << 16) |
+                         ((uint32_t)sp[3] << 24);
+      scales[t] = __builtin_bit_cast(float, u);
+    }
+  }
+}
+
+hipError_t record_repack_launch(const void* payload, long long count, int block, int bits,
+                                uint32_t* codes, float* scales, hipStream_t stream) {
+  const long long words = bits == 8 ? (count + 3) / 4 : (count + 7) / 8;
+  const long long nblocks = (count + block - 1) / block;
+  const long long total = words > nblocks ? words : nblocks;
+  long long grid = (total + kThreads - 1) / kThreads;
+  if (grid > 65536) grid = 65536;
+  if (grid < 1) grid = 1;
+  hipLaunchKernelGGL(record_repack_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                     (const uint8_t*)payload, count, block, bits, codes, scales);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Dequantization to fp32 [N][K].  Chunk-aligned rows use the same code
 // expansion as the matvec kernels; other shapes decode element by element.
 // ---------------------------------------------------------------------------

@@ -152,6 +152,29 @@ aexq_status aexq_weight_q8_from_f32(aexq_ctx* ctx, const float* data, int n, int
 aexq_status aexq_weight_q4_from_f32(aexq_ctx* ctx, const float* data, int n, int k,
                                     int trans_b, aexq_weight** out);
 
+/* AQSGET8 archive header (32 bytes at the start of a .q8 archive), checked as
+ * the NcnnQ8ArchiveReader constructor does (Q8A:277-291); quant_bits 0 reads
+ * as 8 (Q8A:293).  Outputs may be NULL. */
+aexq_status aexq_archive_header(const void* buf, size_t len, int* quant_bits,
+                                int* default_block, int* record_count);
+
+/* One Gemm weight record of an AQSGET8 archive (its 24-byte header and
+ * payload, host memory) into the device layout, as AexisGemmLayer.LoadLayer
+ * reads and uploads it for a transB layer (GL:60-141):
+ *   bits 4, Q4 record: TryReadInt4QuantizedTensor -> ReadQ4PackedArray
+ *     (Q8A:385-431) -> direct upload (GS:12966-12996; the group must divide k);
+ *   bits 8, Q8 record: TryReadQuantizedTensor -> ReadPackedArray with the
+ *     expected block k (Q8A:341-383; another block is AEXQ_ERR_FORMAT);
+ *   any other record (raw fp32, or the other quantized kind): ReadArray
+ *     (Q8A:295-339) to float32, then quantized per output row as the float
+ *     overloads do (GS:12838-12885, 12912-12964).
+ * Direct records are copied to the device as they are and repacked there.
+ * The record's element count must be n*k; *consumed (nullable) receives the
+ * record's size in bytes (header + payload). */
+aexq_status aexq_weight_from_record(aexq_ctx* ctx, int bits, const void* record,
+                                    size_t record_len, int n, int k, aexq_weight** out,
+                                    size_t* consumed);
+
 /* A stack of `batch` copies of one packed weight, contiguous on the device.
  * Used for a layer stack and for cold-HBM measurement; copy 0 holds `packed`,
  * the others are device-side duplicates. */
@@ -235,7 +258,9 @@ aexq_status aexq_rope_kv_append(aexq_ctx* ctx, void* q, const void* k, const voi
  * (AexisSdpaAttentionPack4CDHW_Impl, MM:420-544): scores q.k * scale, softmax
  * with the maximum subtracted and the sum floored at 1e-20, output sum p * v;
  * query head h reads key/value head h / (heads_q / heads_kv).  q [heads_q][d],
- * caches [heads_kv][capacity][d], out [heads_q][d]; fp16; d == 128. */
+ * caches [heads_kv][capacity][d], out [heads_q][d]; fp16; d == 128;
+ * length <= 32768.  Launches on one context run in stream order (the split
+ * merge keeps per-context counters). */
 aexq_status aexq_attention_decode(aexq_ctx* ctx, const void* q, const void* k_cache,
                                   const void* v_cache, int heads_q, int heads_kv, int head_dim,
                                   int capacity, int length, float scale, void* out);
