@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the per-config extras")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the config-3 decode step timing and print its JSON (for "
+                         "profiling that step); not the benchmark line")
     ap.add_argument("--calib", action="store_true",
                     help="also run one 256 MiB fp32 neg kernel (known HBM traffic) to scale "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -288,7 +291,9 @@ def config3(torch, aexq, ctx, steps: int = 30):
         "frac_of_roofline": round(1000.0 / graph_ms / roof, 4),
         "GBps_graph": round(b["total"] / (graph_ms * 1e-3) / 1e9, 1),
         "kv_heads": cfg.heads_kv, "positions": cfg.capacity, "layers": cfg.layers,
-        "launches_per_token": 1 + cfg.layers * 6 + 3}}
+        # embedding; per layer q/k/v, attention, o_proj, gate/up, down; final
+        # norm, LM head and argmax finalize
+        "launches_per_token": 1 + cfg.layers * 5 + 3}}
     log(f"config3: {out['config3_decode']}")
     del g, sess
     torch.cuda.empty_cache()
@@ -338,6 +343,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     ctx = aexq.Context(0)
+    if args.decode_only:
+        print(json.dumps(config3(torch, aexq, ctx, steps=max(args.steps, 10))), flush=True)
+        return
     if args.calib:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
