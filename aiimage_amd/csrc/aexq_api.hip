@@ -910,6 +910,11 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     tiles_total += (int)add;
   }
   p.total_tiles = tiles_total;
+  // M = 1 RMSNorm-in over one activation row (not batched; a group shares x):
+  // each workgroup stages the normalised row once in LDS (K <= 8192 always
+  // holds there)
+  if (plan->kind == kPlanStream && M == 1 && xv.batch == 1 && K <= 8192 && (p.flags & kFlagRms))
+    p.flags |= kFlagXShared;
   plan->x_f32 = xv.dtype == AEXQ_DTYPE_F32;
   plan->x_batch = xv.batch;
   plan->x_rstride_in = xv.rstride;

@@ -20,6 +20,7 @@ enum : int {
   kFlagAlphaIn = 8,    // alpha * (beta*C + sum) (Pack4 linear); else beta*C + alpha*sum (tiled)
   kFlagScaleF16 = 16,  // scales are fp16 (else fp32)
   kFlagXf32 = 32,      // activations fp32 (generic kernel only)
+  kFlagXShared = 64,   // M = 1 streaming RMSNorm-in: every tile multiplies the same row
 };
 
 // Scale granularity of a streaming kernel: one per row (Q8), per 16 codes
@@ -98,6 +99,9 @@ const QmvEntry* qmv_table_q4(int* count);
 const QmvEntry* qmv_find(const QmvConfig& cfg);
 // resident workgroups of an entry per CU (occupancy query, cached)
 int qmv_blocks_per_cu(const QmvEntry* e);
+// Dynamic LDS of a streaming launch with kFlagXShared: the fp16 activation row
+// and one fp32 partial per wave.
+inline size_t qmv_stage_bytes(int k) { return (((size_t)k * 2 + 15) & ~(size_t)15) + kWaves * 4; }
 hipError_t qmv_launch(const QmvEntry* e, const QmvParams& p, int grid, hipStream_t stream);
 
 // Small-M MFMA kernel registry (aexq_qmm.hip): rows M <= 64 per launch.

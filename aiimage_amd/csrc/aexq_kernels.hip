@@ -398,7 +398,9 @@ int qmv_blocks_per_cu(const QmvEntry* e) {
 
 hipError_t qmv_launch(const QmvEntry* e, const QmvParams& p, int grid, hipStream_t stream) {
   if (!e) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL(e->fn, dim3(grid), dim3(kThreads), 0, stream, p);
+  // a shared activation row is staged once per workgroup in dynamic LDS
+  const size_t lds = (p.flags & kFlagXShared) ? qmv_stage_bytes(p.k) : 0;
+  hipLaunchKernelGGL(e->fn, dim3(grid), dim3(kThreads), lds, stream, p);
   return hipGetLastError();
 }
 

@@ -267,6 +267,105 @@ struct Qmv {
     }
   }
 
+  // M = 1 RMSNorm-in with one activation row for the whole launch
+  // (kFlagXShared): the workgroup's 256 threads stage fp16(x * gamma) into
+  // LDS, 8 elements each per pass, and reduce sum(x^2) through LDS -- one
+  // memory round trip and one barrier for every wave of the workgroup,
+  // instead of each wave walking its chunks' activations and gamma.
+  // stage_issue() issues every pass's x and gamma loads (before the tile's
+  // weight loads, so that waiting for them does not wait for the weights);
+  // stage_finish() forms the row, and returns its factor.  Every thread of
+  // the workgroup calls both.
+  static constexpr int kStagePasses = 4;  // K <= 4 * 256 * 8
+  struct Stage {
+    u32x4 x[kStagePasses];
+    f32x4 g[kStagePasses][2];
+  };
+
+  static __device__ __forceinline__ void stage_issue(const QmvParams& p, Stage& st) {
+    const bool use_gamma = p.gamma != nullptr;
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.mat[0].x, (short)0, p.k * 2, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.gamma, (short)0, use_gamma ? p.k * 4 : 0, kBufferRsrcWord3);
+#pragma unroll
+    for (int it = 0; it < kStagePasses; ++it) {
+      const int e0 = (it * kThreads + (int)threadIdx.x) * 8;  // past K: reads 0
+      st.x[it] =
+          __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, e0 * 2, 0, 0));
+      st.g[it][0] =
+          __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(grs, e0 * 4, 0, 0));
+      st.g[it][1] =
+          __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(grs, e0 * 4 + 16, 0, 0));
+    }
+  }
+
+  static __device__ __forceinline__ float stage_finish(const QmvParams& p, const Stage& st,
+                                                       int lane, int wave) {
+    extern __shared__ __align__(16) uint8_t qmv_stage[];
+    f16* xs = (f16*)qmv_stage;
+    float* red = (float*)(qmv_stage + (((size_t)p.k * 2 + 15) & ~(size_t)15));
+    const bool use_gamma = p.gamma != nullptr;
+    float ss = 0.0f;
+#pragma unroll
+    for (int it = 0; it < kStagePasses; ++it) {
+      const int e0 = (it * kThreads + (int)threadIdx.x) * 8;
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 h = as_h2(st.x[it][e]);
+        const float a = (float)h[0], b = (float)h[1];
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+        const float g0 = use_gamma ? st.g[it][e / 2][2 * (e % 2)] : 1.0f;
+        const float g1 = use_gamma ? st.g[it][e / 2][2 * (e % 2) + 1] : 1.0f;
+        const f16x2 r = {(f16)(a * g0), (f16)(b * g1)};
+        o[e] = as_u(r);
+      }
+      if (e0 < p.k) *(u32x4*)(xs + e0) = o;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot += red[w];
+    return rsqrtf(fmaxf(tot / (float)p.k + p.eps, 1e-20f));
+  }
+
+  // A wave's activation registers from the staged row.
+  static __device__ __forceinline__ void load_x_staged(const QmvParams& p, int sub, XRegs& xr) {
+    extern __shared__ __align__(16) uint8_t qmv_stage[];
+    const f16* xs = (const f16*)qmv_stage;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ci = sub + c * LPR;
+      uint32_t raw[XW];
+      if (ci < p.chunks) {
+        const u32x4* src = (const u32x4*)(xs + ci * (XW * 2));
+#pragma unroll
+        for (int v = 0; v < XW / 4; ++v) {
+          const u32x4 t = src[v];
+          raw[4 * v + 0] = t[0];
+          raw[4 * v + 1] = t[1];
+          raw[4 * v + 2] = t[2];
+          raw[4 * v + 3] = t[3];
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < XW; ++d) raw[d] = 0u;
+      }
+      if constexpr (FMT == kQ8) {
+#pragma unroll
+        for (int d = 0; d < XW; ++d) xr[0][c][d] = raw[d];
+      } else {
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          q4_xpairs(raw[4 * d], raw[4 * d + 1], raw[4 * d + 2], raw[4 * d + 3], &xr[0][c][4 * d]);
+      }
+    }
+  }
+
   // Dot products, row reduction, epilogue and store of one tile.
   static __device__ __forceinline__ void compute(const QmvParams& p, const Cursor& cu,
                                                  const Offsets& o, const Buf& buf,
@@ -424,15 +523,32 @@ void qmv_kernel(const QmvParams p) {
     bs[m] = -INFINITY;
   }
 
-  if (t0 < t1) {
-    const typename Q::Offsets o = Q::offsets(p, sub, slot);
-    typename Q::Cursor cu = Q::locate(p, t0);
-    typename Q::Buf A, B;
-    typename Q::XRegs xr;
-    float xinv[MMAX];
-    Q::load(p, cu, o, A, true, slot);
-    const f16* xcur = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
-    Q::load_x(p, xcur, sub, xr, xinv);
+  // a wave without tiles (t0 == t1) still takes part in the staging barrier
+  const bool has_tiles = t0 < t1;
+  const typename Q::Offsets o = Q::offsets(p, sub, slot);
+  typename Q::Cursor cu = Q::locate(p, has_tiles ? t0 : 0);
+  typename Q::Buf A, B;
+  typename Q::XRegs xr;
+  float xinv[MMAX];
+  const f16* xcur = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
+  bool staged = false;
+  if constexpr (MMAX == 1) {
+    if (p.flags & kFlagXShared) {
+      typename Q::Stage st;
+      Q::stage_issue(p, st);
+      __builtin_amdgcn_sched_barrier(0);  // the staging loads go out before the codes
+      Q::load(p, cu, o, A, has_tiles, slot);
+      xinv[0] = Q::stage_finish(p, st, lane, wave);
+      Q::load_x_staged(p, sub, xr);
+      staged = true;
+    }
+  }
+  if (!staged) {
+    Q::load(p, cu, o, A, has_tiles, slot);
+    if (has_tiles) Q::load_x(p, xcur, sub, xr, xinv);
+  }
+
+  if (has_tiles) {
     int t = t0;
     while (true) {
       // Tile t is in A and its activation rows in xr.  Tile t+1's loads are

@@ -146,8 +146,10 @@ def test_small_m_streaming_rms_residual(ctx, aexq, orc, m):
 @pytest.mark.parametrize("bits", [4, 8])
 def test_stacked_batched_x_rms_matches_single(ctx, aexq, orc, monkeypatch, bits):
     """A weight stack with one activation row per copy: each wave re-loads (and
-    re-normalises) x when its tiles cross into the next copy; every copy must
-    equal the single launch on its own x, bit for bit."""
+    re-normalises) x when its tiles cross into the next copy.  Every copy must
+    match the single launch on its own x up to fp16 rounding (a single launch
+    stages its row once per workgroup and reduces sum(x^2) in another order, so
+    1/rms may differ in its last bit), and the oracle to 1e-3."""
     _announce(f"stacked batched x rms bits={bits}")
     from aiimage_amd import synth
     monkeypatch.setenv("AEXQ_QMV_BLOCKS_PER_CU", "1")
@@ -170,7 +172,9 @@ def test_stacked_batched_x_rms_matches_single(ctx, aexq, orc, monkeypatch, bits)
     ctx.linear(st, xd, yd, rmsnorm=True, rms_gamma=gamma, rms_eps=eps)
     torch.cuda.synchronize()
     for c in range(copies):
-        assert torch.equal(out[c * n:(c + 1) * n], singles[c][:n]), c
+        got_c = out[c * n:(c + 1) * n].float().cpu().numpy()
+        one_c = singles[c][:n].float().cpu().numpy()
+        assert normwise(got_c, one_c) <= 2.0 ** -10, c
     xn = orc.rmsnorm(xs.astype(np.float32), eps, synth.rms_gamma(k, 731))
     ref = orc.gemm_gpu_semantics(xn.astype(np.float16).astype(np.float32), wf)
     got = out.cpu().numpy().reshape(copies, n)
