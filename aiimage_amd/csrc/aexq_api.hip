@@ -814,9 +814,19 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   plan->fast = false;
   if (mfma_ok && size_ok) {
     const int mt = M <= 16 ? 1 : 2;
+    // 256-wide K steps whose code fetches cover 128 contiguous bytes of 8 rows
+    // per instruction, where K and the scale layout allow
+    const bool wide = K % 256 == 0 && (fmt == kQ8 || gmode == kG32) &&
+                      getenv("AEXQ_QMM_NARROW") == nullptr;
     const int nt = swiglu ? (mt == 1 ? 2 : 1) : (mt == 1 ? 4 : 2);
-    QmmConfig mc{fmt, gmode, mt, nt, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16};
-    plan->mentry = qmm_find(mc);
+    QmmConfig mc{fmt, gmode, mt, nt, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16, false};
+    if (wide) {
+      QmmConfig wc = mc;
+      wc.wide = true;
+      if (fmt == kQ8 && mt == 1) wc.nt = nt > 1 ? nt / 2 : 1;
+      plan->mentry = qmm_find(wc);
+    }
+    if (!plan->mentry) plan->mentry = qmm_find(mc);
     if (plan->mentry) {
       plan->kind = kPlanMfma;
       plan->rms_prepass = rms_in;
@@ -930,7 +940,9 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     int per_cu = qmm_blocks_per_cu(plan->mentry);
     const char* env = getenv("AEXQ_QMM_BLOCKS_PER_CU");
     if (env && atoi(env) > 0) per_cu = atoi(env);
-    const long long need = ((long long)tiles_total + kWaves - 1) / kWaves;
+    // narrow kernel: a wave per tile; wide kernel: a workgroup per tile
+    const long long need = plan->mentry->cfg.wide ? (long long)tiles_total
+                                                  : ((long long)tiles_total + kWaves - 1) / kWaves;
     const long long cap = (long long)per_cu * ctx->cus;
     plan->grid = (int)(need < cap ? need : cap);
     if (plan->grid < 1) plan->grid = 1;
@@ -1009,10 +1021,11 @@ extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, cons
     if (st)
       snprintf(diag, diag_len, "%s", g_last_error.c_str());
     else if (plan.kind == kPlanMfma)
-      snprintf(diag, diag_len, "kernel=qmm bits=%d mt=%d nt=%d swiglu=%d rms_prepass=%d "
+      snprintf(diag, diag_len, "kernel=qmm bits=%d mt=%d nt=%d swiglu=%d wide=%d rms_prepass=%d "
                "tiles=%d grid=%d mblock=%d",
                w->bits, plan.mentry->cfg.mt, plan.mentry->cfg.nt, (int)plan.mentry->cfg.pair,
-               (int)plan.rms_prepass, plan.p.total_tiles, plan.grid, plan.mblock);
+               (int)plan.mentry->cfg.wide, (int)plan.rms_prepass, plan.p.total_tiles, plan.grid,
+               plan.mblock);
     else
       snprintf(diag, diag_len,
                "kernel=%s bits=%d lpr=%d cpl=%d u=%d mmax=%d swiglu=%d tiles=%d grid=%d",

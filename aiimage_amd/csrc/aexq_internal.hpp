@@ -108,6 +108,7 @@ hipError_t qmv_launch(const QmvEntry* e, const QmvParams& p, int grid, hipStream
 struct QmmConfig {
   int fmt, gmode, mt, nt;
   bool pair, sf16;  // SwiGLU pair; fp16 (else fp32) scales
+  bool wide;        // 256-wide K steps (aexq_qmmw.hpp; K % 256 == 0, Q8 or Q4 group 32)
 };
 struct QmmEntry {
   QmmConfig cfg;
@@ -115,6 +116,7 @@ struct QmmEntry {
   int tn;  // weight rows per tile
 };
 const QmmEntry* qmm_find(const QmmConfig& cfg);
+const QmmEntry* qmmw_table(int* count);  // the wide-step entries (aexq_qmmw.hip)
 int qmm_blocks_per_cu(const QmmEntry* e);
 hipError_t qmm_launch(const QmmEntry* e, const QmvParams& p, int grid, hipStream_t stream);
 // RMSNorm of activation rows into fp16 rows (the M > 1 form of RMSNorm-in):

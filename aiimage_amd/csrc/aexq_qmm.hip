@@ -7,7 +7,8 @@ namespace aexq {
 
 #define QMME(FMT, GM, MT, NT, PAIR, SF16)                                                        \
   QmmEntry {                                                                                    \
-    QmmConfig{FMT, GM, MT, NT, PAIR, SF16}, &qmm_kernel<FMT, GM, MT, NT, PAIR, SF16>, 16 * NT   \
+    QmmConfig{FMT, GM, MT, NT, PAIR, SF16, false}, &qmm_kernel<FMT, GM, MT, NT, PAIR, SF16>,    \
+        16 * NT                                                                                 \
   }
 
 // single weights: 4 blocks at M <= 16, 2 at M <= 32; SwiGLU pairs stream two
@@ -25,24 +26,32 @@ static const QmmEntry kTable[] = {
 static constexpr int kCount = (int)(sizeof(kTable) / sizeof(kTable[0]));
 
 const QmmEntry* qmm_find(const QmmConfig& c) {
-  for (int i = 0; i < kCount; ++i) {
-    const QmmConfig& q = kTable[i].cfg;
+  int nw = 0;
+  const QmmEntry* tw = qmmw_table(&nw);
+  const QmmEntry* t = c.wide ? tw : kTable;
+  const int n = c.wide ? nw : kCount;
+  for (int i = 0; i < n; ++i) {
+    const QmmConfig& q = t[i].cfg;
     if (q.fmt == c.fmt && q.gmode == c.gmode && q.mt == c.mt && q.nt == c.nt &&
         q.pair == c.pair && q.sf16 == c.sf16)
-      return &kTable[i];
+      return &t[i];
   }
   return nullptr;
 }
 
 int qmm_blocks_per_cu(const QmmEntry* e) {
-  static int cache[kCount];
-  const int i = (int)(e - kTable);
-  if (i >= 0 && i < kCount && cache[i] > 0) return cache[i];
+  static int cache[kCount], cache_w[64];
+  int nw = 0;
+  const QmmEntry* tw = qmmw_table(&nw);
+  int* slot = nullptr;
+  if (e >= kTable && e < kTable + kCount) slot = &cache[e - kTable];
+  if (e >= tw && e < tw + nw && e - tw < 64) slot = &cache_w[e - tw];
+  if (slot && *slot > 0) return *slot;
   int blocks = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, e->fn, kThreads, 0) != hipSuccess ||
       blocks <= 0)
     blocks = 1;
-  if (i >= 0 && i < kCount) cache[i] = blocks;
+  if (slot) *slot = blocks;
   return blocks;
 }
 

@@ -1,0 +1,33 @@
+// Instantiations of the wide-step small-M MFMA kernel (aexq_qmmw.hpp) and its
+// table: Q4 with one scale per 32 codes and Q8 with one scale per row, fp16
+// or fp32 scales; MT 16-row activation tiles by NT 16-row weight blocks.
+#include "aexq_qmmw.hpp"
+
+namespace aexq {
+
+#define QMMWE(FMT, MT, NT, PAIR, SF16)                                                        \
+  QmmEntry {                                                                                  \
+    QmmConfig{FMT, FMT == kQ8 ? kGRow : kG32, MT, NT, PAIR, SF16, true},                      \
+        &qmmw_kernel<FMT, MT, NT, PAIR, SF16>, kWaves * 16 * NT                               \
+  }
+
+// Blocks per wave: 4 at M <= 16, 2 at M <= 32, halved for SwiGLU pairs; Q8
+// at M <= 16 half of that (its steps carry twice the code bytes, and the
+// shorter tile measured faster there)
+#define QMMW_Q4(SF16)                                                                         \
+  QMMWE(kQ4, 1, 4, false, SF16), QMMWE(kQ4, 2, 2, false, SF16), QMMWE(kQ4, 1, 2, true, SF16), \
+      QMMWE(kQ4, 2, 1, true, SF16)
+#define QMMW_Q8(SF16)                                                                         \
+  QMMWE(kQ8, 1, 2, false, SF16), QMMWE(kQ8, 2, 2, false, SF16), QMMWE(kQ8, 1, 1, true, SF16), \
+      QMMWE(kQ8, 2, 1, true, SF16)
+
+static const QmmEntry kTableW[] = {QMMW_Q4(true), QMMW_Q4(false), QMMW_Q8(true), QMMW_Q8(false)};
+
+static constexpr int kCountW = (int)(sizeof(kTableW) / sizeof(kTableW[0]));
+
+const QmmEntry* qmmw_table(int* count) {
+  *count = kCountW;
+  return kTableW;
+}
+
+}  // namespace aexq

@@ -1,0 +1,329 @@
+// Small-M (2..32 rows per launch) quantized matmul on gfx950 MFMA, wide-step
+// form: Y[M][N] = X[M][K] W[N][K]^T for Q4 with one scale per 32 codes and
+// Q8 with one scale per row, K a multiple of 256.
+//
+// A workgroup owns a contiguous range of (weight tile of 4 waves x 16 NT
+// rows, 256-wide K step) pairs and walks them with its four waves in step:
+// each wave streams its NT 16-row blocks of the tile, the activation rows of
+// the step (16 MT rows x 256 codes) are loaded once per workgroup into a
+// double-buffered LDS slice that every wave reads its MFMA A fragments from,
+// and one barrier per step publishes the next slice.  The slice's loads are
+// issued before the next step's weight loads, so that barrier never waits on
+// HBM.  Codes are fetched the way HBM serves them best: every load
+// instruction covers 8 rows x 128 contiguous bytes (lane l: row l / 8, bytes
+// 16 (l % 8)); a block then goes through a wave-private LDS buffer laid out
+// so that MFMA lane (n, kb) reads its row's B units for all eight 32-code
+// groups with two (Q4) or four (Q8) 16-byte reads (a wave's LDS operations
+// complete in order, so this needs no barrier).  Codes become exact fp16
+// integers in registers; Q4 scales are applied in fp32 to each group's MFMA
+// result (one group = one MFMA K extent), Q8 row scales once at the end, as
+// in aexq_qmm.hpp.
+#pragma once
+
+#include "aexq_qmm.hpp"
+
+namespace aexq {
+
+template <int FMT, int MT, int NT, bool PAIR, bool SF16>
+struct QmmW {
+  static constexpr int GM = FMT == kQ8 ? kGRow : kG32;
+  using Base = Qmm<FMT, GM, MT, NT, PAIR, SF16>;
+  using Cursor = typename Base::Cursor;  // s = 256-wide K step
+  using Acc = typename Base::Acc;
+  static constexpr int TN = 16 * NT;          // rows of one wave's blocks
+  static constexpr int TNG = kWaves * TN;     // rows of a workgroup tile
+  static constexpr int XRS = 512 + 16;        // LDS activation row stride (256 fp16 + pad)
+  static constexpr int XSL = 16 * MT * XRS;   // LDS bytes of one activation slice
+  static constexpr int XV = 2 * MT;           // 16-byte activation loads per thread per step
+  static constexpr int NW = PAIR ? 2 : 1;
+  static constexpr int RB = FMT == kQ8 ? 256 : 128;  // code bytes of a row per step
+  static constexpr int WI = RB / 64;                 // 16-byte loads per lane per 16-row block
+  static constexpr int RS = RB + 32;                 // LDS row stride (padded against conflicts)
+  static constexpr int BLK = 16 * RS;                // LDS bytes of one 16-row block
+  static constexpr int LDS_WAVE = NW * NT * BLK;
+  static constexpr int SV = FMT == kQ8 ? 0 : (SF16 ? 1 : 2);  // 16-byte scale loads per block
+
+  struct Buf {
+    u32x4 w[NW][NT][WI];
+    u32x4 s[NW][NT][SV > 0 ? SV : 1];
+  };
+
+  static __device__ __forceinline__ Cursor locate(const QmvParams& p, int t) {
+    const int steps = p.k / 256;
+    const int tile = t / steps;
+    int j = 0;
+    for (int i = 1; i < p.nmat; ++i)
+      if (tile >= p.mat[i].tile_base) j = i;
+    const int local = tile - p.mat[j].tile_base;
+    Cursor c;
+    c.j = j;
+    c.b = local / p.mat[j].tiles;
+    c.rt = local - c.b * p.mat[j].tiles;
+    c.s = t - tile * steps;
+    return c;
+  }
+
+  static __device__ __forceinline__ Cursor advance(const QmvParams& p, Cursor c) {
+    if (++c.s == p.k / 256) {
+      c.s = 0;
+      if (++c.rt == p.mat[c.j].tiles) {
+        c.rt = 0;
+        if (++c.b == p.batch) {
+          c.b = 0;
+          ++c.j;
+        }
+      }
+    }
+    return c;
+  }
+
+  // The weight loads of one step for this wave's blocks (rows r0 + [0, TN) of
+  // the workgroup tile), branch-free (buffer resources zero-fill rows past N).
+  static __device__ __forceinline__ void load(const QmvParams& p, const Cursor& cu, int lane,
+                                              int wave, Buf& buf) {
+    const QmvMat& mt = p.mat[cu.j];
+    const int n_l = lane & 15;
+    const int lr = lane >> 3, lc = lane & 7;  // load pattern: row lr (+8), 16-byte column lc
+    constexpr int sb = SF16 ? 2 : 4;
+    const int row_bytes = FMT == kQ8 ? p.k : p.k / 2;
+    const int r0 = cu.rt * TNG + wave * TN;
+    const int rows = mt.n > r0 ? mt.n - r0 : 0;
+    const int wnum = rows > 0 ? rows * row_bytes - cu.s * RB : 0;
+    const int sper = FMT == kQ8 ? 1 : p.groups_per_row;
+    const int snum = rows > 0 ? (rows * sper - cu.s * 8) * sb + 16 : 0;
+#pragma unroll
+    for (int h = 0; h < NW; ++h) {
+      const char* wb = (const char*)(h == 0 ? mt.w : mt.w2) + (cu.b * mt.w_bstride) * 4 +
+                       (long long)r0 * row_bytes + cu.s * RB;
+      const __amdgpu_buffer_rsrc_t wr =
+          __builtin_amdgcn_make_buffer_rsrc((void*)wb, (short)0, wnum, kBufferRsrcWord3);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < WI; ++i) {
+          // Q4: i = row half; Q8: bit 0 = row half, bit 1 = 128-byte half of the step
+          const int rr = 16 * nt + 8 * (i & 1) + lr;
+          const int cb = 128 * (i >> 1) + 16 * lc;
+          buf.w[h][nt][i] = __builtin_bit_cast(
+              u32x4,
+              __builtin_amdgcn_raw_buffer_load_b128(wr, rr * row_bytes + cb, 0, kStreamAux));
+        }
+      if constexpr (SV > 0) {
+        const char* sbp = (const char*)(h == 0 ? mt.s : mt.s2) +
+                          (cu.b * mt.s_bstride + (long long)r0 * sper + cu.s * 8) * sb;
+        const __amdgpu_buffer_rsrc_t sr =
+            __builtin_amdgcn_make_buffer_rsrc((void*)sbp, (short)0, snum, kBufferRsrcWord3);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int v = 0; v < SV; ++v)
+            buf.s[h][nt][v] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           sr, (16 * nt + n_l) * sper * sb + 16 * v, 0, 0));
+      }
+    }
+  }
+
+  // The workgroup's activation slice of one step (16 MT rows x 256 codes):
+  // thread t loads 32 bytes of row t / 16 per 16-row tile (rows past M read 0).
+  static __device__ __forceinline__ void load_x(const QmvParams& p, const Cursor& cu,
+                                                u32x4 (&xv)[XV]) {
+    const QmvMat& mt = p.mat[cu.j];
+    const long long rs2 = p.x_rstride * 2;
+    const char* xb = (const char*)mt.x + cu.b * mt.x_bstride * 2 + cu.s * 512;
+    const int xnum = (int)(p.m * rs2) - cu.s * 512;
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, xnum, kBufferRsrcWord3);
+    const int row = threadIdx.x >> 4, col = (threadIdx.x & 15) * 32;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int v = 0; v < 2; ++v)
+        xv[2 * m + v] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       xr, (16 * m + row) * (int)rs2 + col + 16 * v, 0, 0));
+  }
+
+  static __device__ __forceinline__ void store_x(uint8_t* xs, const u32x4 (&xv)[XV]) {
+    const int row = threadIdx.x >> 4, col = (threadIdx.x & 15) * 32;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int v = 0; v < 2; ++v)
+        *(u32x4*)(xs + (16 * m + row) * XRS + col + 16 * v) = xv[2 * m + v];
+  }
+
+  // Consumes one step: the codes pass through LDS into MFMA layout, then
+  // eight 32-code groups.
+  static __device__ __forceinline__ void compute(const QmvParams& p, int lane, uint8_t* lds,
+                                                 const uint8_t* xs, const Buf& buf, Acc& acc) {
+    const int n_l = lane & 15, kb = lane >> 4;
+    const int lr = lane >> 3, lc = lane & 7;
+    // LDS: row n, group g, 8-code unit kb at n * RS + kb * (RB / 4) + g * (RB / 32)
+    // (Q4: 4 bytes per unit, Q8: 8), so MFMA lane (n, kb) finds its eight
+    // groups' units contiguous
+#pragma unroll
+    for (int h = 0; h < NW; ++h)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        uint8_t* blk = lds + (h * NT + nt) * BLK;
+#pragma unroll
+        for (int i = 0; i < WI; ++i) {
+          const int n = 8 * (i & 1) + lr;
+          const u32x4 c = buf.w[h][nt][i];
+          if constexpr (FMT == kQ8) {
+            // bytes 128 (i >> 1) + 16 lc: group 4 (i >> 1) + lc / 2, units 2 (lc & 1) + {0, 1}
+            const int g = 4 * (i >> 1) + (lc >> 1);
+            const int u0 = 2 * (lc & 1);
+            typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+            *(u32x2v*)(blk + n * RS + u0 * 64 + g * 8) = u32x2v{c[0], c[1]};
+            *(u32x2v*)(blk + n * RS + (u0 + 1) * 64 + g * 8) = u32x2v{c[2], c[3]};
+          } else {
+            // 16 bytes = group lc, units 0..3
+#pragma unroll
+            for (int u = 0; u < 4; ++u) *(uint32_t*)(blk + n * RS + u * 32 + lc * 4) = c[u];
+          }
+        }
+      }
+    __builtin_amdgcn_wave_barrier();
+    // B units of lane (n_l, kb): Q4 one dword per group, Q8 two
+    constexpr int UW = FMT == kQ8 ? 2 : 1;
+    uint32_t unit[NW][NT][8][UW];
+#pragma unroll
+    for (int h = 0; h < NW; ++h)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const uint8_t* src = lds + (h * NT + nt) * BLK + n_l * RS + kb * (RB / 4);
+#pragma unroll
+        for (int v = 0; v < 2 * UW; ++v) {
+          const u32x4 t = *(const u32x4*)(src + 16 * v);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int d = 4 * v + e;  // dword index in the lane's contiguous run
+            unit[h][nt][d / UW][d % UW] = t[e];
+          }
+        }
+      }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      f16x8 bf[NW][NT];
+#pragma unroll
+      for (int h = 0; h < NW; ++h)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          if constexpr (FMT == kQ8) {
+            uint32_t a0, a1, b0, b1;
+            q8_pairs(unit[h][nt][g][0], a0, a1);
+            q8_pairs(unit[h][nt][g][1], b0, b1);
+            bf[h][nt] = pack8(a0, a1, b0, b1);
+          } else {
+            uint32_t e[4];
+            q4_pairs(unit[h][nt][g][0], e);
+            bf[h][nt] = pack8(e[0], e[1], e[2], e[3]);
+          }
+        }
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const u32x4 xv = *(const u32x4*)(xs + (16 * m + n_l) * XRS + 2 * (32 * g + 8 * kb));
+        f16x8 af;
+        if constexpr (FMT == kQ8) {
+          af = __builtin_bit_cast(f16x8, xv);
+        } else {
+          uint32_t xp[4];
+          q4_xpairs(xv[0], xv[1], xv[2], xv[3], xp);
+          af = pack8(xp[0], xp[1], xp[2], xp[3]);
+        }
+#pragma unroll
+        for (int h = 0; h < NW; ++h)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            if constexpr (FMT == kQ8) {
+              acc.v[h][m][nt] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[h][nt], acc.v[h][m][nt], 0, 0, 0);
+            } else {
+              const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+              const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[h][nt], z, 0, 0, 0);
+              float sc;
+              if constexpr (SF16)
+                sc = Base::scale16(buf.s[h][nt][0], g);
+              else
+                sc = as_f32(buf.s[h][nt][g >> 2][g & 3]);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc.v[h][m][nt][r] = fmaf(sc, t[r], acc.v[h][m][nt][r]);
+            }
+          }
+      }
+    }
+  }
+};
+
+template <int FMT, int MT, int NT, bool PAIR, bool SF16>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void qmmw_kernel(const QmvParams p) {
+  using Q = QmmW<FMT, MT, NT, PAIR, SF16>;
+  __shared__ __align__(16) uint8_t lds_all[kWaves][Q::LDS_WAVE];
+  __shared__ __align__(16) uint8_t xs_all[2][Q::XSL];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint8_t* lds = lds_all[wave];
+  // a workgroup's range is whole tiles, so a tile's K steps never split
+  const int steps = p.k / 256;
+  const int t0 = (int)((long long)blockIdx.x * p.total_tiles / gridDim.x) * steps;
+  const int t1 = (int)((long long)(blockIdx.x + 1) * p.total_tiles / gridDim.x) * steps;
+  if (t0 >= t1) return;  // the whole workgroup: no barrier is left waiting
+
+  typename Q::Cursor cu = Q::locate(p, t0);
+  typename Q::Buf A, B;
+  typename Q::Acc acc;
+  u32x4 xv[Q::XV];
+#pragma unroll
+  for (int h = 0; h < Q::NW; ++h)
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc.v[h][m][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // the wave's own cursor for the weight rows and the epilogue
+  auto mine = [&](typename Q::Cursor c) {
+    c.rt = c.rt * kWaves + wave;
+    return c;
+  };
+  Q::load_x(p, cu, xv);
+  Q::load(p, cu, lane, wave, A);
+  Q::store_x(xs_all[0], xv);
+  __syncthreads();
+  int t = t0;
+  int sl = 0;
+  while (true) {
+    // step t: codes in A, activations in slice sl; step t + 1's activation
+    // loads go out first, then its codes into B
+    bool more = t + 1 < t1;
+    typename Q::Cursor nx = more ? Q::advance(p, cu) : cu;
+    Q::load_x(p, nx, xv);
+    Q::load(p, nx, lane, wave, B);
+    __builtin_amdgcn_sched_barrier(0);
+    Q::compute(p, lane, lds, xs_all[sl], A, acc);
+    if (cu.s == steps - 1) Q::Base::finish(p, mine(cu), lane, acc);
+    if (!more) break;
+    Q::store_x(xs_all[sl ^ 1], xv);
+    __syncthreads();
+    ++t;
+    cu = nx;
+    sl ^= 1;
+    more = t + 1 < t1;
+    nx = more ? Q::advance(p, cu) : cu;
+    Q::load_x(p, nx, xv);
+    Q::load(p, nx, lane, wave, A);
+    __builtin_amdgcn_sched_barrier(0);
+    Q::compute(p, lane, lds, xs_all[sl], B, acc);
+    if (cu.s == steps - 1) Q::Base::finish(p, mine(cu), lane, acc);
+    if (!more) break;
+    Q::store_x(xs_all[sl ^ 1], xv);
+    __syncthreads();
+    ++t;
+    cu = nx;
+    sl ^= 1;
+  }
+}
+
+}  // namespace aexq
