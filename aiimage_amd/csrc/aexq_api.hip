@@ -1248,7 +1248,7 @@ static aexq_status attn_prepare(aexq_ctx* ctx, const char* op, int heads_q, int 
   if (splits > attn_max_splits())
     return fail(AEXQ_ERR_UNSUPPORTED, op, "length=%d needs %d splits (at most %d)", length,
                 splits, attn_max_splits());
-  const long long need = (long long)heads_q * splits * (head_dim + 2);
+  const long long need = (long long)heads_q * splits * attn_part_stride();
   HIP_TRY(op, hipSetDevice(ctx->device));
   if (need > ctx->attn_cap) {
     (void)hipFree(ctx->attn_part);
@@ -1262,8 +1262,9 @@ static aexq_status attn_prepare(aexq_ctx* ctx, const char* op, int heads_q, int 
     (void)hipFree(ctx->attn_count);
     ctx->attn_count = nullptr;
     ctx->attn_count_cap = 0;
-    HIP_TRY(op, hipMalloc((void**)&ctx->attn_count, heads_kv * sizeof(int)));
-    HIP_TRY(op, hipMemset(ctx->attn_count, 0, heads_kv * sizeof(int)));
+    const size_t bytes = (size_t)heads_kv * attn_counter_stride() * sizeof(int);
+    HIP_TRY(op, hipMalloc((void**)&ctx->attn_count, bytes));
+    HIP_TRY(op, hipMemset(ctx->attn_count, 0, bytes));
     ctx->attn_count_cap = heads_kv;
   }
   return AEXQ_OK;

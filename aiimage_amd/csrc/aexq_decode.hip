@@ -90,8 +90,10 @@ hipError_t rope_kv_launch(void* q, const void* k, const void* v, void* kcache, v
 // the workgroup -- q, the RoPE tables and new row, then its K and V rows --
 // is issued before the first wait, and q (rotated here when RoPE is fused)
 // meets K after one barrier:
-//   scores   lanes 4i..4i+3 own position p0 + i, each 32 of its 128 dims, for
-//            all G heads (v_dot2 with fp32 accumulation, quad reduction);
+//   scores   lanes 4i..4i+3 own position p0 + i, lane 4i + j the dims
+//            32 r + 8 j + [0, 8) for r < 4 (so one load instruction covers 64
+//            contiguous bytes of 16 rows), for all G heads (v_dot2 with fp32
+//            accumulation, quad reduction);
 //   softmax  max / sum per head over the split's positions (wave shuffles,
 //            then LDS across the 4 waves);
 //   P V      wave w owns positions p0 + 16 w + [0, 16), lane l dimensions
@@ -115,6 +117,11 @@ __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 constexpr int kAttnPos = 64;         // positions per split
+constexpr int kAttnStride = kAttnDim + 4;  // partial row: max, sum, 2 pad, acc[128] (16-byte aligned)
+constexpr int kCoherentAux = 16;     // buffer-load cache policy sc1: read at agent coherence
+// One counter per 256-byte line: atomics to one line are serialized where they
+// are performed (about 15 ns each), so the kv heads' counters do not share one.
+constexpr int kAttnCounterStride = 64;
 constexpr int kAttnMaxSplits = 512;  // combine staging in LDS
 
 template <int G>
@@ -174,7 +181,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     kreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            krs, (p0 + pl) * 256 + qq * 64 + i * 16, 0, 0));
+                                            krs, (p0 + pl) * 256 + i * 64 + qq * 16, 0, 0));
   // V rows: wave w owns positions p0 + 16 w + [0, 16), lane l dimensions 2l, 2l + 1
   uint32_t vreg[16];
 #pragma unroll
@@ -218,43 +225,53 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     // the cache row at `pos` was loaded before it was written: take the new one
     if (p0 + pl == pos) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kreg[i] = *(const u32x4*)&kn[qq * 32 + i * 8];
+      for (int i = 0; i < 4; ++i) kreg[i] = *(const u32x4*)&kn[i * 32 + qq * 8];
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i)
       if (p0 + 16 * wave + i == pos) vreg[i] = *(const uint32_t*)&vn[2 * lane];
   }
 
-  // 3. scores of position p0 + pl for every head
+  // 3. scores of position p0 + pl for every head (quad sums by DPP)
   const bool live = p0 + pl < len;
   float sc[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const u32x4* qv = (const u32x4*)&qs[h][qq * 32];
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const u32x4 qw = qv[i];
+      const u32x4 qw = *(const u32x4*)&qs[h][i * 32 + qq * 8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc = dot2(kreg[i][e], qw[e], acc);
     }
-    acc += __shfl_xor(acc, 1, 64);
-    acc += __shfl_xor(acc, 2, 64);
-    sc[h] = live ? acc * scale : -INFINITY;
+    sc[h] = acc;
   }
-
-  // 4. softmax statistics of the split per head
-  __shared__ float red[kAttnThreads / 64][G];
-  __shared__ float es[G][kAttnPos];
-  float mx[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) sc[h] += dpp<0xB1>(sc[h]);  // quad_perm [1,0,3,2]
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    float m = sc[h];
-    m = fmaxf(m, __shfl_xor(m, 4, 64));
-    m = fmaxf(m, __shfl_xor(m, 8, 64));
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
-    if (lane == 0) red[wave][h] = m;
+    sc[h] += dpp<0x4E>(sc[h]);  // quad_perm [2,3,0,1]
+    sc[h] = live ? sc[h] * scale : -INFINITY;
+  }
+
+  // 4. softmax statistics of the split per head: the 16 positions of a wave
+  // reduce within DPP rows (row_ror 4, 8), then across rows with the lane
+  // shuffles of all heads issued together; the 4 waves meet in LDS
+  __shared__ float red[kAttnThreads / 64][G];
+  __shared__ float es[G][kAttnPos];
+  float mx[G], rr[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    rr[h] = fmaxf(sc[h], dpp<0x124>(sc[h]));
+    rr[h] = fmaxf(rr[h], dpp<0x128>(rr[h]));
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) rr[h] = fmaxf(rr[h], __shfl_xor(rr[h], 16, 64));
+#pragma unroll
+  for (int h = 0; h < G; ++h) rr[h] = fmaxf(rr[h], __shfl_xor(rr[h], 32, 64));
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) red[wave][h] = rr[h];
   }
   __syncthreads();
 #pragma unroll
@@ -265,19 +282,27 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     mx[h] = m;  // finite: every split holds at least one live position
   }
   __syncthreads();
-  float sm[G];
+  float ex[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const float e = live ? __expf(sc[h] - mx[h]) : 0.0f;
-    if (qq == 0) es[h][pl] = e;
-    float s = e;
-    s += __shfl_xor(s, 4, 64);
-    s += __shfl_xor(s, 8, 64);
-    s += __shfl_xor(s, 16, 64);
-    s += __shfl_xor(s, 32, 64);
-    if (lane == 0) red[wave][h] = s;
+    ex[h] = live ? __expf(sc[h] - mx[h]) : 0.0f;
+    rr[h] = ex[h] + dpp<0x124>(ex[h]);
+    rr[h] += dpp<0x128>(rr[h]);
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) rr[h] += __shfl_xor(rr[h], 16, 64);
+#pragma unroll
+  for (int h = 0; h < G; ++h) rr[h] += __shfl_xor(rr[h], 32, 64);
+  if (qq == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) es[h][pl] = ex[h];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) red[wave][h] = rr[h];
   }
   __syncthreads();
+  float sm[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     float s = 0.0f;
@@ -288,7 +313,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
 
   // 5. P V: wave w, dimensions 2 lane and 2 lane + 1 over its 16 positions;
   // the four waves' sums meet in LDS
-  __shared__ float pv[kAttnThreads / 64][G][kAttnDim];
+  __shared__ __align__(16) float pv[kAttnThreads / 32][G][kAttnDim];  // waves here, 8 row groups in the merge
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     float a0 = 0.0f, a1 = 0.0f;
@@ -303,7 +328,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     pv[wave][h][2 * lane + 1] = a1;
   }
   __syncthreads();
-  const long long stride = kAttnDim + 2;
   const int d = t & (kAttnDim - 1), vh = t >> 7;
   if (vh == 0) {
 #pragma unroll
@@ -311,8 +335,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
       float a = 0.0f;
 #pragma unroll
       for (int w = 0; w < kAttnThreads / 64; ++w) a += pv[w][h][d];
-      float* o = part + ((long long)(g * G + h) * splits + c) * stride;
-      store_coherent(o + 2 + d, a);
+      float* o = part + ((long long)(g * G + h) * splits + c) * kAttnStride;
+      store_coherent(o + 4 + d, a);
       if (d == 0) {
         store_coherent(o, mx[h]);
         store_coherent(o + 1, sm[h]);
@@ -327,15 +351,44 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   __shared__ int last;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (t == 0) last = atomicAdd(&counters[g], 1) == splits - 1;
+  if (t == 0) last = atomicAdd(&counters[g * kAttnCounterStride], 1) == splits - 1;
   __syncthreads();
   if (!last) return;
+  // Loads of the merge: the split statistics (row t of the G * splits rows
+  // (head, split) in registers), then the first chunk of accumulator rows, all
+  // in flight together.  Thread (rg = t / 32, dq = t % 32) reads dims 4 dq ..
+  // 4 dq + 3 of splits rg + 8 j of every head; splits past the last one are
+  // sent out of the buffer range, which reads 0.
   __shared__ float cm[G * kAttnMaxSplits];  // split maxima, then weights
   __shared__ float cl[G * kAttnMaxSplits];  // split sums
-  const float* pg = part + (long long)g * G * splits * stride;
-  for (int i = t; i < G * splits; i += kAttnThreads) {
-    cm[i] = load_coherent(pg + (long long)i * stride);
-    cl[i] = load_coherent(pg + (long long)i * stride + 1);
+  const int rows = G * splits;
+  const float* pg = part + (long long)g * rows * kAttnStride;
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)pg, (short)0, rows * kAttnStride * 4, kBufferRsrcWord3);
+  constexpr int JJ = 16 / G;  // accumulator rows per head and thread in one chunk
+  constexpr int kChunk = 8 * JJ;
+  const int dq = t & 31, rg = t >> 5;
+  const float m0 = as_f32(__builtin_amdgcn_raw_buffer_load_b32(prs, t * kAttnStride * 4, 0, kCoherentAux));
+  const float l0 = as_f32(__builtin_amdgcn_raw_buffer_load_b32(prs, (t * kAttnStride + 1) * 4, 0, kCoherentAux));
+  u32x4 av[G][JJ];
+  auto issue = [&](int s0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int j = 0; j < JJ; ++j) {
+        const int s2 = s0 + rg + 8 * j;
+        const int off = s2 < splits ? ((h * splits + s2) * kAttnStride + 4 + 4 * dq) * 4 : 0x7FFFFFF0;
+        av[h][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, kCoherentAux));
+      }
+  };
+  issue(0);
+  if (t < rows) {
+    cm[t] = m0;
+    cl[t] = l0;
+  }
+  for (int i = t + kAttnThreads; i < rows; i += kAttnThreads) {
+    cm[i] = as_f32(__builtin_amdgcn_raw_buffer_load_b32(prs, i * kAttnStride * 4, 0, kCoherentAux));
+    cl[i] = as_f32(__builtin_amdgcn_raw_buffer_load_b32(prs, (i * kAttnStride + 1) * 4, 0, kCoherentAux));
   }
   __syncthreads();
   // per head: M = max m_s (each wave reduces the heads h == wave mod 4)
@@ -343,12 +396,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
   for (int h = wave; h < G; h += kAttnThreads / 64) {
     float m = -INFINITY;
     for (int s2 = lane; s2 < splits; s2 += 64) m = fmaxf(m, cm[h * splits + s2]);
-    m = fmaxf(m, __shfl_xor(m, 1, 64));
-    m = fmaxf(m, __shfl_xor(m, 2, 64));
-    m = fmaxf(m, __shfl_xor(m, 4, 64));
-    m = fmaxf(m, __shfl_xor(m, 8, 64));
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    m = wave_max(m);
     float l = 0.0f;
     for (int s2 = lane; s2 < splits; s2 += 64) {
       const float w = __expf(cm[h * splits + s2] - m);
@@ -362,21 +410,46 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     }
   }
   __syncthreads();
-  // thread t: dimension d of heads vh, vh + 2, ...
-  for (int h = vh; h < G; h += 2) {
-    const float* ph = pg + (long long)h * splits * stride + 2 + d;
-    const float* wh = cm + h * splits;
-    float a = 0.0f;
-#pragma unroll 8
-    for (int s2 = 0; s2 < splits; ++s2)
-      a = fmaf(load_coherent(ph + (long long)s2 * stride), wh[s2], a);
-    out[((long long)g * G + h) * kAttnDim + d] = (f16)(a / fmaxf(hl[h], 1e-20f));
+  float ac[G][4];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ac[h][e] = 0.0f;
+  for (int s0 = 0;;) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int j = 0; j < JJ; ++j) {
+        const int s2 = min(s0 + rg + 8 * j, splits - 1);  // rows past the end loaded 0
+        const float w = cm[h * splits + s2];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ac[h][e] = fmaf(as_f32(av[h][j][e]), w, ac[h][e]);
+      }
+    s0 += kChunk;
+    if (s0 >= splits) break;
+    issue(s0);
   }
-  if (t == 0) counters[g] = 0;  // ready for the next launch
+  // the eight row groups' sums meet in LDS
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const f32x4 v = {ac[h][0], ac[h][1], ac[h][2], ac[h][3]};
+    *(f32x4*)&pv[rg][h][4 * dq] = v;
+  }
+  __syncthreads();
+  for (int i = t; i < G * kAttnDim; i += kAttnThreads) {
+    const int h = i / kAttnDim, dd = i % kAttnDim;
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnThreads / 32; ++w) a += pv[w][h][dd];
+    out[((long long)g * G + h) * kAttnDim + dd] = (f16)(a / fmaxf(hl[h], 1e-20f));
+  }
+  if (t == 0) counters[g * kAttnCounterStride] = 0;  // ready for the next launch
 }
 
 int attn_splits(int len) { return (len + kAttnPos - 1) / kAttnPos; }
 int attn_max_splits() { return kAttnMaxSplits; }
+int attn_part_stride() { return kAttnStride; }
+int attn_counter_stride() { return kAttnCounterStride; }
 
 hipError_t attn_decode_launch(const void* q, const void* kcache, const void* vcache, int hq,
                               int hkv, int cap, int len, float scale, float* part, int* counters,

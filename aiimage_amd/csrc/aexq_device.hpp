@@ -91,6 +91,16 @@ __device__ __forceinline__ float group_sum(float v) {
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
+// Maximum over the 64 lanes, by the same DPP steps as group_sum.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<0x128>(v));  // row_ror:8
+  v = fmaxf(v, dpp<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+
 // Argmax order of the reference scan (MM:645-686: element 0 first, then any
 // later value > best): a NaN at index 0 is never replaced, a NaN elsewhere never
 // wins, ties go to the lower index.  Returns true when (av, ai) beats (bv, bi).

@@ -148,6 +148,8 @@ hipError_t rope_kv_launch(void* q, const void* k, const void* v, void* kcache, v
 // splits of a decode attention over `len` positions, and the most one launch takes
 int attn_splits(int len);
 int attn_max_splits();
+int attn_part_stride();  // fp32 words per (head, split) partial row
+int attn_counter_stride();  // ints between the kv heads' split counters
 // part: hq * splits * (128 + 2) floats; counters: hkv ints, zero before the
 // first launch (every launch leaves them zero).  knew/vnew/cosv/sinv non-null:
 // RoPE of q and of the new k row plus the K/V append at position len - 1.

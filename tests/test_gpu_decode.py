@@ -51,10 +51,15 @@ def f16(a):
     return np.asarray(a, np.float64).astype(np.float16).astype(np.float32)
 
 
-@pytest.mark.parametrize("hq,hkv,length,cap", [(16, 4, 41, 64), (16, 4, 2048, 2048), (8, 8, 5, 16),
-                                               (16, 2, 97, 128)])
-def test_rope_kv_append_attention(ctx, aexq, orc, hq, hkv, length, cap):
-    _announce(f"rope+attention hq={hq} hkv={hkv} len={length}")
+@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("hq,hkv,length,cap", [
+    (16, 4, 41, 64), (16, 4, 2048, 2048), (8, 8, 5, 16), (16, 2, 97, 128),
+    # merges over several chunks of split rows, more than one row of statistics per thread
+    (16, 4, 8192, 8192), (16, 2, 4100, 4160), (8, 8, 9000, 9000)])
+def test_rope_kv_append_attention(ctx, aexq, orc, hq, hkv, length, cap, fused):
+    """RoPE + KV append + attention, as two launches or fused in one; the
+    fused kernel rotates q in LDS and leaves the caller's q as it was."""
+    _announce(f"rope+attention hq={hq} hkv={hkv} len={length} fused={fused}")
     d = 128
     pos = length - 1
     rng = np.random.default_rng(length + hq)
@@ -69,13 +74,20 @@ def test_rope_kv_append_attention(ctx, aexq, orc, hq, hkv, length, cap):
     tcos, tsin = torch.as_tensor(cos_t).cuda(), torch.as_tensor(sin_t).cuda()
     out = torch.zeros(hq * d, dtype=torch.float16, device="cuda")
     scale = 1.0 / np.sqrt(d)
-    ctx.rope_kv_append(tq, tk, tv, tkc, tvc, hq, hkv, d, cap, pos, tcos, tsin)
-    ctx.attention_decode(tq, tkc, tvc, hq, hkv, d, cap, length, scale, out)
+    if fused:
+        ctx.attention_decode_rope(tq, tk, tv, tkc, tvc, hq, hkv, d, cap, length, tcos, tsin,
+                                  scale, out)
+    else:
+        ctx.rope_kv_append(tq, tk, tv, tkc, tvc, hq, hkv, d, cap, pos, tcos, tsin)
+        ctx.attention_decode(tq, tkc, tvc, hq, hkv, d, cap, length, scale, out)
     torch.cuda.synchronize()
     # oracle: rotate, round to the fp16 the device stores, append, attend
     q_r = f16(orc.rope_rotate_half(q.astype(np.float32), cos_t, sin_t))
     k_r = f16(orc.rope_rotate_half(k.astype(np.float32), cos_t, sin_t))
-    assert normwise(tq.cpu().numpy().reshape(hq, d), q_r) <= 1e-3
+    if fused:
+        assert np.array_equal(tq.cpu().numpy().reshape(hq, d), q)
+    else:
+        assert normwise(tq.cpu().numpy().reshape(hq, d), q_r) <= 1e-3
     kc_ref = kc.astype(np.float32).copy()
     vc_ref = vc.astype(np.float32).copy()
     kc_ref[:, pos] = k_r
