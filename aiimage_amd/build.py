@@ -14,7 +14,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libaexq.so")
-SOURCES = ["aexq_qmv_q8.hip", "aexq_qmv_q4.hip", "aexq_qmm.hip", "aexq_qmmw.hip", "aexq_kernels.hip",
+SOURCES = ["aexq_qmv_q8.hip", "aexq_qmv_q4.hip", "aexq_qmm.hip", "aexq_qmmw.hip", "aexq_qgemm.hip",
+           "aexq_kernels.hip",
            "aexq_decode.hip", "aexq_api.hip"]
 ARCH = "gfx950"
 

@@ -623,13 +623,14 @@ static aexq_status view_tensor(const aexq_tensor* t, const char* op, const char*
 // ---------------------------------------------------------------------------
 // strict plan
 // ---------------------------------------------------------------------------
-enum PlanKind : int { kPlanGeneric = 0, kPlanStream = 1, kPlanMfma = 2 };
+enum PlanKind : int { kPlanGeneric = 0, kPlanStream = 1, kPlanMfma = 2, kPlanGemm = 3 };
 
 struct Plan {
   int kind = kPlanGeneric;
   bool fast = false;                 // streaming matvec kernel
   const QmvEntry* entry = nullptr;   // streaming kernel
   const QmmEntry* mentry = nullptr;  // MFMA kernel
+  const QgemmEntry* gentry = nullptr;  // tiled GEMM (M > 32)
   int fmt = kQ8;
   int rows_per_tile = 0;
   QmvParams p{};
@@ -812,7 +813,19 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   const bool size_ok = (long long)w0->n * K * w0->bits / 8 < (1LL << 30);
   plan->fmt = fmt;
   plan->fast = false;
-  if (mfma_ok && size_ok) {
+  // M > 32: the tiled GEMM (every row of a weight tile per workgroup pass),
+  // 64-wide K steps, fp16 activation rows 16-byte aligned
+  const bool gemm_ok = M > 32 && K % 64 == 0 && (fmt == kQ8 || w0->block % 32 == 0) &&
+                       (rms_in || x_ok) && getenv("AEXQ_QGEMM_OFF") == nullptr;
+  if (gemm_ok && size_ok) {
+    QgemmConfig gc{fmt, M <= 64 ? 64 : 128, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16};
+    plan->gentry = qgemm_find(gc);
+    if (plan->gentry) {
+      plan->kind = kPlanGemm;
+      plan->rms_prepass = rms_in;
+    }
+  }
+  if (plan->kind != kPlanGemm && mfma_ok && size_ok) {
     const int mt = M <= 16 ? 1 : 2;
     // 256-wide K steps whose code fetches cover 128 contiguous bytes of 8 rows
     // per instruction, where K and the scale layout allow
@@ -833,7 +846,7 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       plan->mblock = 16 * mt;
     }
   }
-  if (plan->kind != kPlanMfma && chunked && group_ok && x_ok && m_ok && rms_ok && size_ok &&
+  if (plan->kind != kPlanMfma && plan->kind != kPlanGemm && chunked && group_ok && x_ok && m_ok && rms_ok && size_ok &&
       chunks > 0) {
     const int mmax = M == 1 ? 1 : 8;
     int lpr = 0, cpl = 0;
@@ -850,7 +863,9 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       if (plan->fast) plan->kind = kPlanStream;
     }
   }
-  if (plan->kind == kPlanMfma) {
+  if (plan->kind == kPlanGemm) {
+    plan->rows_per_tile = qgemm_rows_per_tile(swiglu);
+  } else if (plan->kind == kPlanMfma) {
     plan->rows_per_tile = plan->mentry->tn;
   } else if (plan->fast) {
     plan->rows_per_tile = plan->entry->rw;
@@ -930,13 +945,19 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   plan->x_rstride_in = xv.rstride;
   plan->x_bstride_in = xv.batch == 1 ? 0 : xv.bstride;
   plan->ysz = yv[0].dtype == AEXQ_DTYPE_F32 ? 4 : 2;
-  if (plan->kind == kPlanMfma) {
+  if (plan->kind == kPlanMfma || plan->kind == kPlanGemm) {
     p.flags &= ~kFlagRms;  // normalised by the pre-pass
     if (plan->rms_prepass) {
       // the scratch rows: [x batch][M][K] fp16 (pointer bound at launch)
       p.x_rstride = K;
       for (int i = 0; i < count; ++i) p.mat[i].x_bstride = xv.batch == 1 ? 0 : (long long)M * K;
     }
+  }
+  if (plan->kind == kPlanGemm) {
+    const int bm = plan->gentry->cfg.bm;
+    plan->mblock = bm;
+    plan->grid = (int)(((long long)tiles_total + 7) / 8 * 8 * ((M + bm - 1) / bm));
+  } else if (plan->kind == kPlanMfma) {
     int per_cu = qmm_blocks_per_cu(plan->mentry);
     const char* env = getenv("AEXQ_QMM_BLOCKS_PER_CU");
     if (env && atoi(env) > 0) per_cu = atoi(env);
@@ -984,6 +1005,11 @@ static aexq_status launch_mfma(aexq_ctx* ctx, Plan& plan, const char* op) {
     if (e != hipSuccess) return hip_fail(e, op, "rmsnorm pre-pass launch");
     for (int i = 0; i < p.nmat; ++i) p.mat[i].x = ctx->act_scratch;
   }
+  if (plan.kind == kPlanGemm) {
+    hipError_t e = qgemm_launch(plan.gentry, p, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, op, "gemm kernel launch");
+    return AEXQ_OK;
+  }
   const int ysz = plan.ysz;
   for (int m0 = 0; m0 < M; m0 += plan.mblock) {
     QmvParams q = p;
@@ -1003,7 +1029,7 @@ static aexq_status launch_mfma(aexq_ctx* ctx, Plan& plan, const char* op) {
 
 static aexq_status launch_plan(aexq_ctx* ctx, Plan& plan, const char* op) {
   HIP_TRY(op, hipSetDevice(ctx->device));
-  if (plan.kind == kPlanMfma) return launch_mfma(ctx, plan, op);
+  if (plan.kind == kPlanMfma || plan.kind == kPlanGemm) return launch_mfma(ctx, plan, op);
   hipError_t e = plan.fast ? qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream)
                            : generic_launch(plan.fmt, plan.p, plan.grid, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, op, "kernel launch");
@@ -1020,6 +1046,10 @@ extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, cons
   if (diag && diag_len) {
     if (st)
       snprintf(diag, diag_len, "%s", g_last_error.c_str());
+    else if (plan.kind == kPlanGemm)
+      snprintf(diag, diag_len, "kernel=qgemm bits=%d bm=%d swiglu=%d rms_prepass=%d tiles=%d grid=%d",
+               w->bits, plan.gentry->cfg.bm, (int)plan.gentry->cfg.pair, (int)plan.rms_prepass,
+               plan.p.total_tiles, plan.grid);
     else if (plan.kind == kPlanMfma)
       snprintf(diag, diag_len, "kernel=qmm bits=%d mt=%d nt=%d swiglu=%d wide=%d rms_prepass=%d "
                "tiles=%d grid=%d mblock=%d",

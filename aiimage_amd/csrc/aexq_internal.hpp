@@ -119,6 +119,21 @@ const QmmEntry* qmm_find(const QmmConfig& cfg);
 const QmmEntry* qmmw_table(int* count);  // the wide-step entries (aexq_qmmw.hip)
 int qmm_blocks_per_cu(const QmmEntry* e);
 hipError_t qmm_launch(const QmmEntry* e, const QmvParams& p, int grid, hipStream_t stream);
+// Tiled GEMM for M > 32 rows (aexq_qgemm.hip): K % 64 == 0, Q8 or Q4 with a
+// scale group that is a multiple of 32, fp16 activation rows 16-byte aligned.
+// Tiles are 128 weight rows (64 output columns for a SwiGLU pair) by bm rows.
+struct QgemmConfig {
+  int fmt, bm;
+  bool pair, sf16;
+};
+typedef void (*QgemmFn)(const QmvParams, int);
+struct QgemmEntry {
+  QgemmConfig cfg;
+  QgemmFn fn;
+};
+const QgemmEntry* qgemm_find(const QgemmConfig& cfg);
+int qgemm_rows_per_tile(bool pair);
+hipError_t qgemm_launch(const QgemmEntry* e, const QmvParams& p, hipStream_t stream);
 // RMSNorm of activation rows into fp16 rows (the M > 1 form of RMSNorm-in):
 // out[b][m][k] = fp16(x * rsqrt(max(mean(x^2) + eps, 1e-20)) * gamma[min(k, size-1)])
 hipError_t rmsnorm_rows_launch(const void* x, int x_f32, long long x_rstride, long long x_bstride,

@@ -1,0 +1,42 @@
+// Instantiations of the tiled quantized GEMM (aexq_qgemm.hpp) and its table:
+// Q8 with one scale per row and Q4 with one scale per multiple of 32 codes,
+// fp16 or fp32 scales, single weights or SwiGLU pairs, 64- or 128-row
+// activation tiles.
+#include "aexq_qgemm.hpp"
+
+namespace aexq {
+
+#define QGE(FMT, BM, PAIR, SF16) \
+  QgemmEntry { QgemmConfig{FMT, BM, PAIR, SF16}, &qgemm_kernel<FMT, BM, PAIR, SF16> }
+
+#define QG_BM(FMT, BM) \
+  QGE(FMT, BM, false, true), QGE(FMT, BM, false, false), QGE(FMT, BM, true, true), \
+      QGE(FMT, BM, true, false)
+
+static const QgemmEntry kTableG[] = {QG_BM(kQ4, 64), QG_BM(kQ4, 128), QG_BM(kQ8, 64),
+                                     QG_BM(kQ8, 128)};
+
+static constexpr int kCountG = (int)(sizeof(kTableG) / sizeof(kTableG[0]));
+
+const QgemmEntry* qgemm_find(const QgemmConfig& c) {
+  for (int i = 0; i < kCountG; ++i) {
+    const QgemmConfig& q = kTableG[i].cfg;
+    if (q.fmt == c.fmt && q.bm == c.bm && q.pair == c.pair && q.sf16 == c.sf16)
+      return &kTableG[i];
+  }
+  return nullptr;
+}
+
+int qgemm_rows_per_tile(bool pair) { return pair ? 64 : 128; }
+
+hipError_t qgemm_launch(const QgemmEntry* e, const QmvParams& p, hipStream_t stream) {
+  if (!e) return hipErrorInvalidConfiguration;
+  const int mtiles = (p.m + e->cfg.bm - 1) / e->cfg.bm;
+  const long long groups = (p.total_tiles + 7) / 8;
+  const long long grid = groups * 8 * mtiles;
+  if (grid <= 0 || grid > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(e->fn, dim3((unsigned)grid), dim3(kThreads), 0, stream, p, mtiles);
+  return hipGetLastError();
+}
+
+}  // namespace aexq

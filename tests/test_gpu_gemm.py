@@ -1,0 +1,213 @@
+"""GPU parity of the tiled GEMM path (M > 32 activation rows, aexq_qgemm.hpp)
+against the CPU oracle, through the C ABI.
+
+Bars as in the other parity tests: normwise max|y - r| / max|r| <= 1e-3 of the
+float64 oracle for fp16 outputs, 1e-5 for fp32 outputs; stacked weight copies
+equal the single launch bit for bit.  The dequantised weight inside the GEMM is
+exactly float(q) * scale (codes as exact fp16 integers, scales applied in fp32),
+so fp32 outputs carry only fp32 summation-order differences.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+TOL32 = 1e-5
+
+
+def _announce(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def aexq():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from aiimage_amd import aexq as mod
+    return mod
+
+
+@pytest.fixture(scope="module")
+def ctx(aexq):
+    c = aexq.Context(0)
+    yield c
+    torch.cuda.synchronize()
+    c.close()
+
+
+def normwise(y, r):
+    y = np.asarray(y, np.float64)
+    r = np.asarray(r, np.float64)
+    return float(np.max(np.abs(y - r)) / max(np.max(np.abs(r)), 1e-30))
+
+
+def dev(a, dtype=None):
+    t = torch.as_tensor(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def _weight(ctx, aexq, orc, bits, n, k, seed, group=32, scale_f16=True, code=1):
+    """Device weight and its float64 dequantisation by the oracle."""
+    from aiimage_amd import synth
+    sdt = np.float16 if scale_f16 else np.float32
+    odt = orc.SCALE_F16 if scale_f16 else orc.SCALE_F32
+    if bits == 8:
+        words, scales, _ = synth.q8_weights(n, k, seed, scale_dtype=sdt)
+        w = ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
+        return w, orc.dequant_q8(words, scales, n, k, scale_dtype=odt)
+    words, scales, _ = synth.q4_weights(n, k, seed, group=group, code=code, scale_dtype=sdt)
+    w = ctx.weight(aexq.QuantizedTensor(n * k, group, words, scales, bits=4, nibble_code=code),
+                   n, k)
+    return w, orc.dequant_q4(words, scales, n, k, group, nibble_code=code, scale_dtype=odt)
+
+
+@pytest.mark.parametrize("bits,group,scale_f16,n,k,m,y32", [
+    (4, 32, True, 3072, 1024, 64, False),    # q/k/v grouped shape, one 64-row tile
+    (4, 32, True, 1024, 3584, 512, False),   # down_proj at M = 512
+    (8, 0, True, 1024, 2048, 512, False),    # Q8 o_proj at M = 512
+    (8, 0, False, 1000, 1088, 200, True),    # ragged N and M, K = 17 steps (not a multiple of 128)
+    (4, 64, False, 520, 1024, 97, True),     # one scale per 64 codes, fp32 scales
+    (4, 32, True, 130, 64, 33, True),        # a single K step, 2 rows past a tile
+    (4, 32, False, 256, 512, 129, True),     # reference nibble code below
+])
+def test_gemm_formats(ctx, aexq, orc, bits, group, scale_f16, n, k, m, y32):
+    _announce(f"qgemm q{bits} g={group} f16={scale_f16} n={n} k={k} m={m}")
+    from aiimage_amd import synth
+    code = 0 if (bits == 4 and m == 129) else 1   # two's complement (reference) vs offset-8
+    w, wf = _weight(ctx, aexq, orc, bits, n, k, n + k + m, group=group or k,
+                    scale_f16=scale_f16, code=code)
+    x16 = synth.activations(m, k, m + 5)
+    ydt = torch.float32 if y32 else torch.float16
+    y = aexq.new_activation(m, n, ydt, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    plan = ctx.plan_check(w, xd, yd)
+    assert plan.startswith("kernel=qgemm"), plan
+    ctx.linear(w, xd, yd)
+    torch.cuda.synchronize()
+    stride = aexq.storage_elements(aexq.LAYOUT_PACK4_LINEAR, m, n)
+    got = y.cpu().numpy().astype(np.float64).reshape(m, stride)
+    assert np.all(got[:, n:] == 0)
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    assert normwise(got[:, :n], ref) <= (TOL32 if y32 else TOL)
+
+
+@pytest.mark.parametrize("bits,m,n", [(4, 64, 3584), (4, 150, 1000), (8, 96, 640)])
+def test_gemm_swiglu_rmsnorm(ctx, aexq, orc, bits, m, n):
+    """gate/up with RMSNorm-in (row pre-pass) and SwiGLU-out on the tiled path."""
+    _announce(f"qgemm swiglu rms q{bits} m={m} n={n}")
+    from aiimage_amd import synth
+    k, eps = 1024, 1e-6
+    wg, gf = _weight(ctx, aexq, orc, bits, n, k, 61 + m)
+    wu, uf = _weight(ctx, aexq, orc, bits, n, k, 62 + m)
+    x16 = synth.activations(m, k, 63)
+    gamma = synth.rms_gamma(k, 64)
+    y = aexq.new_activation(m, n, torch.float16, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    kw = dict(rmsnorm=True, rms_gamma=dev(gamma), rms_eps=eps, up=wu)
+    plan = ctx.plan_check(wg, xd, yd, **kw)
+    assert plan.startswith("kernel=qgemm") and "rms_prepass=1" in plan and "swiglu=1" in plan, plan
+    ctx.linear(wg, xd, yd, **kw)
+    torch.cuda.synchronize()
+    xn = orc.rmsnorm(x16.astype(np.float32), eps, gamma).astype(np.float16).astype(np.float32)
+    g = orc.gemm_gpu_semantics(xn, gf)
+    u = orc.gemm_gpu_semantics(xn, uf)
+    ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32)) for r in range(m)])
+    got = y.cpu().numpy().astype(np.float64).reshape(m, -1)[:, :n]
+    assert normwise(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("path", ["qgemm", "qmm"])
+@pytest.mark.parametrize("bcast,layout", [(1, "linear"), (3, "linear"), (4, "tiled")])
+def test_gemm_bias_residual(ctx, aexq, orc, monkeypatch, path, bcast, layout):
+    """alpha/beta/C per row, per element and per column, with the residual, on
+    the tiled GEMM and (switched off) on the 32-row MFMA blocks."""
+    _announce(f"qgemm bias bcast={bcast} layout={layout} path={path}")
+    from aiimage_amd import synth
+    if path == "qmm":
+        monkeypatch.setenv("AEXQ_QGEMM_OFF", "1")
+    n, k, m = 512, 1024, 70
+    w, wf = _weight(ctx, aexq, orc, 8, n, k, 71, scale_f16=False)
+    x16 = synth.activations(m, k, 72)
+    rng = np.random.default_rng(73 + bcast)
+    c = rng.standard_normal({1: m, 3: m * n, 4: n}[bcast]).astype(np.float32)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    lay = aexq.LAYOUT_PACK4_LINEAR if layout == "linear" else aexq.LAYOUT_PACK4_TILED
+    y = aexq.new_activation(m, n, torch.float32, lay)
+    stride = aexq.storage_elements(lay, m, n)
+    rbuf = np.zeros((m, stride), np.float32)
+    rbuf[:, :n] = res
+    rd = dev(rbuf)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, lay)
+    kw = dict(alpha=0.75, beta=1.5, c=dev(c), broadcast_c=bcast,
+              residual=aexq.describe(rd, m, n, lay))
+    assert ctx.plan_check(w, xd, yd, **kw).startswith(f"kernel={path}")
+    ctx.linear(w, xd, yd, **kw)
+    torch.cuda.synchronize()
+    s = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    if bcast == 1:
+        cc = np.repeat(c[:, None], n, 1)
+    elif bcast == 3:
+        cc = c.reshape(m, n)
+    else:
+        cc = np.repeat(c[None, :], m, 0)
+    # Pack4 linear: alpha * (beta C + sum) (MM:1101); tiled: beta C + alpha sum (MM:2301)
+    ref = (0.75 * (1.5 * cc + s) if layout == "linear" else 1.5 * cc + 0.75 * s) + res
+    got = y.cpu().numpy().reshape(m, stride)[:, :n]
+    assert normwise(got, ref) <= TOL32
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gemm_stacked_copies_batched_x_match_single(ctx, aexq, orc, bits):
+    """Size-independent property: a replicated weight stack with one activation
+    matrix per copy gives exactly each copy's single launch."""
+    _announce(f"qgemm stacked q{bits}")
+    from aiimage_amd import synth
+    n, k, m, copies = 640, 1024, 80, 3
+    w, wf = _weight(ctx, aexq, orc, bits, n, k, 81 + bits)
+    xs = synth.activations(copies * m, k, 82)
+    singles = []
+    for c in range(copies):
+        y1 = aexq.new_activation(m, n, torch.float16, aexq.LAYOUT_PACK4_LINEAR)
+        ctx.linear(w, aexq.describe(dev(xs[c * m:(c + 1) * m]), m, k),
+                   aexq.describe(y1, m, n, aexq.LAYOUT_PACK4_LINEAR))
+        singles.append(y1)
+    st = w.replicate(copies)
+    ys = torch.zeros(copies * m * n, dtype=torch.float16, device="cuda")
+    xd = aexq.describe(dev(xs), m, k, batch=copies, batch_stride=m * k)
+    yd = aexq.describe(ys, m, n, aexq.LAYOUT_PACK4_LINEAR, batch=copies, batch_stride=m * n)
+    assert ctx.plan_check(st, xd, yd).startswith("kernel=qgemm")
+    ctx.linear(st, xd, yd)
+    torch.cuda.synchronize()
+    for c in range(copies):
+        assert torch.equal(ys[c * m * n:(c + 1) * m * n], singles[c]), c
+    ref = orc.gemm_gpu_semantics(xs[:m].astype(np.float32), wf)
+    assert normwise(singles[0].cpu().numpy().reshape(m, n), ref) <= TOL
+
+
+def test_gemm_group16_stays_on_mfma_blocks(ctx, aexq, orc):
+    """The reference's shipping Q4 (group 16) is not a tiled-GEMM format: the
+    plan takes the 32-row MFMA blocks and the result still meets the bar."""
+    _announce("qgemm group16 fallback to qmm")
+    from aiimage_amd import synth
+    n, k, m = 512, 1024, 48
+    w, wf = _weight(ctx, aexq, orc, 4, n, k, 91, group=16, scale_f16=False, code=0)
+    x16 = synth.activations(m, k, 92)
+    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    assert ctx.plan_check(w, xd, yd).startswith("kernel=qmm")
+    ctx.linear(w, xd, yd)
+    torch.cuda.synchronize()
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32

@@ -522,7 +522,8 @@ def test_small_m_mfma_config4(ctx, aexq, orc, fmt, n, k, m):
     """Batched decode / short prefill shapes on the MFMA path against the float64 oracle."""
     _announce(f"mfma q{fmt} n={n} k={k} m={m}")
     got, wf, x16, plan = _mm_case(ctx, aexq, orc, fmt, n, k, m, seed=n + k + m)
-    assert plan.startswith("kernel=qmm"), plan
+    # M > 32: the tiled GEMM; M <= 32: one MFMA launch of 16- or 32-row blocks
+    assert plan.startswith("kernel=qgemm" if m > 32 else "kernel=qmm"), plan
     ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
     assert normwise(got, ref) <= TOL
 
@@ -566,11 +567,12 @@ def test_small_m_mfma_swiglu_rmsnorm(ctx, aexq, orc):
 
 
 @pytest.mark.parametrize("bcast", [1, 3])
-def test_small_m_mfma_row_blocks_bias_residual(ctx, aexq, orc, bcast):
+def test_small_m_mfma_row_blocks_bias_residual(ctx, aexq, orc, monkeypatch, bcast):
     """M=33 crosses the 32-row launch blocks: row-indexed C and the residual must
-    follow each block's rows."""
+    follow each block's rows (the tiled GEMM, which would take M > 32, switched off)."""
     _announce(f"mfma m=33 bcast={bcast}")
     from aiimage_amd import synth
+    monkeypatch.setenv("AEXQ_QGEMM_OFF", "1")
     n, k, m = 512, 1024, 33
     words, scales, _ = synth.q8_weights(n, k, 71, scale_dtype=np.float32)
     w = ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
