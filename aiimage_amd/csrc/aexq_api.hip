@@ -818,7 +818,12 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   const bool gemm_ok = M > 32 && K % 64 == 0 && (fmt == kQ8 || w0->block % 32 == 0) &&
                        (rms_in || x_ok) && getenv("AEXQ_QGEMM_OFF") == nullptr;
   if (gemm_ok && size_ok) {
-    QgemmConfig gc{fmt, M <= 64 ? 64 : 128, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16};
+    // Q4 keeps 64-row tiles: its per-group scaling needs the registers a
+    // 128-row tile's accumulators would take
+    int bm = (M <= 64 || fmt == kQ4) ? 64 : 128;
+    const char* benv = getenv("AEXQ_QGEMM_BM");  // tuning override: 64 or 128
+    if (benv && (atoi(benv) == 64 || atoi(benv) == 128)) bm = atoi(benv);
+    QgemmConfig gc{fmt, bm, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16};
     plan->gentry = qgemm_find(gc);
     if (plan->gentry) {
       plan->kind = kPlanGemm;

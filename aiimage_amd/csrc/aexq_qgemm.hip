@@ -1,7 +1,7 @@
 // Instantiations of the tiled quantized GEMM (aexq_qgemm.hpp) and its table:
 // Q8 with one scale per row and Q4 with one scale per multiple of 32 codes,
-// fp16 or fp32 scales, single weights or SwiGLU pairs, 64- or 128-row
-// activation tiles.
+// fp16 or fp32 scales, single weights or SwiGLU pairs; 64-row activation
+// tiles (Q4, Q8) and 128-row tiles (Q8).
 #include "aexq_qgemm.hpp"
 
 namespace aexq {
@@ -13,8 +13,7 @@ namespace aexq {
   QGE(FMT, BM, false, true), QGE(FMT, BM, false, false), QGE(FMT, BM, true, true), \
       QGE(FMT, BM, true, false)
 
-static const QgemmEntry kTableG[] = {QG_BM(kQ4, 64), QG_BM(kQ4, 128), QG_BM(kQ8, 64),
-                                     QG_BM(kQ8, 128)};
+static const QgemmEntry kTableG[] = {QG_BM(kQ4, 64), QG_BM(kQ8, 64), QG_BM(kQ8, 128)};
 
 static constexpr int kCountG = (int)(sizeof(kTableG) / sizeof(kTableG[0]));
 

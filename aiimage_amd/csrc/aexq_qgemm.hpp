@@ -5,15 +5,18 @@
 // A workgroup owns one output tile: BM activation rows by 128 weight rows (a
 // SwiGLU pair: 64 gate rows and the same 64 up rows).  Per 64-wide K step its
 // 256 threads fetch the step's codes once -- each thread the 32 codes of one
-// row that one 16-byte (Q4) or two (Q8) loads bring -- expand them to exact
-// fp16 integers and store them in LDS beside the step's activation tile.  The
-// four waves (2 x 2, each BM/2 rows by 64 weight rows) then run
-// v_mfma_f32_16x16x32_f16 from LDS.  One Q4 scale group is one MFMA K extent,
-// so a group's product is scaled in fp32 into the accumulator and the
-// dequantised weight stays exactly float(q) * scale; Q8 accumulates the whole
-// row in the MFMA and applies its row scale once.  The next step's global
-// loads are in flight while the current step's MFMAs run; LDS is
-// double-buffered with one barrier per step.
+// row that one 16-byte (Q4) or two (Q8) loads bring -- and store them in LDS
+// as they are (in fragment order), beside the step's activation tile.  The four waves (2 x 2, each
+// BM/2 rows by 64 weight rows) read their MFMA B fragments as raw codes (8
+// bytes per lane for Q8, 4 for Q4: LDS carries a half or a quarter of what
+// fp16 weights would), expand them to exact fp16 integers in registers and run
+// v_mfma_f32_16x16x32_f16.  Q4 nibbles expand in (p, p + 4) pair order, so the
+// Q4 activation tile is stored in that order too (the products pair up as in
+// K order).  One Q4 scale group is one MFMA K extent: a group's product is
+// scaled in fp32 into the accumulator, so the dequantised weight stays exactly
+// float(q) * scale; Q8 accumulates the whole row in the MFMA and applies its
+// row scale once.  Global loads run two steps ahead of the MFMAs (two register
+// sets); LDS is double-buffered with one barrier per step.
 //
 // Workgroup b runs on XCD b % 8: the numbering puts the BM-row tiles of one
 // weight tile on one XCD, whose L2 then fetches that weight tile once.
@@ -34,7 +37,15 @@ struct QGemm {
   static constexpr int WM = BM / 2;                  // activation rows per wave
   static constexpr int TM = WM / 16;                 // 16-row A blocks per wave
   static constexpr int TN = 4;                       // 16-row B blocks per wave
-  static constexpr int LS = BK + 8;                  // LDS row stride in halves (144 bytes)
+  static constexpr int LS = BK + 8;                  // activation LDS row stride in halves (144 B)
+  // Code tile in LDS, fragment-major: piece (row, group kk, quarter lk) -- the
+  // P bytes holding codes 32 kk + 8 lk .. + 7 of the row -- sits at
+  //   kk * KB + (row / 16) * 64 P + lk * 16 P + (row % 16) * P,
+  // so the 64 lanes of a fragment read take one contiguous run, and group 1
+  // is skewed by 64 bytes so the two groups' stores fall on different banks.
+  static constexpr int P = FMT == kQ8 ? 8 : 4;
+  static constexpr int KB = (BN / 16) * 64 * P + 64;
+  static constexpr int CB = 2 * KB;  // bytes of one code buffer
   static constexpr int XV = BM * BK / 8 / kThreads;  // 16-byte activation loads per thread
   static constexpr int CV = FMT == kQ8 ? 2 : 1;      // 16-byte code loads per thread
 
@@ -115,45 +126,39 @@ struct QGemm {
     }
   }
 
-  // Stores a step's registers into LDS buffer (xs, ws, ss): the activation
-  // chunks as loaded, the codes as exact fp16 integers in K order.
-  static __device__ __forceinline__ void store(int tid, const Regs& r, f16* xs, f16* ws,
+  // Stores a step's registers into LDS buffer (xs, wc, ss): the activation
+  // chunks (Q4: in the pair order of q4_pairs) and the codes as loaded.
+  static __device__ __forceinline__ void store(int tid, const Regs& r, f16* xs, uint8_t* wc,
                                                float* ss) {
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       const int c = tid + kThreads * v;
-      *(u32x4*)&xs[(c >> 3) * LS + (c & 7) * 8] = r.x[v];
-    }
-    const int row = tid >> 1, sub = tid & 1;
-    f16* dst = ws + row * LS + 32 * sub;
-    if constexpr (FMT == kQ8) {
-#pragma unroll
-      for (int i = 0; i < CV; ++i) {
-        uint32_t e[8];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) q8_pairs(r.c[i][w], e[2 * w], e[2 * w + 1]);
-        *(u32x4*)&dst[16 * i] = u32x4{e[0], e[1], e[2], e[3]};
-        *(u32x4*)&dst[16 * i + 8] = u32x4{e[4], e[5], e[6], e[7]};
+      u32x4 xv = r.x[v];
+      if constexpr (FMT == kQ4) {
+        uint32_t xp[4];
+        q4_xpairs(xv[0], xv[1], xv[2], xv[3], xp);
+        xv = u32x4{xp[0], xp[1], xp[2], xp[3]};
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t q[4];
-        q4_pairs(r.c[0][i], q);  // (n0, n4), (n1, n5), (n2, n6), (n3, n7)
-        u32x4 o;
-        o[0] = __builtin_amdgcn_perm(q[1], q[0], 0x05040100u);  // (n0, n1)
-        o[1] = __builtin_amdgcn_perm(q[3], q[2], 0x05040100u);  // (n2, n3)
-        o[2] = __builtin_amdgcn_perm(q[1], q[0], 0x07060302u);  // (n4, n5)
-        o[3] = __builtin_amdgcn_perm(q[3], q[2], 0x07060302u);  // (n6, n7)
-        *(u32x4*)&dst[8 * i] = o;
-      }
-      ss[row * 2 + sub] = scale_of(r.s, SF16);
+      *(u32x4*)&xs[(c >> 3) * LS + (c & 7) * 8] = xv;
     }
+    const int row = tid >> 1, sub = tid & 1;  // the thread holds group `sub` of the step
+    uint8_t* dst = wc + sub * KB + (row >> 4) * 64 * P + (row & 15) * P;
+#pragma unroll
+    for (int lk = 0; lk < 4; ++lk) {
+      if constexpr (FMT == kQ8) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x4& c = r.c[lk >> 1];
+        *(u32x2*)&dst[lk * 16 * P] = u32x2{c[2 * (lk & 1)], c[2 * (lk & 1) + 1]};
+      } else {
+        *(uint32_t*)&dst[lk * 16 * P] = r.c[0][lk];
+      }
+    }
+    if constexpr (FMT == kQ4) ss[row * 2 + sub] = scale_of(r.s, SF16);
   }
 
-  // The MFMAs of one step from LDS buffer (xs, ws, ss).
+  // The MFMAs of one step from LDS buffer (xs, wc, ss).
   static __device__ __forceinline__ void compute(int lane, int wm, int wn, const f16* xs,
-                                                 const f16* ws, const float* ss,
+                                                 const uint8_t* wc, const float* ss,
                                                  f32x4 (&acc)[TM][TN]) {
     const int l16 = lane & 15, lk = lane >> 4;
 #pragma unroll
@@ -163,8 +168,22 @@ struct QGemm {
       for (int tm = 0; tm < TM; ++tm)
         a[tm] = *(const f16x8*)&xs[(wm * WM + 16 * tm + l16) * LS + 32 * kk + 8 * lk];
 #pragma unroll
-      for (int tn = 0; tn < TN; ++tn)
-        bq[tn] = *(const f16x8*)&ws[(brow(wn, tn) + l16) * LS + 32 * kk + 8 * lk];
+      for (int tn = 0; tn < TN; ++tn) {
+        // codes 32 kk + 8 lk .. + 7 of row brow + l16
+        const uint8_t* src = wc + kk * KB + (brow(wn, tn) >> 4) * 64 * P + lk * 16 * P + l16 * P;
+        if constexpr (FMT == kQ8) {
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 raw = *(const u32x2*)src;
+          uint32_t e0, e1, e2, e3;
+          q8_pairs(raw[0], e0, e1);
+          q8_pairs(raw[1], e2, e3);
+          bq[tn] = pack8(e0, e1, e2, e3);
+        } else {
+          uint32_t e[4];
+          q4_pairs(*(const uint32_t*)src, e);
+          bq[tn] = pack8(e[0], e[1], e[2], e[3]);
+        }
+      }
       if constexpr (FMT == kQ8) {
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
@@ -184,13 +203,7 @@ struct QGemm {
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[tm][tn][r] = fmaf(sc[tn], t[r], acc[tm][tn][r]);
           }
-        // one MFMA, then the four scale FMAs of an earlier one: short-lived products
-#pragma unroll
-        for (int i = 0; i < TM * TN; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);  // one group's fragments live at a time
+        __builtin_amdgcn_sched_barrier(0);  // one group's products live at a time
       }
     }
   }
@@ -250,19 +263,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void qgemm_kernel(const QmvParams p, int mtiles) {
   using G = QGemm<FMT, BM, PAIR, SF16>;
   __shared__ __align__(16) f16 xs[2][BM * G::LS];
-  __shared__ __align__(16) f16 ws[2][G::BN * G::LS];
-  __shared__ float ss[2][G::BN * 2];
+  __shared__ __align__(16) uint8_t ws[2][G::CB];
+  __shared__ float ss[2][FMT == kQ8 ? 1 : G::BN * 2];  // Q4 group scales of a step
   // weight tile tn and row tile tm of this workgroup (see the header)
+  // (readfirstlane: the tile coordinates are workgroup-uniform, so the buffer
+  // resources built from them stay in scalar registers)
   const int bid = blockIdx.x, i = bid >> 3;
-  const int tn = (i / mtiles) * 8 + (bid & 7), tm = i - (i / mtiles) * mtiles;
+  const int tn = __builtin_amdgcn_readfirstlane((i / mtiles) * 8 + (bid & 7));
+  const int tm = __builtin_amdgcn_readfirstlane(i - (i / mtiles) * mtiles);
   if (tn >= p.total_tiles) return;
   int j = 0;
   for (int q = 1; q < p.nmat; ++q)
     if (tn >= p.mat[q].tile_base) j = q;
+  j = __builtin_amdgcn_readfirstlane(j);
   const QmvMat& mt = p.mat[j];
   const int local = tn - mt.tile_base;
-  const int b = local / mt.tiles;
-  const int n0 = (local - b * mt.tiles) * G::NOUT;
+  const int b = __builtin_amdgcn_readfirstlane(local / mt.tiles);
+  const int n0 = __builtin_amdgcn_readfirstlane((local - b * mt.tiles) * G::NOUT);
   const int m0 = tm * BM;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -277,18 +294,27 @@ void qgemm_kernel(const QmvParams p, int mtiles) {
 #pragma unroll
     for (int c = 0; c < G::TN; ++c) acc[a][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  typename G::Regs r;
-  G::load(p, src, 0, tid, r);
-  G::store(tid, r, xs[0], ws[0], ss[0]);
+  // Two register sets rotate: while LDS buffer (st & 1) is consumed, step
+  // st + 1 waits in one set (stored after the MFMAs) and step st + 2 is being
+  // fetched into the other, so a load has two steps of MFMAs to land.
+  typename G::Regs ra, rb;
+  G::load(p, src, 0, tid, ra);
+  if (steps > 1) G::load(p, src, 1, tid, rb);
+  G::store(tid, ra, xs[0], ws[0], ss[0]);
   __syncthreads();
-  for (int st = 0; st < steps; ++st) {
-    const int cur = st & 1;
-    const bool more = st + 1 < steps;
-    if (more) G::load(p, src, st + 1, tid, r);
-    __builtin_amdgcn_sched_barrier(0);  // the next step's loads stay ahead of the MFMAs
-    G::compute(lane, wm, wn, xs[cur], ws[cur], ss[cur], acc);
-    if (more) G::store(tid, r, xs[cur ^ 1], ws[cur ^ 1], ss[cur ^ 1]);
+  for (int st = 0;;) {
+    if (st + 2 < steps) G::load(p, src, st + 2, tid, ra);
+    __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the MFMAs
+    G::compute(lane, wm, wn, xs[0], ws[0], ss[0], acc);
+    if (st + 1 < steps) G::store(tid, rb, xs[1], ws[1], ss[1]);
     __syncthreads();
+    if (++st >= steps) break;
+    if (st + 2 < steps) G::load(p, src, st + 2, tid, rb);
+    __builtin_amdgcn_sched_barrier(0);
+    G::compute(lane, wm, wn, xs[1], ws[1], ss[1], acc);
+    if (st + 1 < steps) G::store(tid, ra, xs[0], ws[0], ss[0]);
+    __syncthreads();
+    if (++st >= steps) break;
   }
   G::finish(p, mt, b, n0, m0, lane, wm, wn, acc);
 }
