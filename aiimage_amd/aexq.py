@@ -23,7 +23,8 @@ import torch
 
 from . import _abi
 from ._abi import (DTYPE_F16, DTYPE_F32, EPI_RESIDUAL_ADD, EPI_RMSNORM_IN, EPI_SWIGLU_OUT,
-                   LAYOUT_LINEAR, LAYOUT_PACK4_LINEAR, LAYOUT_PACK4_TILED, NIBBLE_OFFSET8,
+                   LAYOUT_HEAD_PACKED, LAYOUT_LINEAR, LAYOUT_PACK4_LINEAR, LAYOUT_PACK4_TILED,
+                   NIBBLE_OFFSET8,
                    NIBBLE_TWOS, InvalidOperationError, NotSupportedError, check)
 
 MAX_TEXTURE_SIZE = 16384      # SystemInfo.maxTextureSize of the desktop targets
@@ -43,6 +44,21 @@ def pack4_tiled_storage(rows: int, width: int, max_texture: int = MAX_TEXTURE_SI
     tile_w = min(packs, max(1, min(TILE_WIDTH_LIMIT, max_texture)))
     tile_rows = -(-packs // tile_w)
     return (3, tile_w, max(1, rows) * tile_rows, 1, 4)
+
+
+def head_packed_storage(rows: int, heads: int, head_dim: int) -> tuple:
+    """BufferShape of the attention head-packed layout (GL:1003-1043): {3, head_dim,
+    rows, 1, heads}, stored as ceil(heads/4) slices of rows x head_dim float4 texels."""
+    return (3, head_dim, max(1, rows), 1, heads)
+
+
+def tensor_elements(layout: int, rows: int, width: int, head_dim: int = 0) -> int:
+    """Elements one [rows][width] tensor occupies in storage."""
+    if layout == LAYOUT_HEAD_PACKED:
+        if head_dim <= 0 or width % head_dim:
+            raise InvalidOperationError(_abi.ERR_SHAPE, f"width {width} is not heads x head_dim {head_dim}")
+        return -(-(width // head_dim) // 4) * max(1, rows) * head_dim * 4
+    return storage_elements(layout, rows, width) * rows
 
 
 def storage_elements(layout: int, rows: int, width: int) -> int:
@@ -74,11 +90,16 @@ def _dtype_code(t: torch.Tensor) -> int:
 
 
 def describe(t: torch.Tensor, rows: int, width: int, layout: int = LAYOUT_LINEAR,
-             batch: int = 1, batch_stride: int = 0) -> _abi.Tensor:
-    """aexq_tensor for a device tensor holding `batch` [rows][width] matrices."""
+             batch: int = 1, batch_stride: int = 0, head_dim: int = 0) -> _abi.Tensor:
+    """aexq_tensor for a device tensor holding `batch` [rows][width] matrices
+    (`head_dim` for the attention head-packed layout)."""
     d = _abi.Tensor()
     d.logical = _abi.Shape(2, width, rows, 1, 1)
-    if layout == LAYOUT_LINEAR:
+    if layout == LAYOUT_HEAD_PACKED:
+        if head_dim <= 0 or width % head_dim:
+            raise InvalidOperationError(_abi.ERR_SHAPE, f"width {width} is not heads x head_dim {head_dim}")
+        d.storage = _abi.Shape(*head_packed_storage(rows, width // head_dim, head_dim))
+    elif layout == LAYOUT_LINEAR:
         d.storage = _abi.Shape(2, width, rows, 1, 1)
     elif layout == LAYOUT_PACK4_LINEAR:
         d.storage = _abi.Shape(*pack4_linear_storage(rows, width))
@@ -86,7 +107,7 @@ def describe(t: torch.Tensor, rows: int, width: int, layout: int = LAYOUT_LINEAR
         d.storage = _abi.Shape(*pack4_tiled_storage(rows, width))
     else:
         raise NotSupportedError(_abi.ERR_UNSUPPORTED, f"layout {layout}")
-    need = storage_elements(layout, rows, width) * rows + (batch - 1) * batch_stride
+    need = tensor_elements(layout, rows, width, head_dim) + (batch - 1) * batch_stride
     if t.numel() < need:
         raise InvalidOperationError(_abi.ERR_SHAPE,
                                     f"tensor holds {t.numel()} elements, layout needs {need}")
@@ -100,9 +121,9 @@ def describe(t: torch.Tensor, rows: int, width: int, layout: int = LAYOUT_LINEAR
 
 
 def new_activation(rows: int, width: int, dtype=torch.float16, layout: int = LAYOUT_LINEAR,
-                   device: str = "cuda", batch: int = 1) -> torch.Tensor:
+                   device: str = "cuda", batch: int = 1, head_dim: int = 0) -> torch.Tensor:
     """A zeroed device buffer with the storage of `layout` for [batch][rows][width]."""
-    per = storage_elements(layout, rows, width) * rows
+    per = tensor_elements(layout, rows, width, head_dim)
     return torch.zeros(batch * per, dtype=dtype, device=device)
 
 

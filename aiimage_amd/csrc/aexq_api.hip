@@ -59,6 +59,8 @@ struct aexq_ctx {
   // RMS-normalised activation rows of the MFMA path, grown on demand
   void* act_scratch = nullptr;
   long long act_cap = 0;
+  void* gather_scratch = nullptr;  // dense rows of a head-packed x
+  long long gather_cap = 0;
   // decode attention split partials
   float* attn_part = nullptr;
   long long attn_cap = 0;
@@ -114,6 +116,7 @@ extern "C" void aexq_destroy(aexq_ctx* ctx) {
   (void)hipFree(ctx->part_second);
   (void)hipFree(ctx->logits_scratch);
   (void)hipFree(ctx->act_scratch);
+  (void)hipFree(ctx->gather_scratch);
   (void)hipFree(ctx->attn_part);
   (void)hipFree(ctx->attn_count);
   delete ctx;
@@ -551,6 +554,8 @@ struct TensorView {
   long long bstride = 0;
   int dtype = AEXQ_DTYPE_F16;
   void* data = nullptr;
+  int head_dim = 0;      // attention head-packed layout: head dim and head count
+  int heads = 0;
 };
 
 static bool same_shape(const aexq_shape& a, int dims, int w, int h, int d, int c) {
@@ -611,9 +616,22 @@ static aexq_status view_tensor(const aexq_tensor* t, const char* op, const char*
       v->padded = packs * 4;
       break;
     }
-    case AEXQ_LAYOUT_HEAD_PACKED:
-      return fail(AEXQ_ERR_UNSUPPORTED, op,
-                  "%s layout=HEAD_PACKED | rejectedFallback=attention-head-packed Gemm", name);
+    case AEXQ_LAYOUT_HEAD_PACKED: {
+      // BufferShape {3, head_dim, rows, 1, heads} (GL:1003-1043): ceil(heads/4)
+      // slices of rows x head_dim texels, lane head % 4 (MM:1192-1389)
+      const aexq_shape& S = t->storage;
+      if (S.dims != 3 || S.d != 1 || S.w <= 0 || S.c <= 0 || S.h != H ||
+          (long long)S.w * S.c != W)
+        return fail(AEXQ_ERR_SHAPE, op,
+                    "%s head-packed storage {%d,%d,%d,%d,%d} != {3,head_dim,%d,1,heads} with "
+                    "head_dim*heads=%d",
+                    name, S.dims, S.w, S.h, S.d, S.c, H, W);
+      v->head_dim = S.w;
+      v->heads = S.c;
+      v->rstride = 0;  // not row-major
+      v->padded = (S.c + 3) / 4 * 4 * S.w;
+      break;
+    }
     default:
       return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "%s layout=%d", name, t->layout);
   }
@@ -644,6 +662,11 @@ struct Plan {
   long long x_rstride_in = 0;
   long long x_bstride_in = 0;
   int ysz = 2;
+  // head-packed x: gathered into dense rows (the context's gather scratch) first
+  bool x_gather = false;
+  const void* xg_src = nullptr;
+  int xg_heads = 0, xg_hd = 0, xg_rows = 0, xg_batch = 1, xg_f32 = 0;
+  long long xg_bstride = 0;
 };
 
 // Shape of the streaming kernel for `chunks` 16-byte code chunks per row:
@@ -734,6 +757,24 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   TensorView xv;
   aexq_status st = view_tensor(x, op, "x", &xv);
   if (st) return st;
+  if (xv.head_dim) {
+    if (argmax)
+      return fail(AEXQ_ERR_UNSUPPORTED, op, "LM head x in the head-packed layout");
+    // gathered at launch into dense rows [batch][M][W]; plan over that view
+    plan->x_gather = true;
+    plan->xg_src = xv.data;
+    plan->xg_heads = xv.heads;
+    plan->xg_hd = xv.head_dim;
+    plan->xg_rows = xv.rows;
+    plan->xg_batch = xv.batch;
+    plan->xg_bstride = xv.bstride;
+    plan->xg_f32 = xv.dtype == AEXQ_DTYPE_F32;
+    xv.rstride = xv.width;
+    xv.padded = xv.width;
+    xv.bstride = (long long)xv.rows * xv.width;
+    xv.data = ctx->gather_scratch ? ctx->gather_scratch : (void*)(uintptr_t)256;  // bound at launch
+    xv.head_dim = xv.heads = 0;
+  }
   const int K = w0->k;
   if (xv.width != K)
     return fail(AEXQ_ERR_SHAPE, op, "x width=%d != weight K=%d | layer=Gemm", xv.width, K);
@@ -768,6 +809,10 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   }
   if (argmax && yv[0].dtype != AEXQ_DTYPE_F32)
     return fail(AEXQ_ERR_UNSUPPORTED, op, "LM-head logits must be fp32");
+  if (yv[0].head_dim && (argmax || (a.flags & AEXQ_EPI_RESIDUAL_ADD)))
+    return fail(AEXQ_ERR_UNSUPPORTED, op,
+                "head-packed y with %s | rejectedFallback=attention-head-packed Gemm",
+                argmax ? "the LM head" : "a residual add");
   TensorView rv;
   if (a.flags & AEXQ_EPI_RESIDUAL_ADD) {
     st = view_tensor(a.residual, op, "residual", &rv);
@@ -931,6 +976,7 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     mt.y_bstride = ys[i] ? yv[i].bstride : 0;
     mt.r_bstride = (a.flags & AEXQ_EPI_RESIDUAL_ADD) ? rv.bstride : 0;
     mt.y_rstride = yv[i].rstride;
+    mt.y_hd = yv[i].head_dim;
     mt.n = w->n;
     mt.n_store = ys[i] ? yv[i].padded : w->n;
     mt.tiles = (mt.n_store + plan->rows_per_tile - 1) / plan->rows_per_tile;
@@ -940,6 +986,7 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     tiles_total += (int)add;
   }
   p.total_tiles = tiles_total;
+  p.y_rows = M;
   // M = 1 RMSNorm-in over one activation row (not batched; a group shares x):
   // each workgroup stages the normalised row once in LDS (K <= 8192 always
   // holds there)
@@ -1023,7 +1070,8 @@ static aexq_status launch_mfma(aexq_ctx* ctx, Plan& plan, const char* op) {
     for (int i = 0; i < q.nmat; ++i) {
       QmvMat& mt = q.mat[i];
       mt.x = (const char*)mt.x + (long long)m0 * q.x_rstride * 2;
-      if (mt.y) mt.y = (char*)mt.y + (long long)m0 * mt.y_rstride * ysz;
+      // a head-packed output indexes rows from the tensor's first (out_index)
+      if (mt.y && mt.y_hd == 0) mt.y = (char*)mt.y + (long long)m0 * mt.y_rstride * ysz;
       if (mt.res) mt.res = (const char*)mt.res + (long long)m0 * q.r_rstride * ysz;
     }
     hipError_t e = qmm_launch(plan.mentry, q, plan.grid, ctx->stream);
@@ -1032,8 +1080,33 @@ static aexq_status launch_mfma(aexq_ctx* ctx, Plan& plan, const char* op) {
   return AEXQ_OK;
 }
 
+// Head-packed x: gather it into dense rows in the context's scratch and point
+// the plan's activations there.
+static aexq_status gather_x(aexq_ctx* ctx, Plan& plan, const char* op) {
+  const int width = plan.xg_heads * plan.xg_hd;
+  const long long need =
+      (long long)plan.xg_batch * plan.xg_rows * width * (plan.xg_f32 ? 4 : 2);
+  if (need > ctx->gather_cap) {
+    (void)hipFree(ctx->gather_scratch);
+    ctx->gather_scratch = nullptr;
+    ctx->gather_cap = 0;
+    HIP_TRY(op, hipMalloc(&ctx->gather_scratch, need));
+    ctx->gather_cap = need;
+  }
+  hipError_t e = head_gather_launch(plan.xg_src, plan.xg_f32, plan.xg_rows, plan.xg_heads,
+                                    plan.xg_hd, plan.xg_batch, plan.xg_bstride,
+                                    ctx->gather_scratch, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "head-packed x gather launch");
+  for (int i = 0; i < plan.p.nmat; ++i) plan.p.mat[i].x = ctx->gather_scratch;
+  return AEXQ_OK;
+}
+
 static aexq_status launch_plan(aexq_ctx* ctx, Plan& plan, const char* op) {
   HIP_TRY(op, hipSetDevice(ctx->device));
+  if (plan.x_gather) {
+    aexq_status st = gather_x(ctx, plan, op);
+    if (st) return st;
+  }
   if (plan.kind == kPlanMfma || plan.kind == kPlanGemm) return launch_mfma(ctx, plan, op);
   hipError_t e = plan.fast ? qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream)
                            : generic_launch(plan.fmt, plan.p, plan.grid, ctx->stream);

@@ -168,6 +168,17 @@ __device__ __forceinline__ float scale_of(uint32_t bits, bool f16_scale) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
+// Element index of output (row, n) of matrix mt: row-major, or the attention
+// head-packed layout of MM:1192-1318 -- slice head / 4 of rows x head_dim
+// texels, lane head % 4 -- whose row index counts from the tensor's first row
+// (the host leaves such an output's pointer at row 0 for every row block).
+__device__ __forceinline__ long long out_index(const QmvParams& p, const QmvMat& mt, int row,
+                                               int n) {
+  if (mt.y_hd == 0) return (long long)row * mt.y_rstride + n;
+  const int head = n / mt.y_hd, d = n - head * mt.y_hd;
+  return (((long long)(head >> 2) * p.y_rows + p.m_base + row) * mt.y_hd + d) * 4 + (head & 3);
+}
+
 // Bias, alpha and beta as the reference Gemm resolves them (MM:688-705, 812-820):
 // Pack4-linear output is alpha*(beta*C + sum), tiled output beta*C + alpha*sum.
 __device__ __forceinline__ float gemm_epilogue(const QmvParams& p, int m, int r, float v) {

@@ -38,7 +38,8 @@ struct QmvMat {
   void* y;             // outputs [m][y_rstride]
   const void* res;     // residual [m][r_rstride] (dtype of y) or null
   long long w_bstride, s_bstride, x_bstride, y_bstride, r_bstride;
-  long long y_rstride; // elements between output rows of this matrix
+  long long y_rstride; // elements between output rows of this matrix (row-major outputs)
+  int y_hd;            // head dim of an attention head-packed output; 0: row-major
   int n;               // logical rows (output width N)
   int n_store;         // rows written: n plus zero-filled storage padding
   int tiles;           // row tiles per batch entry
@@ -52,6 +53,7 @@ struct QmvParams {
   int k;               // reduction length (shared)
   int m;               // activation rows
   int m_base;          // first activation row of this launch (row index of bias C)
+  int y_rows;          // rows of a head-packed output tensor (its slices' row count)
   int group;           // scale block (elements); == k for per-row
   int groups_per_row;  // k / group
   int chunks;          // 16-byte code chunks per row
@@ -149,6 +151,10 @@ int logits_argmax_cols_per_wg();
 // codes and fp32 scales of a weight with `count` elements.
 hipError_t record_repack_launch(const void* payload, long long count, int block, int bits,
                                 uint32_t* codes, float* scales, hipStream_t stream);
+// Attention head-packed activation [b][ceil(heads/4)][rows][head_dim][4] ->
+// dense rows [b][rows][heads*head_dim] of the same dtype (MM:1320-1389 reads).
+hipError_t head_gather_launch(const void* src, int f32, int rows, int heads, int head_dim,
+                              int batch, long long src_bstride, void* dst, hipStream_t stream);
 hipError_t dequant_launch(int fmt, const uint32_t* w, const void* s, int scale_f16, int n, int k,
                           int group, float* out, hipStream_t stream);
 hipError_t replicate_launch(const void* src, void* dst, long long bytes, int copies,

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kThreads) void generic_kernel(const QmvParams p) {
       } else {
         v = 0.0f;
       }
-      const long long yi = (long long)m * mt.y_rstride + r;
+      const long long yi = out_index(p, mt, m, r);
       if (yf32)
         ((float*)yb)[yi] = v;
       else
@@ -426,6 +426,42 @@ hipError_t logits_argmax_launch(const float* logits, int m, int n, long long rst
 
 hipError_t argmax_finalize_launch(const ArgmaxParams& a, hipStream_t stream) {
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3(a.m), dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Attention head-packed input (the SDPA context o_proj reads, MM:1320-1389:
+// AexisReadPack4Channel(arr, dim, row, head)) into dense rows: one thread per
+// element of [batch][rows][heads * head_dim].
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kThreads) void head_gather_kernel(const T* src, int rows, int heads,
+                                                               int head_dim, long long sbs,
+                                                               T* dst) {
+  const int width = heads * head_dim;
+  const long long per = (long long)rows * width;
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= per) return;
+  const int b = blockIdx.y;
+  const int row = (int)(i / width), col = (int)(i - (long long)row * width);
+  const int head = col / head_dim, d = col - head * head_dim;
+  dst[b * per + i] =
+      src[b * sbs + (((long long)(head >> 2) * rows + row) * head_dim + d) * 4 + (head & 3)];
+}
+
+hipError_t head_gather_launch(const void* src, int f32, int rows, int heads, int head_dim,
+                              int batch, long long src_bstride, void* dst, hipStream_t stream) {
+  const long long per = (long long)rows * heads * head_dim;
+  const long long blocks = (per + kThreads - 1) / kThreads;
+  if (blocks <= 0 || blocks > 0x7fffffffLL || batch <= 0 || batch > 65535)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)blocks, (unsigned)batch);
+  if (f32)
+    hipLaunchKernelGGL(head_gather_kernel<float>, grid, dim3(kThreads), 0, stream,
+                       (const float*)src, rows, heads, head_dim, src_bstride, (float*)dst);
+  else
+    hipLaunchKernelGGL(head_gather_kernel<f16>, grid, dim3(kThreads), 0, stream,
+                       (const f16*)src, rows, heads, head_dim, src_bstride, (f16*)dst);
   return hipGetLastError();
 }
 

@@ -247,7 +247,7 @@ struct QGemm {
                 v += yf32 ? ((const float*)rb)[ri] : (float)((const f16*)rb)[ri];
               }
             }
-            const long long yi = (long long)m * mt.y_rstride + n;
+            const long long yi = out_index(p, mt, m, n);
             if (yf32)
               ((float*)yb)[yi] = v;
             else

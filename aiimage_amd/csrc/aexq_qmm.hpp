@@ -315,7 +315,7 @@ struct Qmm {
                 v += yf32 ? ((const float*)rb)[ri] : (float)((const f16*)rb)[ri];
               }
             }
-            const long long yi = (long long)row * mt.y_rstride + n;
+            const long long yi = out_index(p, mt, row, n);
             if (yf32)
               ((float*)yb)[yi] = v;
             else

@@ -479,7 +479,7 @@ struct Qmv {
         }
         // one lane per row stores; the lanes of a slot hold identical values
         if (sub == ((u * MMAX + m) & (LPR - 1)) && r < mt.n_store && m < p.m && mt.y) {
-          const long long yi = (long long)m * mt.y_rstride + r;
+          const long long yi = out_index(p, mt, m, r);
           if (yf32)
             ((float*)yb)[yi] = v;
           else

@@ -58,7 +58,12 @@ typedef int aexq_status;
 #define AEXQ_LAYOUT_LINEAR 0       /* LinearMat: [h][w] row-major */
 #define AEXQ_LAYOUT_PACK4_LINEAR 1 /* Pack4 linear: storage {3, ceil(w/4), h, 1, 4} */
 #define AEXQ_LAYOUT_PACK4_TILED 2  /* Pack4 tiled: storage {3, tileWidth, h*tileRows, 1, 4} */
-#define AEXQ_LAYOUT_HEAD_PACKED 3  /* attention head-packed (MM:1192-1389): no kernel yet */
+/* attention head-packed (MM:1192-1389, GL:1003-1043): storage {3, head_dim, h, 1, heads} with
+ * logical w = heads * head_dim; element (row, head * head_dim + d) at
+ * (((head / 4) * h + row) * head_dim + d) * 4 + head % 4, lanes of heads past `heads` zero.
+ * As y (q/k/v projections) the kernels store it directly; as x (o_proj) it is gathered into
+ * dense rows first.  Not with a residual add or the LM head. */
+#define AEXQ_LAYOUT_HEAD_PACKED 3
 
 /* epilogue flags of aexq_linear_args.flags */
 #define AEXQ_EPI_RMSNORM_IN 0x1u   /* x' = fp16(x * rsqrt(max(mean(x^2)+eps,1e-20)) * gamma) (CC:4531-4557) */

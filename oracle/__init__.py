@@ -74,6 +74,8 @@ def _declare(L):
         "orc_rope_table": (None, [i32, i32, ctypes.c_double, P, P]),
         "orc_rope_rotate_half": (None, [P, i32, i32, P, P, P]),
         "orc_sdpa_decode": (None, [P, P, P, i32, i32, i32, i32, f32, P]),
+        "orc_head_pack": (None, [P, i32, i32, i32, P]),
+        "orc_head_unpack": (None, [P, i32, i32, i32, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -331,4 +333,22 @@ def sdpa_decode(q, k, v, scale: float):
     hkv, length, _ = k.shape
     out = np.empty((hq, d), np.float64)
     lib().orc_sdpa_decode(_p(q), _p(k), _p(v), hq, hkv, d, length, scale, _p(out))
+    return out
+
+
+def head_pack(x, heads: int, head_dim: int):
+    """[rows][heads*head_dim] -> the attention head-packed storage (MM:1192-1318),
+    flat float32 of ceil(heads/4) * rows * head_dim * 4 values."""
+    x = _c(x, np.float32)
+    rows = x.shape[0]
+    out = np.empty(((heads + 3) // 4) * rows * head_dim * 4, np.float32)
+    lib().orc_head_pack(_p(x), rows, heads, head_dim, _p(out))
+    return out
+
+
+def head_unpack(buf, rows: int, heads: int, head_dim: int):
+    """Head-packed storage -> [rows][heads*head_dim] (MM:1320-1389 reads)."""
+    buf = _c(buf, np.float32)
+    out = np.empty((rows, heads * head_dim), np.float32)
+    lib().orc_head_unpack(_p(buf), rows, heads, head_dim, _p(out))
     return out

@@ -734,3 +734,33 @@ void orc_sdpa_decode(const float* q, const float* k, const float* v, int heads_q
   }
   free(s);
 }
+
+/*
+ * Attention head-packed texture layout.  The Q/K/V Gemm variants write
+ * _GemmTexOutArr[int3(dim, row, head / 4)] with lane head % 4 set by
+ * AexisWriteLane and the lanes of heads past numHeads left 0
+ * (MM:1192-1318); o_proj reads its input through
+ * AexisReadPack4Channel(arr, dim, row, head) (MM:1320-1389).  Storage is
+ * BufferShape {3, head_dim, rows, 1, heads} (GL:1003-1043): a texture array
+ * of ceil(heads / 4) slices of rows x head_dim float4 texels, so element
+ * (row, head * head_dim + d) of the logical [rows][heads * head_dim] matrix
+ * sits at (((head / 4) * rows + row) * head_dim + d) * 4 + head % 4.
+ * dst holds ceil(heads / 4) * rows * head_dim * 4 values.
+ */
+void orc_head_pack(const float* src, int rows, int heads, int head_dim, float* dst) {
+  const size_t total = (size_t)((heads + 3) / 4) * rows * head_dim * 4;
+  for (size_t i = 0; i < total; ++i) dst[i] = 0.0f;
+  for (int r = 0; r < rows; ++r)
+    for (int h = 0; h < heads; ++h)
+      for (int d = 0; d < head_dim; ++d)
+        dst[(((size_t)(h / 4) * rows + r) * head_dim + d) * 4 + (h % 4)] =
+            src[(size_t)r * heads * head_dim + (size_t)h * head_dim + d];
+}
+
+void orc_head_unpack(const float* src, int rows, int heads, int head_dim, float* dst) {
+  for (int r = 0; r < rows; ++r)
+    for (int h = 0; h < heads; ++h)
+      for (int d = 0; d < head_dim; ++d)
+        dst[(size_t)r * heads * head_dim + (size_t)h * head_dim + d] =
+            src[(((size_t)(h / 4) * rows + r) * head_dim + d) * 4 + (h % 4)];
+}

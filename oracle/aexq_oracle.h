@@ -98,6 +98,9 @@ void orc_rope_rotate_half(const float* x, int heads, int head_dim, const float* 
                           const float* sin_t, float* out);
 void orc_sdpa_decode(const float* q, const float* k, const float* v, int heads_q, int heads_kv,
                      int head_dim, int length, float scale, double* out);
+/* attention head-packed layout (MM:1192-1389): [ceil(heads/4)][rows][head_dim][4] */
+void orc_head_pack(const float* src, int rows, int heads, int head_dim, float* dst);
+void orc_head_unpack(const float* src, int rows, int heads, int head_dim, float* dst);
 
 #ifdef __cplusplus
 }

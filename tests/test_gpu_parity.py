@@ -356,7 +356,8 @@ def test_strict_plan_rejects_without_fallback(ctx, aexq):
     assert ctx.plan_check(w, xd, yd).startswith("kernel=qmv")
     bad = aexq.describe(y, 1, n, aexq.LAYOUT_PACK4_LINEAR)
     bad.layout = _abi.LAYOUT_HEAD_PACKED
-    with pytest.raises(_abi.NotSupportedError):
+    bad.storage = _abi.Shape(3, 48, 1, 1, 4)     # 4 heads of 48 do not make width 256
+    with pytest.raises(_abi.InvalidOperationError):
         ctx.linear(w, xd, bad)
     with pytest.raises(_abi.InvalidOperationError):
         ctx.linear(w, aexq.describe(x, 1, k), aexq.describe(y, 1, n // 2, aexq.LAYOUT_PACK4_LINEAR))

@@ -481,3 +481,27 @@ def test_sdpa_decode_properties(orc):
     o = orc.sdpa_decode(q8, k2, v2, 0.3)
     assert np.all(o[:4] == o[0]) and np.all(o[4:] == o[4]) and not np.allclose(o[0], o[4])
     np.testing.assert_allclose(o[0], orc.sdpa_decode(q8[:1], k2[:1], v2[:1], 0.3)[0], rtol=1e-12)
+
+
+def test_head_packed_layout_positions(orc):
+    """The attention head-packed layout against texel positions worked out by
+    hand from MM:1192-1318 (texel (dim, row, head / 4), lane head % 4, lanes of
+    missing heads 0): 6 heads of 3 dims over 2 rows fill two slices, the second
+    holding heads 4 and 5 in lanes 0 and 1."""
+    rows, heads, hd = 2, 6, 3
+    x = np.arange(1, rows * heads * hd + 1, dtype=np.float32).reshape(rows, heads * hd)
+    buf = orc.head_pack(x, heads, hd)
+    assert buf.size == 48                      # 2 slices x 2 rows x 3 texels x 4 lanes
+    assert buf[0] == x[0, 0]                   # row 0, head 0, d 0: slice 0, texel 0, lane 0
+    assert buf[1] == x[0, 3]                   # row 0, head 1, d 0: lane 1 of that texel
+    assert buf[11] == x[0, 3 * 3 + 2]          # row 0, head 3, d 2: texel 2, lane 3
+    assert buf[18] == x[1, 2 * 3 + 1]          # row 1, head 2, d 1: texel 3 + 1, lane 2
+    assert buf[45] == x[1, 5 * 3 + 2]          # row 1, head 5, d 2: slice 1, texel 3 + 2, lane 1
+    tail = buf[24:].reshape(rows, hd, 4)
+    assert np.all(tail[:, :, 2:] == 0)         # heads 6 and 7 do not exist
+    assert np.array_equal(orc.head_unpack(buf, rows, heads, hd), x)
+    # four heads exactly fill one slice: every lane is a value
+    y = np.arange(1, 3 * 4 * 5 + 1, dtype=np.float32).reshape(3, 20)
+    b2 = orc.head_pack(y, 4, 5)
+    assert b2.size == 60 and np.all(b2 != 0)
+    assert np.array_equal(orc.head_unpack(b2, 3, 4, 5), y)
