@@ -83,6 +83,7 @@ struct aexq_weight {
   long long code_stride = 0;   // bytes between copies
   long long scale_stride = 0;  // bytes between copies
   bool owns = true;
+  bool scales_small = false;   // fp16 scales, all finite with |s| <= 4096 (split-scale GEMM)
 };
 
 static long long round_up(long long v, long long a) { return (v + a - 1) / a * a; }
@@ -200,6 +201,13 @@ static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const 
     const uint32_t* in = (const uint32_t*)packed;
     for (long long i = 0; i < nw; ++i) recoded[(size_t)i] = in[i] ^ flip;
     src = recoded.data();
+  }
+  if (scale_dtype == AEXQ_DTYPE_F16) {
+    // |s| <= 4096 (bits 0x6C00): q * s_hi stays inside fp16 for every code
+    const uint16_t* sb = (const uint16_t*)scales;
+    bool small = true;
+    for (long long i = 0; i < w->scale_count && small; ++i) small = (sb[i] & 0x7FFFu) <= 0x6C00u;
+    w->scales_small = small;
   }
   hipError_t e = hipMemcpy(w->codes, src, w->code_bytes, hipMemcpyHostToDevice);
   if (e == hipSuccess)
@@ -865,10 +873,15 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   if (gemm_ok && size_ok) {
     // Q4 keeps 64-row tiles: its per-group scaling needs the registers a
     // 128-row tile's accumulators would take
-    int bm = (M <= 64 || fmt == kQ4) ? 64 : 128;
+    // Q4 takes 128-row tiles only with split fp16 scales (its per-group
+    // scaling otherwise needs the registers the larger tile's accumulators take)
+    bool small = fmt == kQ4 && w0->scale_dtype == AEXQ_DTYPE_F16 && (!swiglu || a.up->scales_small);
+    for (int i = 0; i < count; ++i) small = small && ws[i]->scales_small;
+    const bool split = small && M > 64 && getenv("AEXQ_QGEMM_NOSPLIT") == nullptr;
+    int bm = (M <= 64 || (fmt == kQ4 && !split)) ? 64 : 128;
     const char* benv = getenv("AEXQ_QGEMM_BM");  // tuning override: 64 or 128
-    if (benv && (atoi(benv) == 64 || atoi(benv) == 128)) bm = atoi(benv);
-    QgemmConfig gc{fmt, bm, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16};
+    if (benv && (atoi(benv) == 64 || atoi(benv) == 128) && !split) bm = atoi(benv);
+    QgemmConfig gc{fmt, bm, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16, split};
     plan->gentry = qgemm_find(gc);
     if (plan->gentry) {
       plan->kind = kPlanGemm;
@@ -1125,9 +1138,10 @@ extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, cons
     if (st)
       snprintf(diag, diag_len, "%s", g_last_error.c_str());
     else if (plan.kind == kPlanGemm)
-      snprintf(diag, diag_len, "kernel=qgemm bits=%d bm=%d swiglu=%d rms_prepass=%d tiles=%d grid=%d",
-               w->bits, plan.gentry->cfg.bm, (int)plan.gentry->cfg.pair, (int)plan.rms_prepass,
-               plan.p.total_tiles, plan.grid);
+      snprintf(diag, diag_len,
+               "kernel=qgemm bits=%d bm=%d swiglu=%d split=%d rms_prepass=%d tiles=%d grid=%d",
+               w->bits, plan.gentry->cfg.bm, (int)plan.gentry->cfg.pair,
+               (int)plan.gentry->cfg.split, (int)plan.rms_prepass, plan.p.total_tiles, plan.grid);
     else if (plan.kind == kPlanMfma)
       snprintf(diag, diag_len, "kernel=qmm bits=%d mt=%d nt=%d swiglu=%d wide=%d rms_prepass=%d "
                "tiles=%d grid=%d mblock=%d",

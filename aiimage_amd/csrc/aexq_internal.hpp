@@ -127,6 +127,7 @@ hipError_t qmm_launch(const QmmEntry* e, const QmvParams& p, int grid, hipStream
 struct QgemmConfig {
   int fmt, bm;
   bool pair, sf16;
+  bool split;  // Q4 fp16 scales folded into B as exact hi + lo parts (|scale| <= 4096)
 };
 typedef void (*QgemmFn)(const QmvParams, int);
 struct QgemmEntry {

@@ -1,26 +1,30 @@
 // Instantiations of the tiled quantized GEMM (aexq_qgemm.hpp) and its table:
 // Q8 with one scale per row and Q4 with one scale per multiple of 32 codes,
 // fp16 or fp32 scales, single weights or SwiGLU pairs; 64-row activation
-// tiles (Q4, Q8) and 128-row tiles (Q8).
+// tiles (Q4, Q8) and 128-row tiles (Q8; Q4 with split fp16 scales).
 #include "aexq_qgemm.hpp"
 
 namespace aexq {
 
-#define QGE(FMT, BM, PAIR, SF16) \
-  QgemmEntry { QgemmConfig{FMT, BM, PAIR, SF16}, &qgemm_kernel<FMT, BM, PAIR, SF16> }
+#define QGE(FMT, BM, PAIR, SF16, SPLIT) \
+  QgemmEntry { QgemmConfig{FMT, BM, PAIR, SF16, SPLIT}, &qgemm_kernel<FMT, BM, PAIR, SF16, SPLIT> }
 
 #define QG_BM(FMT, BM) \
-  QGE(FMT, BM, false, true), QGE(FMT, BM, false, false), QGE(FMT, BM, true, true), \
-      QGE(FMT, BM, true, false)
+  QGE(FMT, BM, false, true, false), QGE(FMT, BM, false, false, false), \
+      QGE(FMT, BM, true, true, false), QGE(FMT, BM, true, false, false)
 
-static const QgemmEntry kTableG[] = {QG_BM(kQ4, 64), QG_BM(kQ8, 64), QG_BM(kQ8, 128)};
+// Q4 with fp16 scales split into B (128-row tiles): single weights and pairs
+static const QgemmEntry kTableG[] = {QG_BM(kQ4, 64), QG_BM(kQ8, 64), QG_BM(kQ8, 128),
+                                     QGE(kQ4, 128, false, true, true),
+                                     QGE(kQ4, 128, true, true, true)};
 
 static constexpr int kCountG = (int)(sizeof(kTableG) / sizeof(kTableG[0]));
 
 const QgemmEntry* qgemm_find(const QgemmConfig& c) {
   for (int i = 0; i < kCountG; ++i) {
     const QgemmConfig& q = kTableG[i].cfg;
-    if (q.fmt == c.fmt && q.bm == c.bm && q.pair == c.pair && q.sf16 == c.sf16)
+    if (q.fmt == c.fmt && q.bm == c.bm && q.pair == c.pair && q.sf16 == c.sf16 &&
+        q.split == c.split)
       return &kTableG[i];
   }
   return nullptr;

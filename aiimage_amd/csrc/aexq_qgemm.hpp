@@ -15,8 +15,14 @@
 // K order).  One Q4 scale group is one MFMA K extent: a group's product is
 // scaled in fp32 into the accumulator, so the dequantised weight stays exactly
 // float(q) * scale; Q8 accumulates the whole row in the MFMA and applies its
-// row scale once.  Global loads run two steps ahead of the MFMAs (two register
-// sets); LDS is double-buffered with one barrier per step.
+// row scale once.  With SPLIT (Q4, fp16 scales of magnitude <= 4096) the scale
+// goes into B instead: s = s_hi + s_lo with s_hi the top 7 significand bits,
+// and q * s_hi, q * s_lo are exact fp16 values (|q| <= 8 has at most 3
+// significant bits), so two MFMAs accumulate x * (q * s) exactly in the fp32
+// accumulator with no per-output scaling -- the B expansion is shared by the
+// tile's BM / 32 A blocks, where the per-group FMAs were per output.  Global
+// loads run two steps ahead of the MFMAs (two register sets); LDS is
+// double-buffered with one barrier per step.
 //
 // Workgroup b runs on XCD b % 8: the numbering puts the BM-row tiles of one
 // weight tile on one XCD, whose L2 then fetches that weight tile once.
@@ -29,8 +35,9 @@
 
 namespace aexq {
 
-template <int FMT, int BM, bool PAIR, bool SF16>
+template <int FMT, int BM, bool PAIR, bool SF16, bool SPLIT>
 struct QGemm {
+  static_assert(!SPLIT || (FMT == kQ4 && SF16), "split scales are for Q4 with fp16 scales");
   static constexpr int BN = 128;                     // weight rows of a tile
   static constexpr int BK = 64;                      // K per step
   static constexpr int NOUT = PAIR ? BN / 2 : BN;    // output columns of a tile
@@ -153,7 +160,16 @@ struct QGemm {
         *(uint32_t*)&dst[lk * 16 * P] = r.c[0][lk];
       }
     }
-    if constexpr (FMT == kQ4) ss[row * 2 + sub] = scale_of(r.s, SF16);
+    if constexpr (SPLIT) {
+      // (s_hi, s_lo): s_hi keeps the top 7 significand bits, s_lo = s - s_hi exactly
+      const f16 sv = __builtin_bit_cast(f16, (uint16_t)r.s);
+      const f16 hi = __builtin_bit_cast(f16, (uint16_t)(r.s & 0xFFF0u));
+      const f16 lo = sv - hi;
+      const f16x2 pr = {hi, lo};
+      ((uint32_t*)ss)[row * 2 + sub] = as_u(pr);
+    } else if constexpr (FMT == kQ4) {
+      ss[row * 2 + sub] = scale_of(r.s, SF16);
+    }
   }
 
   // The MFMAs of one step from LDS buffer (xs, wc, ss).
@@ -167,6 +183,27 @@ struct QGemm {
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
         a[tm] = *(const f16x8*)&xs[(wm * WM + 16 * tm + l16) * LS + 32 * kk + 8 * lk];
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+          const uint8_t* src =
+              wc + kk * KB + (brow(wn, tn) >> 4) * 64 * P + lk * 16 * P + l16 * P;
+          uint32_t e[4];
+          q4_pairs(*(const uint32_t*)src, e);
+          const f16x2 sp = as_h2(((const uint32_t*)ss)[(brow(wn, tn) + l16) * 2 + kk]);
+          const f16x2 shi = {sp[0], sp[0]}, slo = {sp[1], sp[1]};
+          const f16x8 bhi = pack8(as_u(as_h2(e[0]) * shi), as_u(as_h2(e[1]) * shi),
+                                  as_u(as_h2(e[2]) * shi), as_u(as_h2(e[3]) * shi));
+          const f16x8 blo = pack8(as_u(as_h2(e[0]) * slo), as_u(as_h2(e[1]) * slo),
+                                  as_u(as_h2(e[2]) * slo), as_u(as_h2(e[3]) * slo));
+#pragma unroll
+          for (int tm = 0; tm < TM; ++tm) {
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bhi, acc[tm][tn], 0, 0, 0);
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], blo, acc[tm][tn], 0, 0, 0);
+          }
+        }
+        continue;
+      }
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
         // codes 32 kk + 8 lk .. + 7 of row brow + l16
@@ -258,10 +295,10 @@ struct QGemm {
   }
 };
 
-template <int FMT, int BM, bool PAIR, bool SF16>
+template <int FMT, int BM, bool PAIR, bool SF16, bool SPLIT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void qgemm_kernel(const QmvParams p, int mtiles) {
-  using G = QGemm<FMT, BM, PAIR, SF16>;
+  using G = QGemm<FMT, BM, PAIR, SF16, SPLIT>;
   __shared__ __align__(16) f16 xs[2][BM * G::LS];
   __shared__ __align__(16) uint8_t ws[2][G::CB];
   __shared__ float ss[2][FMT == kQ8 ? 1 : G::BN * 2];  // Q4 group scales of a step

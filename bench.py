@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the config-3 decode step timing and print its JSON (for "
                          "profiling that step); not the benchmark line")
+    ap.add_argument("--config4-only", action="store_true",
+                    help="run only the config-4 timings (M in {16, 64, 512}, Q4 and Q8) and print "
+                         "their JSON (for profiling those kernels); not the benchmark line")
     ap.add_argument("--calib", action="store_true",
                     help="also run one 256 MiB fp32 neg kernel (known HBM traffic) to scale "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -345,6 +348,9 @@ def main():
     ctx = aexq.Context(0)
     if args.decode_only:
         print(json.dumps(config3(torch, aexq, ctx, steps=max(args.steps, 10))), flush=True)
+        return
+    if args.config4_only:
+        print(json.dumps(config4(torch, aexq, synth, ctx)), flush=True)
         return
     if args.calib:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")

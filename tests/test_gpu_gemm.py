@@ -211,3 +211,60 @@ def test_gemm_group16_stays_on_mfma_blocks(ctx, aexq, orc):
     torch.cuda.synchronize()
     ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
     assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_gemm_q4_split_scales_exact(ctx, aexq, orc, monkeypatch, split):
+    """Q4 with fp16 scales above 64 rows folds each scale into B as two exact
+    fp16 parts (s_hi = top 7 significand bits, s_lo = s - s_hi); with the split
+    switched off the per-group fp32 scaling runs.  Both meet the fp32-output
+    bar against the float64 oracle, with fp16-subnormal and large scales among
+    the groups."""
+    _announce(f"qgemm q4 split={split}")
+    from aiimage_amd import synth
+    if not split:
+        monkeypatch.setenv("AEXQ_QGEMM_NOSPLIT", "1")
+    n, k, m = 512, 1024, 130
+    words, scales, _ = synth.q4_weights(n, k, 95, group=32, code=synth.NIBBLE_OFFSET8)
+    bits = scales.view(np.uint16).copy()
+    bits[:300] = np.arange(1, 301, dtype=np.uint16)              # subnormal scales
+    bits[300:310] = np.float16(1000.0).view(np.uint16)           # large, still <= 4096
+    bits[310:320] = np.float16(4096.0).view(np.uint16)           # the bound itself
+    sc = bits.view(np.float16)
+    w = ctx.weight(aexq.QuantizedTensor(n * k, 32, words, sc, bits=4,
+                                        nibble_code=synth.NIBBLE_OFFSET8), n, k)
+    wf = orc.dequant_q4(words, sc, n, k, 32, synth.NIBBLE_OFFSET8, orc.SCALE_F16)
+    x16 = synth.activations(m, k, 96)
+    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    plan = ctx.plan_check(w, xd, yd)
+    assert f"split={int(split)}" in plan, plan
+    ctx.linear(w, xd, yd)
+    torch.cuda.synchronize()
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
+
+
+def test_gemm_q4_scale_above_bound_keeps_group_scaling(ctx, aexq, orc):
+    """A scale above 4096 could overflow q * s_hi in fp16: such a weight stays on
+    the per-group fp32 scaling."""
+    _announce("qgemm q4 scale > 4096")
+    from aiimage_amd import synth
+    n, k, m = 256, 512, 96
+    words, scales, _ = synth.q4_weights(n, k, 97, group=32, code=synth.NIBBLE_OFFSET8)
+    sc = scales.copy()
+    sc[5] = np.float16(5000.0)
+    w = ctx.weight(aexq.QuantizedTensor(n * k, 32, words, sc, bits=4,
+                                        nibble_code=synth.NIBBLE_OFFSET8), n, k)
+    wf = orc.dequant_q4(words, sc, n, k, 32, synth.NIBBLE_OFFSET8, orc.SCALE_F16)
+    x16 = synth.activations(m, k, 98)
+    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    plan = ctx.plan_check(w, xd, yd)
+    assert "split=0" in plan, plan
+    ctx.linear(w, xd, yd)
+    torch.cuda.synchronize()
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
