@@ -181,3 +181,40 @@ def test_malformed_records_are_rejected(ctx, aexq, orc):
     q4_g24 = orc.record_write_q4(_values(4, 48, 51), 24)
     with pytest.raises(_abi.ArgumentError):             # group must divide K
         ctx.weight_from_record(q4_g24, 6, 32, bits=4)
+
+
+def test_sharded_archive_into_device_weights(ctx, aexq, orc, tmp_path):
+    """A manifest-backed, sharded AQSGET8 archive (MAS:50-158) walked into device
+    weights record by record: each dequantises bit-exactly to the oracle's reader."""
+    _announce("sharded archive load")
+    import hashlib
+    import json
+    import os
+    from aiimage_amd import assets
+    shapes = [(64, 256, 4), (40, 128, 8), (32, 64, 4)]
+    recs = []
+    for i, (n, k, bits) in enumerate(shapes):
+        v = _values(n, k, 60 + i)
+        recs.append(orc.record_write_q4(v, 32) if bits == 4 else orc.record_write_q8(v, k))
+    blob = orc.archive_header(4, 32, len(recs), 777) + b"".join(recs)
+    root = str(tmp_path)
+    cuts = [0, 100, 5000, len(blob)]
+    parts = []
+    for j, (a, b) in enumerate(zip(cuts, cuts[1:])):
+        rel = "w/shard%d.bin" % j
+        os.makedirs(os.path.join(root, "w"), exist_ok=True)
+        with open(os.path.join(root, rel), "wb") as f:
+            f.write(blob[a:b])
+        parts.append({"file": rel, "bytes": b - a, "sha256": hashlib.sha256(blob[a:b]).hexdigest()})
+    with open(os.path.join(root, assets.Q4_MANIFEST_FILE), "w") as f:
+        json.dump({"schema": assets.Q4_MANIFEST_SCHEMA, "weight_only": True,
+                   "logical_files": {"decoder.aqs": {"stored_bytes": len(blob), "parts": parts}}}, f)
+    a = assets.MobileAssetSet.try_load(root, verify_hashes=True)
+    with a.open_read("decoder.aqs") as s:
+        ws, header = assets.load_archive_weights(ctx, s, shapes)
+    assert header == (4, 32, 3)
+    for (n, k, _), rec, w in zip(shapes, recs, ws):
+        rc, ref, _ = orc.record_read_array(rec, n * k)
+        assert rc == 0
+        assert _same_bits(ctx.dequant(w).cpu().numpy(), ref.reshape(n, k))
+        w.release()
