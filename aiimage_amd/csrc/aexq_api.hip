@@ -870,9 +870,7 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   // 64-wide K steps, fp16 activation rows 16-byte aligned
   const bool gemm_ok = M > 32 && K % 64 == 0 && (fmt == kQ8 || w0->block % 32 == 0) &&
                        (rms_in || x_ok) && getenv("AEXQ_QGEMM_OFF") == nullptr;
-  if (gemm_ok && size_ok) {
-    // Q4 keeps 64-row tiles: its per-group scaling needs the registers a
-    // 128-row tile's accumulators would take
+  if (gemm_ok && size_ok && !argmax) {
     // Q4 takes 128-row tiles only with split fp16 scales (its per-group
     // scaling otherwise needs the registers the larger tile's accumulators take)
     bool small = fmt == kQ4 && w0->scale_dtype == AEXQ_DTYPE_F16 && (!swiglu || a.up->scales_small);
@@ -895,11 +893,17 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     const bool wide = K % 256 == 0 && (fmt == kQ8 || gmode == kG32) &&
                       getenv("AEXQ_QMM_NARROW") == nullptr;
     const int nt = swiglu ? (mt == 1 ? 2 : 1) : (mt == 1 ? 4 : 2);
-    QmmConfig mc{fmt, gmode, mt, nt, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16, false};
+    QmmConfig mc{fmt, gmode, mt, nt, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16, false, false};
     if (wide) {
       QmmConfig wc = mc;
       wc.wide = true;
       if (fmt == kQ8 && mt == 1) wc.nt = nt > 1 ? nt / 2 : 1;
+      if (argmax) {
+        // the LM head: argmax partials fused, one 16-row block per wave (more,
+        // shorter workgroups over the vocabulary measured faster)
+        wc.argmax = true;
+        wc.nt = 1;
+      }
       plan->mentry = qmm_find(wc);
     }
     if (!plan->mentry) plan->mentry = qmm_find(mc);
@@ -1236,6 +1240,24 @@ extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
     ArgmaxParams ap{ctx->part_best, ctx->part_index, ctx->part_second, parts, M, argmax,
                     top2_gap};
     e = argmax_finalize_launch(ap, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
+    return AEXQ_OK;
+  }
+  if (plan.kind == kPlanMfma && plan.mentry->cfg.argmax) {
+    // M = 2..32 rows per launch on the wide MFMA kernel, one partial per
+    // workgroup and row, then the same merge
+    const int parts = plan.grid;
+    st = ensure_parts(ctx, (long long)parts * M, op);
+    if (st) return st;
+    plan.p.part_best = ctx->part_best;
+    plan.p.part_index = ctx->part_index;
+    plan.p.part_second = ctx->part_second;
+    plan.p.parts = parts;
+    st = launch_plan(ctx, plan, op);
+    if (st) return st;
+    ArgmaxParams ap{ctx->part_best, ctx->part_index, ctx->part_second, parts, M, argmax,
+                    top2_gap};
+    hipError_t e = argmax_finalize_launch(ap, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
     return AEXQ_OK;
   }

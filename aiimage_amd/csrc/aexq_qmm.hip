@@ -7,7 +7,8 @@ namespace aexq {
 
 #define QMME(FMT, GM, MT, NT, PAIR, SF16)                                                        \
   QmmEntry {                                                                                    \
-    QmmConfig{FMT, GM, MT, NT, PAIR, SF16, false}, &qmm_kernel<FMT, GM, MT, NT, PAIR, SF16>,    \
+    QmmConfig{FMT, GM, MT, NT, PAIR, SF16, false, false},                                     \
+        &qmm_kernel<FMT, GM, MT, NT, PAIR, SF16>,                                               \
         16 * NT                                                                                 \
   }
 
@@ -33,7 +34,7 @@ const QmmEntry* qmm_find(const QmmConfig& c) {
   for (int i = 0; i < n; ++i) {
     const QmmConfig& q = t[i].cfg;
     if (q.fmt == c.fmt && q.gmode == c.gmode && q.mt == c.mt && q.nt == c.nt &&
-        q.pair == c.pair && q.sf16 == c.sf16)
+        q.pair == c.pair && q.sf16 == c.sf16 && q.argmax == c.argmax)
       return &t[i];
   }
   return nullptr;

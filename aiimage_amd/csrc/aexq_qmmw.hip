@@ -5,11 +5,12 @@
 
 namespace aexq {
 
-#define QMMWE(FMT, MT, NT, PAIR, SF16)                                                        \
+#define QMMWA(FMT, MT, NT, PAIR, SF16, AM)                                                    \
   QmmEntry {                                                                                  \
-    QmmConfig{FMT, FMT == kQ8 ? kGRow : kG32, MT, NT, PAIR, SF16, true},                      \
-        &qmmw_kernel<FMT, MT, NT, PAIR, SF16>, kWaves * 16 * NT                               \
+    QmmConfig{FMT, FMT == kQ8 ? kGRow : kG32, MT, NT, PAIR, SF16, true, AM},                  \
+        &qmmw_kernel<FMT, MT, NT, PAIR, SF16, AM>, kWaves * 16 * NT                           \
   }
+#define QMMWE(FMT, MT, NT, PAIR, SF16) QMMWA(FMT, MT, NT, PAIR, SF16, false)
 
 // Blocks per wave: 4 at M <= 16, 2 at M <= 32, halved for SwiGLU pairs; Q8
 // at M <= 16 half of that (its steps carry twice the code bytes, and the
@@ -21,7 +22,12 @@ namespace aexq {
   QMMWE(kQ8, 1, 2, false, SF16), QMMWE(kQ8, 2, 2, false, SF16), QMMWE(kQ8, 1, 1, true, SF16), \
       QMMWE(kQ8, 2, 1, true, SF16)
 
-static const QmmEntry kTableW[] = {QMMW_Q4(true), QMMW_Q4(false), QMMW_Q8(true), QMMW_Q8(false)};
+// LM heads at M = 2..32 with the fused argmax partials (single weights)
+#define QMMW_AM(FMT, SF16) QMMWA(FMT, 1, 1, false, SF16, true), QMMWA(FMT, 2, 1, false, SF16, true)
+
+static const QmmEntry kTableW[] = {QMMW_Q4(true),      QMMW_Q4(false),      QMMW_Q8(true),
+                                   QMMW_Q8(false),     QMMW_AM(kQ4, true),  QMMW_AM(kQ4, false),
+                                   QMMW_AM(kQ8, true), QMMW_AM(kQ8, false)};
 
 static constexpr int kCountW = (int)(sizeof(kTableW) / sizeof(kTableW[0]));
 

@@ -24,7 +24,7 @@
 
 namespace aexq {
 
-template <int FMT, int MT, int NT, bool PAIR, bool SF16>
+template <int FMT, int MT, int NT, bool PAIR, bool SF16, bool ARGMAX>
 struct QmmW {
   static constexpr int GM = FMT == kQ8 ? kGRow : kG32;
   using Base = Qmm<FMT, GM, MT, NT, PAIR, SF16>;
@@ -153,6 +153,91 @@ struct QmmW {
         *(u32x4*)(xs + (16 * m + row) * XRS + col + 16 * v) = xv[2 * m + v];
   }
 
+  // Argmax partials (the LM head): each lane keeps the (best, index, second)
+  // of its output column for every row it holds (rows 16 m + 4 (lane / 16) + r)
+  // over the tiles the wave finishes; the epilogue value is the one finish()
+  // stores as the logit.
+  struct Best {
+    float v[MT][4], s[MT][4];
+    int i[MT][4];
+  };
+
+  static __device__ __forceinline__ void best_init(Best& b) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        b.v[m][r] = __builtin_nanf("");
+        b.i[m][r] = 0x7fffffff;
+        b.s[m][r] = -INFINITY;
+      }
+  }
+
+  static __device__ __forceinline__ void best_update(const QmvParams& p, const Cursor& cu,
+                                                     int lane, const Acc& acc, Best& b) {
+    const QmvMat& mt = p.mat[cu.j];
+    const int n_l = lane & 15, mq = lane >> 4;
+    constexpr int sb = SF16 ? 2 : 4;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = cu.rt * Base::TN + 16 * nt + n_l;
+      if (n >= mt.n) continue;
+      float rs = 1.0f;
+      if constexpr (FMT == kQ8)
+        rs = load_scale((const char*)mt.s + cu.b * mt.s_bstride * sb, n, SF16);
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * m + 4 * mq + r;
+          if (row < p.m) {
+            const float v = gemm_epilogue(p, p.m_base + row, n, acc.v[0][m][nt][r] * rs);
+            argmax_merge(b.v[m][r], b.i[m][r], b.s[m][r], v, n, -INFINITY);
+          }
+        }
+    }
+  }
+
+  // One partial per row and workgroup: the 16 lanes of a row group, then the
+  // four waves through LDS.  Every wave of the workgroup calls it.
+  static __device__ __forceinline__ void best_write(const QmvParams& p, int lane, int wave,
+                                                    Best& b) {
+    __shared__ float lv[16 * MT][kWaves], ls[16 * MT][kWaves];
+    __shared__ int li[16 * MT][kWaves];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = b.v[m][r], sv = b.s[m][r];
+        int ix = b.i[m][r];
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+          const float ov = __shfl_xor(v, off, 64);
+          const int oi = __shfl_xor(ix, off, 64);
+          const float os = __shfl_xor(sv, off, 64);
+          argmax_merge(v, ix, sv, ov, oi, os);
+        }
+        if ((lane & 15) == 0) {
+          const int row = 16 * m + 4 * (lane >> 4) + r;
+          lv[row][wave] = v;
+          li[row][wave] = ix;
+          ls[row][wave] = sv;
+        }
+      }
+    __syncthreads();
+    const int row = threadIdx.x;
+    if (row < 16 * MT && row < p.m) {
+      float v = lv[row][0], sv = ls[row][0];
+      int ix = li[row][0];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) argmax_merge(v, ix, sv, lv[row][w], li[row][w], ls[row][w]);
+      const long long o = (long long)(p.m_base + row) * p.parts + blockIdx.x;
+      p.part_best[o] = v;
+      p.part_index[o] = ix;
+      p.part_second[o] = sv;
+    }
+  }
+
   // Consumes one step: the codes pass through LDS into MFMA layout, then
   // eight 32-code groups.
   static __device__ __forceinline__ void compute(const QmvParams& p, int lane, uint8_t* lds,
@@ -258,10 +343,10 @@ struct QmmW {
   }
 };
 
-template <int FMT, int MT, int NT, bool PAIR, bool SF16>
+template <int FMT, int MT, int NT, bool PAIR, bool SF16, bool ARGMAX>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void qmmw_kernel(const QmvParams p) {
-  using Q = QmmW<FMT, MT, NT, PAIR, SF16>;
+  using Q = QmmW<FMT, MT, NT, PAIR, SF16, ARGMAX>;
   __shared__ __align__(16) uint8_t lds_all[kWaves][Q::LDS_WAVE];
   __shared__ __align__(16) uint8_t xs_all[2][Q::XSL];
   const int lane = threadIdx.x & 63;
@@ -271,7 +356,21 @@ void qmmw_kernel(const QmvParams p) {
   const int steps = p.k / 256;
   const int t0 = (int)((long long)blockIdx.x * p.total_tiles / gridDim.x) * steps;
   const int t1 = (int)((long long)(blockIdx.x + 1) * p.total_tiles / gridDim.x) * steps;
-  if (t0 >= t1) return;  // the whole workgroup: no barrier is left waiting
+  if (t0 >= t1) {  // the whole workgroup: no barrier is left waiting
+    if constexpr (ARGMAX) {
+      // an empty partial for each row (it never wins the merge)
+      const int row = threadIdx.x;
+      if (row < 16 * MT && row < p.m) {
+        const long long o = (long long)(p.m_base + row) * p.parts + blockIdx.x;
+        p.part_best[o] = __builtin_nanf("");
+        p.part_index[o] = 0x7fffffff;
+        p.part_second[o] = -INFINITY;
+      }
+    }
+    return;
+  }
+  typename Q::Best best;
+  if constexpr (ARGMAX) Q::best_init(best);
 
   typename Q::Cursor cu = Q::locate(p, t0);
   typename Q::Buf A, B;
@@ -303,7 +402,10 @@ void qmmw_kernel(const QmvParams p) {
     Q::load(p, nx, lane, wave, B);
     __builtin_amdgcn_sched_barrier(0);
     Q::compute(p, lane, lds, xs_all[sl], A, acc);
-    if (cu.s == steps - 1) Q::Base::finish(p, mine(cu), lane, acc);
+    if (cu.s == steps - 1) {
+      if constexpr (ARGMAX) Q::best_update(p, mine(cu), lane, acc, best);
+      Q::Base::finish(p, mine(cu), lane, acc);
+    }
     if (!more) break;
     Q::store_x(xs_all[sl ^ 1], xv);
     __syncthreads();
@@ -316,7 +418,10 @@ void qmmw_kernel(const QmvParams p) {
     Q::load(p, nx, lane, wave, A);
     __builtin_amdgcn_sched_barrier(0);
     Q::compute(p, lane, lds, xs_all[sl], B, acc);
-    if (cu.s == steps - 1) Q::Base::finish(p, mine(cu), lane, acc);
+    if (cu.s == steps - 1) {
+      if constexpr (ARGMAX) Q::best_update(p, mine(cu), lane, acc, best);
+      Q::Base::finish(p, mine(cu), lane, acc);
+    }
     if (!more) break;
     Q::store_x(xs_all[sl ^ 1], xv);
     __syncthreads();
@@ -324,6 +429,7 @@ void qmmw_kernel(const QmvParams p) {
     cu = nx;
     sl ^= 1;
   }
+  if constexpr (ARGMAX) Q::best_write(p, lane, wave, best);
 }
 
 }  // namespace aexq

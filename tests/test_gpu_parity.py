@@ -405,6 +405,49 @@ def test_lmhead_argmax_full_vocab(ctx, aexq, orc, m):
     assert np.array_equal(am2.cpu().numpy(), gi)
 
 
+@pytest.mark.parametrize("bits,m,n", [(8, 20, 50000), (8, 40, 30011), (4, 8, 40000), (4, 24, 20000)])
+def test_lmhead_argmax_mfma_rows(ctx, aexq, orc, bits, m, n):
+    """LM heads of 2..32 rows per launch take the wide MFMA kernel with the argmax
+    partials fused (M = 40: two launches whose partials land in their own rows);
+    logits, indices and top-2 gaps against the oracle."""
+    _announce(f"lm head mfma q{bits} m={m} n={n}")
+    from aiimage_amd import synth
+    k = synth.HIDDEN
+    if bits == 8:
+        words, scales, _ = synth.q8_weights(n, k, 0xAE0C0F25 + m)
+        w = ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
+        wf = orc.dequant_q8(words, scales, n, k, scale_dtype=orc.SCALE_F16)
+    else:
+        words, scales, _ = synth.q4_weights(n, k, 0xAE0C0F25 + m, group=32, code=synth.NIBBLE_OFFSET8)
+        w = ctx.weight(aexq.QuantizedTensor(n * k, 32, words, scales, bits=4,
+                                            nibble_code=synth.NIBBLE_OFFSET8), n, k)
+        wf = orc.dequant_q4(words, scales, n, k, 32, synth.NIBBLE_OFFSET8, orc.SCALE_F16)
+    x16 = synth.activations(m, k, 0xAE0C0F26 + m)
+    layout = aexq.LAYOUT_PACK4_LINEAR
+    logits = aexq.new_activation(m, n, torch.float32, layout)
+    am = torch.full((m,), -1, dtype=torch.int32, device="cuda")
+    gap = torch.zeros(m, dtype=torch.float32, device="cuda")
+    xd = aexq.describe(dev(x16), m, k)
+    ld = aexq.describe(logits, m, n, layout)
+    ctx.lmhead_argmax(w, xd, ld, am, gap)
+    torch.cuda.synchronize()
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    stride = aexq.storage_elements(layout, m, n)
+    assert normwise(logits.cpu().numpy().reshape(m, stride)[:, :n], ref) <= 1e-5
+    ref_idx = orc.argmax_rows(ref.astype(np.float32))
+    srt = np.sort(ref, axis=1)
+    ref_gap = srt[:, -1] - srt[:, -2]
+    gi = am.cpu().numpy()
+    for r in range(m):
+        if ref_gap[r] >= ARGMAX_TIE:
+            assert gi[r] == ref_idx[r], (r, gi[r], ref_idx[r])
+    np.testing.assert_allclose(gap.cpu().numpy(), ref_gap, atol=1e-5)
+    am2 = torch.full((m,), -1, dtype=torch.int32, device="cuda")
+    ctx.lmhead_argmax(w, xd, None, am2)
+    torch.cuda.synchronize()
+    assert np.array_equal(am2.cpu().numpy(), gi)
+
+
 def test_argmax_reference_kats_and_rules(ctx, aexq, orc):
     _announce("argmax kats")
     from aiimage_amd import _abi
