@@ -306,31 +306,71 @@ def config3(torch, aexq, ctx, steps: int = 30):
 def cpu_baseline(seconds: float):
     """RunGemmCpu (GS:13328-13381) restated in C, timed on this host: the seven
     linears of one layer on dequantized fp32 weights (dequant untimed, as at
-    reference load time), float64 accumulation, single thread."""
+    reference load time), float64 accumulation, single thread -- the reported
+    baseline.  Beside it, bounded samples of the same loop split over output
+    columns on the host's cores (identical results) and of configs 1 and 5,
+    and the linear part of config 3 derived from them."""
     import numpy as np
 
     import oracle
     from aiimage_amd import synth
+    threads = max(1, min(16, os.cpu_count() or 1))
+
+    def timed(fn, budget):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return el / n, n, el
+
     lin = []
     for i, (name, n, k) in enumerate(synth.LAYER_LINEARS):
         words, scales, _ = synth.q4_weights(n, k, 1000 + i, group=32, code=synth.NIBBLE_OFFSET8)
         wf = oracle.dequant_q4(words, scales, n, k, 32, oracle.NIBBLE_OFFSET8, oracle.SCALE_F16)
         x = synth.activations(1, k, 2000 + i).astype(np.float32)
         lin.append((x, wf, n))
-    layers = 0
-    t0 = time.perf_counter()
-    while True:
+
+    def layer(th):
         for x, wf, n in lin:
-            oracle.gemm_cpu(x, wf, n, True)
-        layers += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    per_layer = el / layers
-    return {"value": LAYER_BYTES / per_layer / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{layers} passes of one layer's 7 Q4 linears (M=1) through the C restatement "
-                      f"of RunGemmCpu on dequantized fp32 weights, {el:.1f} s, "
-                      f"{per_layer * 1e3:.2f} ms per layer; rate in algorithmic quantized bytes"}
+            oracle.gemm_cpu(x, wf, n, True, threads=th)
+
+    per_layer, layers, el = timed(lambda: layer(1), seconds)
+    out = {"value": LAYER_BYTES / per_layer / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"{layers} passes of one layer's 7 Q4 linears (M=1) through the C restatement "
+                     f"of RunGemmCpu on dequantized fp32 weights, {el:.1f} s, "
+                     f"{per_layer * 1e3:.2f} ms per layer; rate in algorithmic quantized bytes"}
+    budget = max(1.0, seconds / 5)
+    per_layer_mt, _, _ = timed(lambda: layer(threads), budget)
+    cfg = {"config2_all_cores": {"GBps": LAYER_BYTES / per_layer_mt / 1e9, "cores": threads}}
+    # config 1: Q8 1024 -> 3584
+    w8, s8, _ = synth.q8_weights(3584, 1024, 3000)
+    wf8 = oracle.dequant_q8(w8, s8, 3584, 1024, scale_dtype=oracle.SCALE_F16)
+    x1 = synth.activations(1, 1024, 3001).astype(np.float32)
+    for th, key in ((1, "config1_single"), (threads, "config1_all_cores")):
+        t, _, _ = timed(lambda th=th: oracle.gemm_cpu(x1, wf8, 3584, True, threads=th), budget)
+        cfg[key] = {"GBps": 3_686_400 / t / 1e9, "cores": th}
+    del wf8
+    # config 5: the Q8 LM head, M = 1
+    wl, sl, _ = synth.q8_weights(synth.VOCAB, synth.HIDDEN, 3002)
+    wfl = oracle.dequant_q8(wl, sl, synth.VOCAB, synth.HIDDEN, scale_dtype=oracle.SCALE_F16)
+    del wl
+    xl = synth.activations(1, synth.HIDDEN, 3003).astype(np.float32)
+    lm = {}
+    for th, key in ((1, "config5_m1_single"), (threads, "config5_m1_all_cores")):
+        t, _, _ = timed(lambda th=th: oracle.gemm_cpu(xl, wfl, synth.VOCAB, True, threads=th), budget)
+        lm[th] = t
+        cfg[key] = {"GBps": 156_496_128 / t / 1e9, "ms": t * 1e3, "cores": th}
+    del wfl
+    # config 3, linear part only (24 layers + LM head; no attention on the CPU path)
+    for th, key, pl in ((1, "config3_linears_single", per_layer),
+                        (threads, "config3_linears_all_cores", per_layer_mt)):
+        step = 24 * pl + lm[th]
+        cfg[key] = {"tokens_per_s": 1.0 / step, "ms_per_token": step * 1e3, "cores": th}
+    out["configs"] = {k: {a: (round(b, 4) if isinstance(b, float) else b) for a, b in v.items()}
+                      for k, v in cfg.items()}
+    return out
 
 
 def main():
