@@ -144,13 +144,23 @@ struct QmmW {
                        xr, (16 * m + row) * (int)rs2 + col + 16 * v, 0, 0));
   }
 
+  // Stores the slice; Q4 chunks of 8 activations go in the (p, p + 4) pair
+  // order that q4_pairs gives the codes, once per workgroup rather than per
+  // MFMA.
   static __device__ __forceinline__ void store_x(uint8_t* xs, const u32x4 (&xv)[XV]) {
     const int row = threadIdx.x >> 4, col = (threadIdx.x & 15) * 32;
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-      for (int v = 0; v < 2; ++v)
-        *(u32x4*)(xs + (16 * m + row) * XRS + col + 16 * v) = xv[2 * m + v];
+      for (int v = 0; v < 2; ++v) {
+        u32x4 c = xv[2 * m + v];
+        if constexpr (FMT == kQ4) {
+          uint32_t xp[4];
+          q4_xpairs(c[0], c[1], c[2], c[3], xp);
+          c = u32x4{xp[0], xp[1], xp[2], xp[3]};
+        }
+        *(u32x4*)(xs + (16 * m + row) * XRS + col + 16 * v) = c;
+      }
   }
 
   // Argmax partials (the LM head): each lane keeps the (best, index, second)
@@ -310,15 +320,9 @@ struct QmmW {
         }
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const u32x4 xv = *(const u32x4*)(xs + (16 * m + n_l) * XRS + 2 * (32 * g + 8 * kb));
-        f16x8 af;
-        if constexpr (FMT == kQ8) {
-          af = __builtin_bit_cast(f16x8, xv);
-        } else {
-          uint32_t xp[4];
-          q4_xpairs(xv[0], xv[1], xv[2], xv[3], xp);
-          af = pack8(xp[0], xp[1], xp[2], xp[3]);
-        }
+        // (Q4: already in pair order, see store_x)
+        const f16x8 af =
+            *(const f16x8*)(xs + (16 * m + n_l) * XRS + 2 * (32 * g + 8 * kb));
 #pragma unroll
         for (int h = 0; h < NW; ++h)
 #pragma unroll
