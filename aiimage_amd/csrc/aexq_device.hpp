@@ -39,20 +39,27 @@ __device__ __forceinline__ void q8_pairs(uint32_t u, uint32_t& lo, uint32_t& hi)
 
 // Eight offset-8 nibbles of one device word (n0 in bits 0-3; the device copy
 // always holds offset-8 codes n = q + 8) -> four fp16 pairs of the exact codes,
-// pair p holding elements (p, p + 4).  Five bit operations and four packed
-// fp16 operations, all exact:
+// pair p holding elements (p, p + 4).  One shift, four v_and_or_b32 and four
+// packed fp16 operations, all exact:
 //   even nibbles: bits 0x6400|n       = 1024 + n    ; + (-1032)         -> n - 8
 //   odd nibbles:  bits 0x6400|(n<<4)  = 1024 + 16n  ; * 1/16 + (-72)    -> n - 8
+// gfx950's VOP3 encoding takes no literal operand, so with the masks and the
+// exponent pattern as literals (w & m) | E compiles to a v_and_b32 and a
+// v_or_b32; held in registers (the empty asm statements hide the values from
+// constant folding) it is a single v_and_or_b32.
 __device__ __forceinline__ void q4_pairs(uint32_t w, uint32_t q[4]) {
-  const uint32_t E = 0x64006400u;
+  uint32_t E = 0x64006400u, lo = 0x000F000Fu, hi = 0x00F000F0u;
+  __asm__("" : "+v"(E));
+  __asm__("" : "+s"(lo));
+  __asm__("" : "+s"(hi));
   const f16x2 b_even = {(f16)-1032.0f, (f16)-1032.0f};
   const f16x2 s_odd = {(f16)0.0625f, (f16)0.0625f};
   const f16x2 b_odd = {(f16)-72.0f, (f16)-72.0f};
   const uint32_t w8 = w >> 8;
-  const f16x2 a = as_h2((w & 0x000F000Fu) | E);   // (n0, n4)
-  const f16x2 b = as_h2((w & 0x00F000F0u) | E);   // (n1, n5) * 16
-  const f16x2 c = as_h2((w8 & 0x000F000Fu) | E);  // (n2, n6)
-  const f16x2 d = as_h2((w8 & 0x00F000F0u) | E);  // (n3, n7) * 16
+  const f16x2 a = as_h2((w & lo) | E);   // (n0, n4)
+  const f16x2 b = as_h2((w & hi) | E);   // (n1, n5) * 16
+  const f16x2 c = as_h2((w8 & lo) | E);  // (n2, n6)
+  const f16x2 d = as_h2((w8 & hi) | E);  // (n3, n7) * 16
   q[0] = as_u(a + b_even);
   q[1] = as_u(__builtin_elementwise_fma(b, s_odd, b_odd));
   q[2] = as_u(c + b_even);
