@@ -66,6 +66,9 @@ struct aexq_ctx {
   long long attn_cap = 0;
   int* attn_count = nullptr;  // per kv head: splits finished in the running launch
   int attn_count_cap = 0;
+  // split-K partial planes of the MFMA kernels (floats), grown on demand
+  float* sk_part = nullptr;
+  long long sk_cap = 0;
 };
 
 struct aexq_weight {
@@ -120,6 +123,7 @@ extern "C" void aexq_destroy(aexq_ctx* ctx) {
   (void)hipFree(ctx->gather_scratch);
   (void)hipFree(ctx->attn_part);
   (void)hipFree(ctx->attn_count);
+  (void)hipFree(ctx->sk_part);
   delete ctx;
 }
 
@@ -675,7 +679,69 @@ struct Plan {
   const void* xg_src = nullptr;
   int xg_heads = 0, xg_hd = 0, xg_rows = 0, xg_batch = 1, xg_f32 = 0;
   long long xg_bstride = 0;
+  // split K (MFMA kernels): sk_chunks chunks of sk_cs K steps per tile, partials
+  // summed by the fix-up launch; sk_nw = 2 for a SwiGLU pair
+  int sk_chunks = 1, sk_cs = 0, sk_nw = 1;
 };
+
+// Split K for an MFMA launch of `units` independent tiles of `steps` K steps
+// on at most `slots` resident workgroups: the chunk count with the least
+// estimated time -- the rounds of whole workgroups times the K steps each
+// runs (step_us per step, measured per kernel family: these launches wait on
+// load latency, not on bandwidth), plus, once split, the fix-up launch and the
+// fp32 partials written and read back (plane_bytes per chunk).  A layer's
+// linear at M = 16..512 has few tiles (8 for a 1024-row output), so without
+// the split a handful of workgroups would walk all of K on a 256-CU part.
+// AEXQ_SPLITK=n forces n chunks (1: no split).
+static void pick_split(long long units, int steps, long long slots, double step_us,
+                       double plane_bytes, int* chunks, int* cs) {
+  constexpr double kFixupUs = 5.0;         // the fix-up launch and its round trips
+  constexpr double kPartBytesPerUs = 5e6;  // partial planes written and read back
+  constexpr double kMaxPartBytes = 256.0 * 1024 * 1024;
+  *chunks = 1;
+  *cs = steps;
+  if (steps < 2 || units < 1 || slots < 1) return;
+  const char* env = getenv("AEXQ_SPLITK");
+  if (env && atoi(env) >= 1) {
+    const int want = atoi(env) < steps ? atoi(env) : steps;
+    *cs = (steps + want - 1) / want;
+    *chunks = (steps + *cs - 1) / *cs;
+    if (*chunks < 2) *cs = steps;
+    return;
+  }
+  double best = 0.0;
+  for (int c = 1; c <= steps; ++c) {
+    const int w = (steps + c - 1) / c;  // steps per chunk
+    const int n = (steps + w - 1) / w;  // chunks that takes
+    if (n != c) continue;               // same chunking as a smaller count
+    if (n > 1 && n * plane_bytes > kMaxPartBytes) break;
+    const long long work = units * n;
+    const long long rounds = (work + slots - 1) / slots;
+    double t = (double)rounds * w * step_us;
+    if (n > 1) t += kFixupUs + n * plane_bytes * 2.0 / kPartBytesPerUs;
+    if (c == 1 || t < best) {
+      best = t;
+      *chunks = n;
+      *cs = w;
+    }
+  }
+  if (*chunks < 2) {
+    *chunks = 1;
+    *cs = steps;
+  }
+}
+
+// Partial-plane layout of one split launch (per-matrix offsets, plane size in
+// floats, 256-byte aligned planes).
+static long long splitk_layout(QmvParams& q, int nw) {
+  long long off = 0;
+  for (int i = 0; i < q.nmat; ++i) {
+    q.mat[i].sk_off = off;
+    off += (long long)q.batch * q.m * nw * q.mat[i].n_store;
+  }
+  q.sk_plane = (off + 63) & ~63LL;
+  return q.sk_plane;
+}
 
 // Shape of the streaming kernel for `chunks` 16-byte code chunks per row:
 // the smallest lanes-per-row x chunks-per-lane capacity that covers the row,
@@ -1022,18 +1088,34 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       for (int i = 0; i < count; ++i) p.mat[i].x_bstride = xv.batch == 1 ? 0 : (long long)M * K;
     }
   }
+  const int nw = swiglu ? 2 : 1;
+  plan->sk_nw = nw;
   if (plan->kind == kPlanGemm) {
     const int bm = plan->gentry->cfg.bm;
+    const int mtiles = (M + bm - 1) / bm;
     plan->mblock = bm;
-    plan->grid = (int)(((long long)tiles_total + 7) / 8 * 8 * ((M + bm - 1) / bm));
+    const long long slots = (long long)qgemm_blocks_per_cu(plan->gentry) * ctx->cus;
+    // per-step times measured on single-layer launches (graph replays)
+    const double step_us = fmt == kQ4 ? (bm == 128 ? 1.35 : 0.9) : (bm == 128 ? 1.0 : 0.66);
+    pick_split((long long)tiles_total * mtiles, K / 64, slots, step_us,
+               (double)M * nw * tiles_total * plan->rows_per_tile * 4.0,
+               &plan->sk_chunks, &plan->sk_cs);
+    plan->grid = (int)(((long long)tiles_total + 7) / 8 * 8 * mtiles * plan->sk_chunks);
   } else if (plan->kind == kPlanMfma) {
     int per_cu = qmm_blocks_per_cu(plan->mentry);
     const char* env = getenv("AEXQ_QMM_BLOCKS_PER_CU");
     if (env && atoi(env) > 0) per_cu = atoi(env);
-    // narrow kernel: a wave per tile; wide kernel: a workgroup per tile
-    const long long need = plan->mentry->cfg.wide ? (long long)tiles_total
-                                                  : ((long long)tiles_total + kWaves - 1) / kWaves;
     const long long cap = (long long)per_cu * ctx->cus;
+    // the wide kernel splits K where its few tiles would leave the part idle
+    // (never for the argmax partials, which need each tile whole)
+    if (plan->mentry->cfg.wide && !plan->mentry->cfg.argmax)
+      pick_split(tiles_total, K / 256, cap, fmt == kQ4 ? 2.2 : 1.15,
+                 (double)M * nw * tiles_total * plan->rows_per_tile * 4.0, &plan->sk_chunks,
+                 &plan->sk_cs);
+    // narrow kernel: a wave per tile; wide kernel: a workgroup per tile (chunk)
+    const long long need = plan->mentry->cfg.wide
+                               ? (long long)tiles_total * plan->sk_chunks
+                               : ((long long)tiles_total + kWaves - 1) / kWaves;
     plan->grid = (int)(need < cap ? need : cap);
     if (plan->grid < 1) plan->grid = 1;
   } else if (plan->fast) {
@@ -1074,9 +1156,34 @@ static aexq_status launch_mfma(aexq_ctx* ctx, Plan& plan, const char* op) {
     if (e != hipSuccess) return hip_fail(e, op, "rmsnorm pre-pass launch");
     for (int i = 0; i < p.nmat; ++i) p.mat[i].x = ctx->act_scratch;
   }
+  // split K: the partial planes (sized for the largest row block) and, after
+  // each kernel launch, the fix-up that sums them and runs the epilogue
+  const bool split = plan.sk_chunks > 1;
+  const int q8_scale = plan.fmt == kQ8;
+  const int sf16 = (p.flags & kFlagScaleF16) != 0;
+  if (split) {
+    QmvParams q = p;
+    q.m = plan.kind == kPlanGemm || M < plan.mblock ? M : plan.mblock;
+    const long long need = (long long)plan.sk_chunks * splitk_layout(q, plan.sk_nw);
+    if (need > ctx->sk_cap) {
+      (void)hipFree(ctx->sk_part);
+      ctx->sk_part = nullptr;
+      ctx->sk_cap = 0;
+      HIP_TRY(op, hipMalloc((void**)&ctx->sk_part, need * sizeof(float)));
+      ctx->sk_cap = need;
+    }
+    p.sk_part = ctx->sk_part;
+    p.sk_chunks = plan.sk_chunks;
+    p.sk_cs = plan.sk_cs;
+  }
   if (plan.kind == kPlanGemm) {
+    if (split) splitk_layout(p, plan.sk_nw);
     hipError_t e = qgemm_launch(plan.gentry, p, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, op, "gemm kernel launch");
+    if (split) {
+      e = splitk_reduce_launch(p, plan.sk_nw, q8_scale, sf16, ctx->stream);
+      if (e != hipSuccess) return hip_fail(e, op, "split-K fix-up launch");
+    }
     return AEXQ_OK;
   }
   const int ysz = plan.ysz;
@@ -1091,8 +1198,13 @@ static aexq_status launch_mfma(aexq_ctx* ctx, Plan& plan, const char* op) {
       if (mt.y && mt.y_hd == 0) mt.y = (char*)mt.y + (long long)m0 * mt.y_rstride * ysz;
       if (mt.res) mt.res = (const char*)mt.res + (long long)m0 * q.r_rstride * ysz;
     }
+    if (split) splitk_layout(q, plan.sk_nw);
     hipError_t e = qmm_launch(plan.mentry, q, plan.grid, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, op, "mfma kernel launch");
+    if (split) {
+      e = splitk_reduce_launch(q, plan.sk_nw, q8_scale, sf16, ctx->stream);
+      if (e != hipSuccess) return hip_fail(e, op, "split-K fix-up launch");
+    }
   }
   return AEXQ_OK;
 }
@@ -1143,15 +1255,17 @@ extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, cons
       snprintf(diag, diag_len, "%s", g_last_error.c_str());
     else if (plan.kind == kPlanGemm)
       snprintf(diag, diag_len,
-               "kernel=qgemm bits=%d bm=%d swiglu=%d split=%d rms_prepass=%d tiles=%d grid=%d",
+               "kernel=qgemm bits=%d bm=%d swiglu=%d split=%d rms_prepass=%d tiles=%d grid=%d "
+               "splitk=%d",
                w->bits, plan.gentry->cfg.bm, (int)plan.gentry->cfg.pair,
-               (int)plan.gentry->cfg.split, (int)plan.rms_prepass, plan.p.total_tiles, plan.grid);
+               (int)plan.gentry->cfg.split, (int)plan.rms_prepass, plan.p.total_tiles, plan.grid,
+               plan.sk_chunks);
     else if (plan.kind == kPlanMfma)
       snprintf(diag, diag_len, "kernel=qmm bits=%d mt=%d nt=%d swiglu=%d wide=%d rms_prepass=%d "
-               "tiles=%d grid=%d mblock=%d",
+               "tiles=%d grid=%d mblock=%d splitk=%d",
                w->bits, plan.mentry->cfg.mt, plan.mentry->cfg.nt, (int)plan.mentry->cfg.pair,
                (int)plan.mentry->cfg.wide, (int)plan.rms_prepass, plan.p.total_tiles, plan.grid,
-               plan.mblock);
+               plan.mblock, plan.sk_chunks);
     else
       snprintf(diag, diag_len,
                "kernel=%s bits=%d lpr=%d cpl=%d u=%d mmax=%d swiglu=%d tiles=%d grid=%d",

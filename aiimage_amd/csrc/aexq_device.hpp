@@ -19,6 +19,8 @@ __device__ __forceinline__ f16x2 as_h2(uint32_t u) { return __builtin_bit_cast(f
 // ROCm 7.2 clang lowers __builtin_bit_cast(float, v[i]) on an ext_vector
 // element to element 0 for every i.
 __device__ __forceinline__ float as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+// ...and raw bits of an fp32 value (same by-value detour).
+__device__ __forceinline__ uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 __device__ __forceinline__ uint32_t as_u(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
 
 // v_dot2_f32_f16: c + a.x*b.x + a.y*b.y with fp32 accumulation.

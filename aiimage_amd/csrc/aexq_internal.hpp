@@ -44,6 +44,7 @@ struct QmvMat {
   int n_store;         // rows written: n plus zero-filled storage padding
   int tiles;           // row tiles per batch entry
   int tile_base;       // first workgroup of this matrix in the grid
+  long long sk_off;    // split K: this matrix's first float in a partial plane
 };
 
 struct QmvParams {
@@ -72,6 +73,16 @@ struct QmvParams {
   int* part_index;
   float* part_second;
   int parts;
+  // split K (MFMA kernels): the K steps of every tile run as sk_chunks chunks
+  // of sk_cs steps whose fp32 partials go to plane c of sk_part (plane c at
+  // c * sk_plane floats; element (b, row, h, n) of matrix j at sk_off +
+  // ((b * m + row) * NW + h) * n_store + n, h = 1 the SwiGLU up half);
+  // splitk_reduce_launch sums them and applies the epilogue.  sk_chunks <= 1:
+  // no split, the kernels finish their tiles themselves.
+  float* sk_part;
+  long long sk_plane;
+  int sk_chunks;
+  int sk_cs;
 };
 
 struct ArgmaxParams {
@@ -137,6 +148,7 @@ struct QgemmEntry {
 };
 const QgemmEntry* qgemm_find(const QgemmConfig& cfg);
 int qgemm_rows_per_tile(bool pair);
+int qgemm_blocks_per_cu(const QgemmEntry* e);
 hipError_t qgemm_launch(const QgemmEntry* e, const QmvParams& p, hipStream_t stream);
 // RMSNorm of activation rows into fp16 rows (the M > 1 form of RMSNorm-in):
 // out[b][m][k] = fp16(x * rsqrt(max(mean(x^2) + eps, 1e-20)) * gamma[min(k, size-1)])
@@ -144,6 +156,12 @@ hipError_t rmsnorm_rows_launch(const void* x, int x_f32, long long x_rstride, lo
                                int batch, int m, int k, const float* gamma, int gamma_size,
                                float eps, void* out, hipStream_t stream);
 hipError_t generic_launch(int fmt, const QmvParams& p, int grid, hipStream_t stream);
+// Split-K fix-up of an MFMA launch (aexq_kernels.hip): for every output the
+// sk_chunks partials summed in chunk order, then the epilogue of the MFMA
+// kernels' finish(): Q8 row scale (q8_scale), bias / alpha / beta, SwiGLU
+// (nw == 2), residual, the output layout.
+hipError_t splitk_reduce_launch(const QmvParams& p, int nw, int q8_scale, int sf16,
+                                hipStream_t stream);
 int generic_rows_per_wg();
 hipError_t argmax_finalize_launch(const ArgmaxParams& a, hipStream_t stream);
 hipError_t logits_argmax_launch(const float* logits, int m, int n, long long rstride, float* pv,

@@ -465,6 +465,88 @@ hipError_t head_gather_launch(const void* src, int f32, int rows, int heads, int
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Split-K fix-up of the MFMA kernels: one thread per stored output element
+// (matrix j = blockIdx.y, so its fields are workgroup-uniform scalar loads;
+// batch entry b, row, column n < n_store).  The sk_chunks partials
+// are summed in chunk order (the result depends on the plan's chunking only,
+// never on which workgroup finished first), then the epilogue runs as the
+// kernels' finish() runs it (MM:1101 / MM:2301 bias forms, SwiGLU-out,
+// residual); columns in [n, n_store) are written as 0.
+// ---------------------------------------------------------------------------
+template <int NW>
+__global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const QmvParams p, int q8_scale,
+                                                                 int sf16) {
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  const QmvMat& mt = p.mat[blockIdx.y];
+  if (!mt.y || i >= (long long)p.batch * p.m * mt.n_store) return;
+  const int n = (int)(i % mt.n_store);
+  const long long t = i / mt.n_store;
+  const int row = (int)(t % p.m), b = (int)(t / p.m);
+  const bool yf32 = (p.flags & kFlagYf32) != 0;
+  float v = 0.0f;
+  if (n < mt.n) {
+    const float* src = p.sk_part + mt.sk_off + ((long long)b * p.m + row) * NW * mt.n_store + n;
+    // eight chunks' loads in flight at a time, then added in chunk order
+    float g = 0.0f, u = 0.0f;
+    for (int c0 = 0; c0 < p.sk_chunks; c0 += 8) {
+      float gv[8], uv[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const long long o = (long long)(c0 + q) * p.sk_plane;
+        gv[q] = c0 + q < p.sk_chunks ? src[o] : 0.0f;
+        uv[q] = NW == 2 && c0 + q < p.sk_chunks ? src[o + mt.n_store] : 0.0f;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (c0 + q < p.sk_chunks) {
+          g += gv[q];
+          if (NW == 2) u += uv[q];
+        }
+    }
+    float rs0 = 1.0f, rs1 = 1.0f;
+    if (q8_scale) {
+      const int sb = sf16 ? 2 : 4;
+      rs0 = load_scale((const char*)mt.s + b * mt.s_bstride * sb, n, sf16);
+      if (NW == 2) rs1 = load_scale((const char*)mt.s2 + b * mt.s_bstride * sb, n, sf16);
+    }
+    v = gemm_epilogue(p, p.m_base + row, n, g * rs0);
+    if (NW == 2) v = silu(v) * gemm_epilogue(p, p.m_base + row, n, u * rs1);
+    if (mt.res && (p.flags & kFlagResidual)) {
+      const char* rb = (const char*)mt.res + b * mt.r_bstride * (yf32 ? 4 : 2);
+      const long long ri = (long long)row * p.r_rstride + n;
+      v += yf32 ? ((const float*)rb)[ri] : (float)((const f16*)rb)[ri];
+    }
+  }
+  char* yb = (char*)mt.y + b * mt.y_bstride * (yf32 ? 4 : 2);
+  const long long yi = out_index(p, mt, row, n);
+  if (yf32)
+    ((float*)yb)[yi] = v;
+  else
+    ((f16*)yb)[yi] = (f16)v;
+}
+
+hipError_t splitk_reduce_launch(const QmvParams& p, int nw, int q8_scale, int sf16,
+                                hipStream_t stream) {
+  long long most = 0;  // outputs of the largest matrix
+  for (int j = 0; j < p.nmat; ++j) {
+    const long long cnt = (long long)p.batch * p.m * p.mat[j].n_store;
+    most = cnt > most ? cnt : most;
+  }
+  const long long blocks = (most + kThreads - 1) / kThreads;
+  if (blocks <= 0 || blocks > 0x7fffffffLL || p.nmat < 1 || p.nmat > kMaxGroup ||
+      p.sk_chunks < 2 || !p.sk_part)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)blocks, (unsigned)p.nmat);
+  if (nw == 2)
+    hipLaunchKernelGGL(splitk_reduce_kernel<2>, grid, dim3(kThreads), 0, stream, p, q8_scale,
+                       sf16);
+  else
+    hipLaunchKernelGGL(splitk_reduce_kernel<1>, grid, dim3(kThreads), 0, stream, p, q8_scale,
+                       sf16);
+  return hipGetLastError();
+}
+
 hipError_t dequant_launch(int fmt, const uint32_t* w, const void* s, int scale_f16, int n, int k,
                           int group, float* out, hipStream_t stream) {
   const bool chunked = fmt == kQ8 ? (k % 16 == 0) : (k % 32 == 0);

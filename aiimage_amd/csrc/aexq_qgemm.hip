@@ -32,11 +32,24 @@ const QgemmEntry* qgemm_find(const QgemmConfig& c) {
 
 int qgemm_rows_per_tile(bool pair) { return pair ? 64 : 128; }
 
+int qgemm_blocks_per_cu(const QgemmEntry* e) {
+  static int cache[kCountG] = {0};
+  const int idx = (int)(e - kTableG);
+  if (idx < 0 || idx >= kCountG) return 1;
+  if (cache[idx] == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, e->fn, kThreads, 0) != hipSuccess || n < 1)
+      n = 1;
+    cache[idx] = n;
+  }
+  return cache[idx];
+}
+
 hipError_t qgemm_launch(const QgemmEntry* e, const QmvParams& p, hipStream_t stream) {
   if (!e) return hipErrorInvalidConfiguration;
   const int mtiles = (p.m + e->cfg.bm - 1) / e->cfg.bm;
   const long long groups = (p.total_tiles + 7) / 8;
-  const long long grid = groups * 8 * mtiles;
+  const long long grid = groups * 8 * mtiles * (p.sk_chunks > 1 ? p.sk_chunks : 1);
   if (grid <= 0 || grid > 0x7fffffffLL) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL(e->fn, dim3((unsigned)grid), dim3(kThreads), 0, stream, p, mtiles);
   return hipGetLastError();

@@ -293,6 +293,32 @@ struct QGemm {
         }
     }
   }
+
+  // Split K: the thread's raw accumulators of K chunk c (no row scale, no
+  // epilogue) into partial plane c.
+  static __device__ __forceinline__ void spill(const QmvParams& p, const QmvMat& mt, int b,
+                                               int n0, int m0, int lane, int wm, int wn, int c,
+                                               const f32x4 (&acc)[TM][TN]) {
+    const int l16 = lane & 15, lk = lane >> 4;
+    constexpr int NW = PAIR ? 2 : 1;
+    constexpr int TO = PAIR ? TN / 2 : TN;
+    float* base = p.sk_part + (long long)c * p.sk_plane + mt.sk_off +
+                  (long long)b * p.m * NW * mt.n_store;
+#pragma unroll
+    for (int to = 0; to < TO; ++to) {
+      const int n = n0 + (PAIR ? 32 * wn + 16 * to : 64 * wn + 16 * to) + l16;
+      if (n >= mt.n) continue;
+#pragma unroll
+      for (int h = 0; h < NW; ++h)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm * WM + 16 * tm + 4 * lk + r;
+            if (m < p.m) base[((long long)m * NW + h) * mt.n_store + n] = acc[tm][to + 2 * h][r];
+          }
+    }
+  }
 };
 
 template <int FMT, int BM, bool PAIR, bool SF16, bool SPLIT>
@@ -302,12 +328,17 @@ void qgemm_kernel(const QmvParams p, int mtiles) {
   __shared__ __align__(16) f16 xs[2][BM * G::LS];
   __shared__ __align__(16) uint8_t ws[2][G::CB];
   __shared__ float ss[2][FMT == kQ8 ? 1 : G::BN * 2];  // Q4 group scales of a step
-  // weight tile tn and row tile tm of this workgroup (see the header)
+  // weight tile tn, row tile tm and K chunk kc of this workgroup (see the
+  // header; the chunks of a split K sit next to each other on one XCD)
   // (readfirstlane: the tile coordinates are workgroup-uniform, so the buffer
   // resources built from them stay in scalar registers)
+  const int S = p.sk_chunks > 1 ? p.sk_chunks : 1;
+  const int per = mtiles * S;
   const int bid = blockIdx.x, i = bid >> 3;
-  const int tn = __builtin_amdgcn_readfirstlane((i / mtiles) * 8 + (bid & 7));
-  const int tm = __builtin_amdgcn_readfirstlane(i - (i / mtiles) * mtiles);
+  const int tn = __builtin_amdgcn_readfirstlane((i / per) * 8 + (bid & 7));
+  const int rem = i - (i / per) * per;
+  const int tm = __builtin_amdgcn_readfirstlane(rem / S);
+  const int kc = __builtin_amdgcn_readfirstlane(rem - (rem / S) * S);
   if (tn >= p.total_tiles) return;
   int j = 0;
   for (int q = 1; q < p.nmat; ++q)
@@ -324,6 +355,9 @@ void qgemm_kernel(const QmvParams p, int mtiles) {
   const int wm = wave >> 1, wn = wave & 1;
   const typename G::Src src = G::source(p, mt, b, n0, m0, tid, wave);
   const int steps = p.k / G::BK;
+  const int cs = S > 1 ? p.sk_cs : steps;
+  const int s0 = kc * cs, s1 = min(s0 + cs, steps);  // this workgroup's K steps
+  if (s0 >= s1) return;
 
   f32x4 acc[G::TM][G::TN];
 #pragma unroll
@@ -335,25 +369,28 @@ void qgemm_kernel(const QmvParams p, int mtiles) {
   // st + 1 waits in one set (stored after the MFMAs) and step st + 2 is being
   // fetched into the other, so a load has two steps of MFMAs to land.
   typename G::Regs ra, rb;
-  G::load(p, src, 0, tid, ra);
-  if (steps > 1) G::load(p, src, 1, tid, rb);
+  G::load(p, src, s0, tid, ra);
+  if (s0 + 1 < s1) G::load(p, src, s0 + 1, tid, rb);
   G::store(tid, ra, xs[0], ws[0], ss[0]);
   __syncthreads();
-  for (int st = 0;;) {
-    if (st + 2 < steps) G::load(p, src, st + 2, tid, ra);
+  for (int st = s0;;) {
+    if (st + 2 < s1) G::load(p, src, st + 2, tid, ra);
     __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the MFMAs
     G::compute(lane, wm, wn, xs[0], ws[0], ss[0], acc);
-    if (st + 1 < steps) G::store(tid, rb, xs[1], ws[1], ss[1]);
+    if (st + 1 < s1) G::store(tid, rb, xs[1], ws[1], ss[1]);
     __syncthreads();
-    if (++st >= steps) break;
-    if (st + 2 < steps) G::load(p, src, st + 2, tid, rb);
+    if (++st >= s1) break;
+    if (st + 2 < s1) G::load(p, src, st + 2, tid, rb);
     __builtin_amdgcn_sched_barrier(0);
     G::compute(lane, wm, wn, xs[1], ws[1], ss[1], acc);
-    if (st + 1 < steps) G::store(tid, ra, xs[0], ws[0], ss[0]);
+    if (st + 1 < s1) G::store(tid, ra, xs[0], ws[0], ss[0]);
     __syncthreads();
-    if (++st >= steps) break;
+    if (++st >= s1) break;
   }
-  G::finish(p, mt, b, n0, m0, lane, wm, wn, acc);
+  if (S == 1)
+    G::finish(p, mt, b, n0, m0, lane, wm, wn, acc);
+  else
+    G::spill(p, mt, b, n0, m0, lane, wm, wn, kc, acc);
 }
 
 }  // namespace aexq

@@ -330,6 +330,44 @@ struct Qmm {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc.v[h][m][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
+
+  // Split K: the wave's raw accumulators of K chunk c (no row scale, no
+  // epilogue) into partial plane c, then zeroed for the next segment.
+  static __device__ __forceinline__ void spill(const QmvParams& p, const Cursor& cu, int lane,
+                                               int c, Acc& acc) {
+    const QmvMat& mt = p.mat[cu.j];
+    const int n_l = lane & 15, mq = lane >> 4;
+    // the matrix's block of the plane through a buffer resource (scalar
+    // registers) and 32-bit lane offsets
+    const float* base = p.sk_part + (long long)c * p.sk_plane + mt.sk_off +
+                        (long long)cu.b * p.m * NW * mt.n_store;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)base, (short)0, p.m * NW * mt.n_store * 4, kBufferRsrcWord3);
+    const int rstride = NW * mt.n_store * 4;  // bytes between partial rows
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = cu.rt * TN + 16 * nt + n_l;
+      if (n >= mt.n) continue;
+#pragma unroll
+      for (int h = 0; h < NW; ++h)
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = 16 * m + 4 * mq + r;
+            if (row < p.m)
+              __builtin_amdgcn_raw_buffer_store_b32(
+                  f32_bits(acc.v[h][m][nt][r]), rs,
+                  row * rstride + (h * mt.n_store + n) * 4, 0, 0);
+          }
+    }
+#pragma unroll
+    for (int h = 0; h < NW; ++h)
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc.v[h][m][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
 };
 
 template <int FMT, int GM, int MT, int NT, bool PAIR, bool SF16>

@@ -356,10 +356,19 @@ void qmmw_kernel(const QmvParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint8_t* lds = lds_all[wave];
-  // a workgroup's range is whole tiles, so a tile's K steps never split
+  // A workgroup's range is whole (tile, K chunk) items: a tile's K steps split
+  // only at chunk boundaries (split K, sk_chunks > 1), whose partials the
+  // fix-up launch sums.  Items are numbered tile-major, so a range is one
+  // contiguous run of (tile, step) units.
   const int steps = p.k / 256;
-  const int t0 = (int)((long long)blockIdx.x * p.total_tiles / gridDim.x) * steps;
-  const int t1 = (int)((long long)(blockIdx.x + 1) * p.total_tiles / gridDim.x) * steps;
+  const int S = !ARGMAX && p.sk_chunks > 1 ? p.sk_chunks : 1;
+  const int cs = S > 1 ? p.sk_cs : steps;
+  const long long items = (long long)p.total_tiles * S;
+  const long long i0 = (long long)blockIdx.x * items / gridDim.x;
+  const long long i1 = (long long)(blockIdx.x + 1) * items / gridDim.x;
+  const int t0 = (int)((i0 / S) * steps + (i0 % S) * cs);
+  const int t1 = i1 > i0 ? (int)(((i1 - 1) / S) * steps + min((int)((i1 - 1) % S + 1) * cs, steps))
+                         : t0;
   if (t0 >= t1) {  // the whole workgroup: no barrier is left waiting
     if constexpr (ARGMAX) {
       // an empty partial for each row (it never wins the merge)
@@ -391,12 +400,28 @@ void qmmw_kernel(const QmvParams p) {
     c.rt = c.rt * kWaves + wave;
     return c;
   };
+  // the last step of a K chunk: the whole tile's K finishes it here, a chunk
+  // of a split tile leaves its partial (the host never splits an argmax launch)
+  auto segment_end = [&](const typename Q::Cursor& c) {
+    if constexpr (ARGMAX) {
+      Q::best_update(p, mine(c), lane, acc, best);
+      Q::Base::finish(p, mine(c), lane, acc);
+    } else if (S == 1) {
+      Q::Base::finish(p, mine(c), lane, acc);
+    } else {
+      Q::Base::spill(p, mine(c), lane, c.s / cs, acc);
+    }
+  };
   Q::load_x(p, cu, xv);
   Q::load(p, cu, lane, wave, A);
   Q::store_x(xs_all[0], xv);
   __syncthreads();
   int t = t0;
   int sl = 0;
+  // steps left in the running K chunk (ranges start at chunk boundaries; a
+  // tile's shorter last chunk ends with the tile): a countdown, since integer
+  // division would be a VALU sequence in this loop
+  int seg = cs;
   while (true) {
     // step t: codes in A, activations in slice sl; step t + 1's activation
     // loads go out first, then its codes into B
@@ -406,9 +431,9 @@ void qmmw_kernel(const QmvParams p) {
     Q::load(p, nx, lane, wave, B);
     __builtin_amdgcn_sched_barrier(0);
     Q::compute(p, lane, lds, xs_all[sl], A, acc);
-    if (cu.s == steps - 1) {
-      if constexpr (ARGMAX) Q::best_update(p, mine(cu), lane, acc, best);
-      Q::Base::finish(p, mine(cu), lane, acc);
+    if (--seg == 0 || cu.s == steps - 1) {
+      segment_end(cu);
+      seg = cs;
     }
     if (!more) break;
     Q::store_x(xs_all[sl ^ 1], xv);
@@ -422,9 +447,9 @@ void qmmw_kernel(const QmvParams p) {
     Q::load(p, nx, lane, wave, A);
     __builtin_amdgcn_sched_barrier(0);
     Q::compute(p, lane, lds, xs_all[sl], B, acc);
-    if (cu.s == steps - 1) {
-      if constexpr (ARGMAX) Q::best_update(p, mine(cu), lane, acc, best);
-      Q::Base::finish(p, mine(cu), lane, acc);
+    if (--seg == 0 || cu.s == steps - 1) {
+      segment_end(cu);
+      seg = cs;
     }
     if (!more) break;
     Q::store_x(xs_all[sl ^ 1], xv);

@@ -167,11 +167,14 @@ def test_gemm_bias_residual(ctx, aexq, orc, monkeypatch, path, bcast, layout):
     assert normwise(got, ref) <= TOL32
 
 
+@pytest.mark.parametrize("splitk", ["1", "4"])
 @pytest.mark.parametrize("bits", [4, 8])
-def test_gemm_stacked_copies_batched_x_match_single(ctx, aexq, orc, bits):
+def test_gemm_stacked_copies_batched_x_match_single(ctx, aexq, orc, monkeypatch, bits, splitk):
     """Size-independent property: a replicated weight stack with one activation
-    matrix per copy gives exactly each copy's single launch."""
-    _announce(f"qgemm stacked q{bits}")
+    matrix per copy gives exactly each copy's single launch (the same K
+    chunking for both: the plan would split the single launch only)."""
+    _announce(f"qgemm stacked q{bits} splitk={splitk}")
+    monkeypatch.setenv("AEXQ_SPLITK", splitk)
     from aiimage_amd import synth
     n, k, m, copies = 640, 1024, 80, 3
     w, wf = _weight(ctx, aexq, orc, bits, n, k, 81 + bits)

@@ -640,10 +640,13 @@ def test_small_m_mfma_row_blocks_bias_residual(ctx, aexq, orc, monkeypatch, bcas
     assert normwise(got, ref) <= 1e-5
 
 
-def test_small_m_mfma_stacked_copies_match_single(ctx, aexq):
+@pytest.mark.parametrize("splitk", ["1", "4"])
+def test_small_m_mfma_stacked_copies_match_single(ctx, aexq, monkeypatch, splitk):
     """Size-independent property at M=16: every copy of a replicated weight stack
-    gives exactly the single-weight output."""
-    _announce("mfma stacked copies")
+    gives exactly the single-weight output (the same K chunking for both: the
+    plan would split the single launch only)."""
+    _announce(f"mfma stacked copies splitk={splitk}")
+    monkeypatch.setenv("AEXQ_SPLITK", splitk)
     from aiimage_amd import synth
     n, k, m, copies = 2048, 1024, 16, 5
     w, _, _ = _q4_weight(ctx, aexq, n, k, 81)
