@@ -933,19 +933,21 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   plan->fmt = fmt;
   plan->fast = false;
   // M > 32: the tiled GEMM (every row of a weight tile per workgroup pass),
-  // 64-wide K steps, fp16 activation rows 16-byte aligned
-  const bool gemm_ok = M > 32 && K % 64 == 0 && (fmt == kQ8 || w0->block % 32 == 0) &&
+  // 64-wide K steps, fp16 activation rows 16-byte aligned; Q4 scale groups of
+  // 16 (the reference's shipping Q4) or a multiple of 32
+  const bool g16 = fmt == kQ4 && w0->block == 16;
+  const bool gemm_ok = M > 32 && K % 64 == 0 && (fmt == kQ8 || w0->block % 32 == 0 || g16) &&
                        (rms_in || x_ok) && getenv("AEXQ_QGEMM_OFF") == nullptr;
   if (gemm_ok && size_ok && !argmax) {
     // Q4 takes 128-row tiles only with split fp16 scales (its per-group
     // scaling otherwise needs the registers the larger tile's accumulators take)
     bool small = fmt == kQ4 && w0->scale_dtype == AEXQ_DTYPE_F16 && (!swiglu || a.up->scales_small);
     for (int i = 0; i < count; ++i) small = small && ws[i]->scales_small;
-    const bool split = small && M > 64 && getenv("AEXQ_QGEMM_NOSPLIT") == nullptr;
+    const bool split = small && !g16 && M > 64 && getenv("AEXQ_QGEMM_NOSPLIT") == nullptr;
     int bm = (M <= 64 || (fmt == kQ4 && !split)) ? 64 : 128;
     const char* benv = getenv("AEXQ_QGEMM_BM");  // tuning override: 64 or 128
     if (benv && (atoi(benv) == 64 || atoi(benv) == 128) && !split) bm = atoi(benv);
-    QgemmConfig gc{fmt, bm, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16, split};
+    QgemmConfig gc{fmt, bm, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16, split, g16};
     plan->gentry = qgemm_find(gc);
     if (plan->gentry) {
       plan->kind = kPlanGemm;
@@ -1096,7 +1098,8 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     plan->mblock = bm;
     const long long slots = (long long)qgemm_blocks_per_cu(plan->gentry) * ctx->cus;
     // per-step times measured on single-layer launches (graph replays)
-    const double step_us = fmt == kQ4 ? (bm == 128 ? 1.35 : 0.9) : (bm == 128 ? 1.0 : 0.66);
+    const double step_us = fmt == kQ4 ? (bm == 128 ? 1.35 : (g16 ? 1.1 : 0.9))
+                                      : (bm == 128 ? 1.0 : 0.66);
     pick_split((long long)tiles_total * mtiles, K / 64, slots, step_us,
                (double)M * nw * tiles_total * plan->rows_per_tile * 4.0,
                &plan->sk_chunks, &plan->sk_cs);
@@ -1106,16 +1109,17 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     const char* env = getenv("AEXQ_QMM_BLOCKS_PER_CU");
     if (env && atoi(env) > 0) per_cu = atoi(env);
     const long long cap = (long long)per_cu * ctx->cus;
-    // the wide kernel splits K where its few tiles would leave the part idle
-    // (never for the argmax partials, which need each tile whole)
-    if (plan->mentry->cfg.wide && !plan->mentry->cfg.argmax)
-      pick_split(tiles_total, K / 256, cap, fmt == kQ4 ? 2.2 : 1.15,
+    // both kernels split K where their few tiles would leave the part idle
+    // (never for the argmax partials, which need each tile whole); the wide
+    // kernel runs a tile per workgroup, the narrow one a tile per wave
+    const bool wide = plan->mentry->cfg.wide;
+    if (!plan->mentry->cfg.argmax)
+      pick_split(tiles_total, K / (wide ? 256 : 128), wide ? cap : cap * kWaves,
+                 wide ? (fmt == kQ4 ? 2.2 : 1.15) : 1.0,
                  (double)M * nw * tiles_total * plan->rows_per_tile * 4.0, &plan->sk_chunks,
                  &plan->sk_cs);
-    // narrow kernel: a wave per tile; wide kernel: a workgroup per tile (chunk)
-    const long long need = plan->mentry->cfg.wide
-                               ? (long long)tiles_total * plan->sk_chunks
-                               : ((long long)tiles_total + kWaves - 1) / kWaves;
+    const long long items = (long long)tiles_total * plan->sk_chunks;
+    const long long need = wide ? items : (items + kWaves - 1) / kWaves;
     plan->grid = (int)(need < cap ? need : cap);
     if (plan->grid < 1) plan->grid = 1;
   } else if (plan->fast) {

@@ -134,12 +134,13 @@ const QmmEntry* qmmw_table(int* count);  // the wide-step entries (aexq_qmmw.hip
 int qmm_blocks_per_cu(const QmmEntry* e);
 hipError_t qmm_launch(const QmmEntry* e, const QmvParams& p, int grid, hipStream_t stream);
 // Tiled GEMM for M > 32 rows (aexq_qgemm.hip): K % 64 == 0, Q8 or Q4 with a
-// scale group that is a multiple of 32, fp16 activation rows 16-byte aligned.
+// scale group of 16 or a multiple of 32, fp16 activation rows 16-byte aligned.
 // Tiles are 128 weight rows (64 output columns for a SwiGLU pair) by bm rows.
 struct QgemmConfig {
   int fmt, bm;
   bool pair, sf16;
   bool split;  // Q4 fp16 scales folded into B as exact hi + lo parts (|scale| <= 4096)
+  bool g16;    // Q4 with one scale per 16 codes
 };
 typedef void (*QgemmFn)(const QmvParams, int);
 struct QgemmEntry {

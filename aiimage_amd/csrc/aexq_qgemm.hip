@@ -6,17 +6,24 @@
 
 namespace aexq {
 
-#define QGE(FMT, BM, PAIR, SF16, SPLIT) \
-  QgemmEntry { QgemmConfig{FMT, BM, PAIR, SF16, SPLIT}, &qgemm_kernel<FMT, BM, PAIR, SF16, SPLIT> }
+#define QGEG(FMT, BM, PAIR, SF16, SPLIT, G16)                                 \
+  QgemmEntry {                                                                \
+    QgemmConfig{FMT, BM, PAIR, SF16, SPLIT, G16},                             \
+        &qgemm_kernel<FMT, BM, PAIR, SF16, SPLIT, G16>                        \
+  }
+#define QGE(FMT, BM, PAIR, SF16, SPLIT) QGEG(FMT, BM, PAIR, SF16, SPLIT, false)
 
 #define QG_BM(FMT, BM) \
   QGE(FMT, BM, false, true, false), QGE(FMT, BM, false, false, false), \
       QGE(FMT, BM, true, true, false), QGE(FMT, BM, true, false, false)
 
-// Q4 with fp16 scales split into B (128-row tiles): single weights and pairs
-static const QgemmEntry kTableG[] = {QG_BM(kQ4, 64), QG_BM(kQ8, 64), QG_BM(kQ8, 128),
-                                     QGE(kQ4, 128, false, true, true),
-                                     QGE(kQ4, 128, true, true, true)};
+// Q4 with fp16 scales split into B (128-row tiles): single weights and pairs;
+// Q4 with 16-code groups (64-row tiles)
+static const QgemmEntry kTableG[] = {
+    QG_BM(kQ4, 64), QG_BM(kQ8, 64), QG_BM(kQ8, 128), QGE(kQ4, 128, false, true, true),
+    QGE(kQ4, 128, true, true, true), QGEG(kQ4, 64, false, true, false, true),
+    QGEG(kQ4, 64, false, false, false, true), QGEG(kQ4, 64, true, true, false, true),
+    QGEG(kQ4, 64, true, false, false, true)};
 
 static constexpr int kCountG = (int)(sizeof(kTableG) / sizeof(kTableG[0]));
 
@@ -24,7 +31,7 @@ const QgemmEntry* qgemm_find(const QgemmConfig& c) {
   for (int i = 0; i < kCountG; ++i) {
     const QgemmConfig& q = kTableG[i].cfg;
     if (q.fmt == c.fmt && q.bm == c.bm && q.pair == c.pair && q.sf16 == c.sf16 &&
-        q.split == c.split)
+        q.split == c.split && q.g16 == c.g16)
       return &kTableG[i];
   }
   return nullptr;

@@ -24,6 +24,12 @@
 // loads run two steps ahead of the MFMAs (two register sets); LDS is
 // double-buffered with one barrier per step.
 //
+// G16 (Q4 with one scale per 16 codes, the reference's shipping format): an
+// MFMA K extent holds two groups, lanes l / 16 = 0, 1 the first and 2, 3 the
+// second; two MFMAs, each with the other group's lanes' codes zeroed, give
+// the two groups' products, each scaled in fp32 into the accumulator -- the
+// same exact float(q) * scale at twice the MFMA work.
+//
 // Workgroup b runs on XCD b % 8: the numbering puts the BM-row tiles of one
 // weight tile on one XCD, whose L2 then fetches that weight tile once.
 //
@@ -35,9 +41,11 @@
 
 namespace aexq {
 
-template <int FMT, int BM, bool PAIR, bool SF16, bool SPLIT>
+template <int FMT, int BM, bool PAIR, bool SF16, bool SPLIT, bool G16>
 struct QGemm {
   static_assert(!SPLIT || (FMT == kQ4 && SF16), "split scales are for Q4 with fp16 scales");
+  static_assert(!G16 || (FMT == kQ4 && !SPLIT), "16-code groups are a Q4 per-group form");
+  static constexpr int GS = G16 ? 4 : 2;             // Q4 scale groups per K step
   static constexpr int BN = 128;                     // weight rows of a tile
   static constexpr int BK = 64;                      // K per step
   static constexpr int NOUT = PAIR ? BN / 2 : BN;    // output columns of a tile
@@ -59,7 +67,7 @@ struct QGemm {
   struct Regs {
     u32x4 x[XV];
     u32x4 c[CV];
-    uint32_t s;  // Q4: raw bits of the thread's group scale
+    uint32_t s[G16 ? 2 : 1];  // Q4: raw bits of the thread's group scale(s)
   };
 
   // Per-workgroup resources of one tile (wave-uniform).
@@ -119,17 +127,31 @@ struct QGemm {
         r.c[i] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                        s.wr, s.brl * s.rb + st * BK + 32 * s.sub + 16 * i, 0, 0));
-      r.s = 0;
+      r.s[0] = 0;
     } else {
       r.c[0] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(s.wr, s.brl * s.rb + st * 32 + 16 * s.sub,
                                                        0, 0));
       const int g = (st * BK + 32 * s.sub) / p.group;
       const int si = s.brl * p.groups_per_row + g;
-      if constexpr (SF16)
-        r.s = __builtin_amdgcn_raw_buffer_load_b16(s.sr, si * 2, 0, 0);
-      else
-        r.s = __builtin_amdgcn_raw_buffer_load_b32(s.sr, si * 4, 0, 0);
+      if constexpr (G16) {
+        // the two 16-code groups of the thread's 32 codes (si even: aligned)
+        if constexpr (SF16) {
+          const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(s.sr, si * 2, 0, 0);
+          r.s[0] = v & 0xFFFFu;
+          r.s[1] = v >> 16;
+        } else {
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 v =
+              __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(s.sr, si * 4, 0, 0));
+          r.s[0] = v[0];
+          r.s[1] = v[1];
+        }
+      } else if constexpr (SF16) {
+        r.s[0] = __builtin_amdgcn_raw_buffer_load_b16(s.sr, si * 2, 0, 0);
+      } else {
+        r.s[0] = __builtin_amdgcn_raw_buffer_load_b32(s.sr, si * 4, 0, 0);
+      }
     }
   }
 
@@ -162,13 +184,16 @@ struct QGemm {
     }
     if constexpr (SPLIT) {
       // (s_hi, s_lo): s_hi keeps the top 7 significand bits, s_lo = s - s_hi exactly
-      const f16 sv = __builtin_bit_cast(f16, (uint16_t)r.s);
-      const f16 hi = __builtin_bit_cast(f16, (uint16_t)(r.s & 0xFFF0u));
+      const f16 sv = __builtin_bit_cast(f16, (uint16_t)r.s[0]);
+      const f16 hi = __builtin_bit_cast(f16, (uint16_t)(r.s[0] & 0xFFF0u));
       const f16 lo = sv - hi;
       const f16x2 pr = {hi, lo};
       ((uint32_t*)ss)[row * 2 + sub] = as_u(pr);
+    } else if constexpr (G16) {
+      ss[row * 4 + 2 * sub] = scale_of(r.s[0], SF16);
+      ss[row * 4 + 2 * sub + 1] = scale_of(r.s[1], SF16);
     } else if constexpr (FMT == kQ4) {
-      ss[row * 2 + sub] = scale_of(r.s, SF16);
+      ss[row * 2 + sub] = scale_of(r.s[0], SF16);
     }
   }
 
@@ -227,6 +252,33 @@ struct QGemm {
 #pragma unroll
           for (int tn = 0; tn < TN; ++tn)
             acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bq[tn], acc[tm][tn], 0, 0, 0);
+      } else if constexpr (G16) {
+        // group 2 kk in lanes lk < 2, group 2 kk + 1 in lanes lk >= 2
+        const bool first = lk < 2;
+        float s0[TN], s1[TN];
+        f16x8 b0[TN], b1[TN];
+        const f16x8 zero = {};
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+          s0[tn] = ss[(brow(wn, tn) + l16) * 4 + 2 * kk];
+          s1[tn] = ss[(brow(wn, tn) + l16) * 4 + 2 * kk + 1];
+          b0[tn] = first ? bq[tn] : zero;
+          b1[tn] = first ? zero : bq[tn];
+        }
+        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int tn = 0; tn < TN; ++tn) {
+            const f32x4 t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], b0[tn], z, 0, 0, 0);
+            const f32x4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], b1[tn], z, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              acc[tm][tn][r] = fmaf(s0[tn], t0[r], acc[tm][tn][r]);
+              acc[tm][tn][r] = fmaf(s1[tn], t1[r], acc[tm][tn][r]);
+            }
+          }
+        __builtin_amdgcn_sched_barrier(0);
       } else {
         float sc[TN];
 #pragma unroll
@@ -321,13 +373,13 @@ struct QGemm {
   }
 };
 
-template <int FMT, int BM, bool PAIR, bool SF16, bool SPLIT>
+template <int FMT, int BM, bool PAIR, bool SF16, bool SPLIT, bool G16>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void qgemm_kernel(const QmvParams p, int mtiles) {
-  using G = QGemm<FMT, BM, PAIR, SF16, SPLIT>;
+  using G = QGemm<FMT, BM, PAIR, SF16, SPLIT, G16>;
   __shared__ __align__(16) f16 xs[2][BM * G::LS];
   __shared__ __align__(16) uint8_t ws[2][G::CB];
-  __shared__ float ss[2][FMT == kQ8 ? 1 : G::BN * 2];  // Q4 group scales of a step
+  __shared__ float ss[2][FMT == kQ8 ? 1 : G::BN * G::GS];  // Q4 group scales of a step
   // weight tile tn, row tile tm and K chunk kc of this workgroup (see the
   // header; the chunks of a split K sit next to each other on one XCD)
   // (readfirstlane: the tile coordinates are workgroup-uniform, so the buffer

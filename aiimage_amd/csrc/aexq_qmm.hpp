@@ -378,10 +378,18 @@ void qmm_kernel(const QmvParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int gw = blockIdx.x * kWaves + wave;
   const int nw = gridDim.x * kWaves;
-  // a wave's range is whole tiles, so a tile's K slices never split
+  // A wave's range is whole (tile, K chunk) items: a tile's K slices split
+  // only at chunk boundaries (split K, sk_chunks > 1), whose partials the
+  // fix-up launch sums.  Items are numbered tile-major, so a range is one
+  // contiguous run of (tile, slice) units.
   const int steps = p.k / 128;
-  const int t0 = (int)((long long)gw * p.total_tiles / nw) * steps;
-  const int t1 = (int)((long long)(gw + 1) * p.total_tiles / nw) * steps;
+  const int S = p.sk_chunks > 1 ? p.sk_chunks : 1;
+  const int cs = S > 1 ? p.sk_cs : steps;
+  const long long items = (long long)p.total_tiles * S;
+  const long long i0 = (long long)gw * items / nw, i1 = (long long)(gw + 1) * items / nw;
+  const int t0 = (int)((i0 / S) * steps + (i0 % S) * cs);
+  const int t1 = i1 > i0 ? (int)(((i1 - 1) / S) * steps + min((int)((i1 - 1) % S + 1) * cs, steps))
+                         : t0;
   if (t0 >= t1) return;
 
   typename Q::Cursor cu = Q::locate(p, t0);
@@ -395,6 +403,15 @@ void qmm_kernel(const QmvParams p) {
       for (int nt = 0; nt < NT; ++nt) acc.v[h][m][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   Q::load(p, cu, lane, A);
   int t = t0;
+  // K slices left in the running chunk: a countdown (integer division would be
+  // a VALU sequence in this loop); a tile's shorter last chunk ends with it
+  int seg = cs;
+  auto segment_end = [&](const typename Q::Cursor& c) {
+    if (S == 1)
+      Q::finish(p, c, lane, acc);
+    else
+      Q::spill(p, c, lane, c.s / cs, acc);
+  };
   while (true) {
     bool more = t + 1 < t1;
     typename Q::Cursor nx = more ? Q::advance(p, cu) : cu;
@@ -403,7 +420,10 @@ void qmm_kernel(const QmvParams p) {
     // sinks it below the MFMAs and every slice waits for its own loads)
     __builtin_amdgcn_sched_barrier(0);
     Q::compute(p, lane, A, acc);
-    if (cu.s == steps - 1) Q::finish(p, cu, lane, acc);
+    if (--seg == 0 || cu.s == steps - 1) {
+      segment_end(cu);
+      seg = cs;
+    }
     if (!more) break;
     ++t;
     cu = nx;
@@ -412,7 +432,10 @@ void qmm_kernel(const QmvParams p) {
     Q::load(p, nx, lane, A);
     __builtin_amdgcn_sched_barrier(0);
     Q::compute(p, lane, B, acc);
-    if (cu.s == steps - 1) Q::finish(p, cu, lane, acc);
+    if (--seg == 0 || cu.s == steps - 1) {
+      segment_end(cu);
+      seg = cs;
+    }
     if (!more) break;
     ++t;
     cu = nx;

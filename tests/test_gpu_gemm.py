@@ -198,22 +198,41 @@ def test_gemm_stacked_copies_batched_x_match_single(ctx, aexq, orc, monkeypatch,
     assert normwise(singles[0].cpu().numpy().reshape(m, n), ref) <= TOL
 
 
-def test_gemm_group16_stays_on_mfma_blocks(ctx, aexq, orc):
-    """The reference's shipping Q4 (group 16) is not a tiled-GEMM format: the
-    plan takes the 32-row MFMA blocks and the result still meets the bar."""
-    _announce("qgemm group16 fallback to qmm")
+@pytest.mark.parametrize("scale_f16,n,k,m,swiglu", [
+    (False, 512, 1024, 48, False),    # the reference's shipping Q4: group 16, fp32 scales
+    (False, 1000, 2048, 300, False),  # ragged N, three 64-row tiles and a partial one
+    (True, 1024, 3584, 64, False),    # fp16 scales, down_proj shape
+    (False, 1024, 1024, 128, True),   # gate/up pair
+])
+def test_gemm_group16(ctx, aexq, orc, scale_f16, n, k, m, swiglu):
+    """Q4 with one scale per 16 codes on the tiled GEMM: two MFMAs per 32-code
+    extent, each group's product scaled in fp32 (exact float(q) * scale)."""
+    _announce(f"qgemm group16 f16={scale_f16} n={n} k={k} m={m} swiglu={swiglu}")
     from aiimage_amd import synth
-    n, k, m = 512, 1024, 48
-    w, wf = _weight(ctx, aexq, orc, 4, n, k, 91, group=16, scale_f16=False, code=0)
+    w, wf = _weight(ctx, aexq, orc, 4, n, k, 91 + m, group=16, scale_f16=scale_f16, code=0)
     x16 = synth.activations(m, k, 92)
     y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
     xd = aexq.describe(dev(x16), m, k)
     yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
-    assert ctx.plan_check(w, xd, yd).startswith("kernel=qmm")
-    ctx.linear(w, xd, yd)
+    kw = {}
+    if swiglu:
+        wu, uf = _weight(ctx, aexq, orc, 4, n, k, 93 + m, group=16, scale_f16=scale_f16, code=0)
+        kw = dict(up=wu)
+    plan = ctx.plan_check(w, xd, yd, **kw)
+    assert plan.startswith("kernel=qgemm") and "bm=64" in plan, plan
+    ctx.linear(w, xd, yd, **kw)
     torch.cuda.synchronize()
-    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
-    assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
+    g = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    if swiglu:
+        u = orc.gemm_gpu_semantics(x16.astype(np.float32), uf)
+        ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32))
+                        for r in range(m)])
+    else:
+        ref = g
+    stride = aexq.storage_elements(aexq.LAYOUT_PACK4_LINEAR, m, n)
+    got = y.cpu().numpy().reshape(m, stride)
+    assert np.all(got[:, n:] == 0)
+    assert normwise(got[:, :n], ref) <= TOL32
 
 
 @pytest.mark.parametrize("split", [True, False])

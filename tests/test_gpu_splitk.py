@@ -56,7 +56,7 @@ def dev(a, dtype=None):
     return t.cuda()
 
 
-def _weight(ctx, aexq, orc, bits, n, k, seed, group=32, scale_f16=True):
+def _weight(ctx, aexq, orc, bits, n, k, seed, group=32, scale_f16=True, code=1):
     from aiimage_amd import synth
     sdt = np.float16 if scale_f16 else np.float32
     odt = orc.SCALE_F16 if scale_f16 else orc.SCALE_F32
@@ -64,9 +64,10 @@ def _weight(ctx, aexq, orc, bits, n, k, seed, group=32, scale_f16=True):
         words, scales, _ = synth.q8_weights(n, k, seed, scale_dtype=sdt)
         w = ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
         return w, orc.dequant_q8(words, scales, n, k, scale_dtype=odt)
-    words, scales, _ = synth.q4_weights(n, k, seed, group=group, scale_dtype=sdt)
-    w = ctx.weight(aexq.QuantizedTensor(n * k, group, words, scales, bits=4, nibble_code=1), n, k)
-    return w, orc.dequant_q4(words, scales, n, k, group, nibble_code=1, scale_dtype=odt)
+    words, scales, _ = synth.q4_weights(n, k, seed, group=group, code=code, scale_dtype=sdt)
+    w = ctx.weight(aexq.QuantizedTensor(n * k, group, words, scales, bits=4, nibble_code=code),
+                   n, k)
+    return w, orc.dequant_q4(words, scales, n, k, group, nibble_code=code, scale_dtype=odt)
 
 
 def _splitk(plan):
@@ -123,6 +124,41 @@ def test_split_matches_oracle(ctx, aexq, orc, monkeypatch, bits, scale_f16, n, k
     assert torch.equal(y, y2)
     one = y1.cpu().numpy().astype(np.float64).reshape(m, stride)[:, :n]
     assert normwise(got[:, :n], one) <= (TOL32 if y32 else TOL)
+
+
+@pytest.mark.parametrize("bits,group,n,k,m,pair", [
+    (4, 16, 1024, 2048, 16, False),   # the reference's shipping Q4: group 16, fp32 scales
+    (4, 16, 1024, 3584, 32, True),    # ... gate/up pair at M = 32
+    (8, 0, 1024, 1152, 16, False),    # K = 9 x 128: not a multiple of the wide step
+])
+def test_split_narrow_kernel(ctx, aexq, orc, bits, group, n, k, m, pair):
+    """The 128-wide-slice MFMA kernel (group-16 scales, or K not a multiple of
+    256) splits K per wave tile the same way."""
+    _announce(f"splitk narrow q{bits} g={group} n={n} k={k} m={m} pair={pair}")
+    from aiimage_amd import synth
+    w, wf = _weight(ctx, aexq, orc, bits, n, k, 91 + m, group=group or k, scale_f16=False,
+                    code=0)
+    x16 = synth.activations(m, k, 92)
+    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    kw = {}
+    if pair:
+        wu, uf = _weight(ctx, aexq, orc, bits, n, k, 93 + m, group=group or k, scale_f16=False,
+                         code=0)
+        kw = dict(up=wu)
+    plan = ctx.plan_check(w, xd, yd, **kw)
+    assert plan.startswith("kernel=qmm") and "wide=0" in plan and _splitk(plan) > 1, plan
+    ctx.linear(w, xd, yd, **kw)
+    torch.cuda.synchronize()
+    g = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    if pair:
+        u = orc.gemm_gpu_semantics(x16.astype(np.float32), uf)
+        ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32))
+                        for r in range(m)])
+    else:
+        ref = g
+    assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
 
 
 @pytest.mark.parametrize("chunks", ["2", "3", "5", "64"])
