@@ -56,8 +56,9 @@ def parse():
                     help="run only the config-3 decode step timing and print its JSON (for "
                          "profiling that step); not the benchmark line")
     ap.add_argument("--config4-only", action="store_true",
-                    help="run only the config-4 timings (M in {16, 64, 512}, Q4 and Q8) and print "
-                         "their JSON (for profiling those kernels); not the benchmark line")
+                    help="run only the config-4 timings (M in {16, 64, 512}, Q4 and Q8; batched "
+                         "copies and single layers) and print their JSON (for profiling those "
+                         "kernels); not the benchmark line")
     ap.add_argument("--calib", action="store_true",
                     help="also run one 256 MiB fp32 neg kernel (known HBM traffic) to scale "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -254,6 +255,89 @@ def config4(torch, aexq, synth, ctx, copies: int = 120):
     return out
 
 
+def config4_single(torch, aexq, synth, ctx, copies: int = 24):
+    """Config 4 as a short prefill meets it: one layer's four launches (q/k/v
+    group and gate/up pair with RMSNorm-in, o_proj, down) on ONE copy of the
+    weights per launch, in Q4 (group 32, fp16 scales), Q8 and the reference's
+    shipping Q4 (group 16, fp32 scales).  `copies` separate layers rotate so
+    the weights come cold from HBM (24 Q4 layers: 220 MB); the calls are
+    captured in a HIP graph and replayed, so the figure is GPU time per layer
+    (the MFMA kernels split K across workgroups here: a single layer has too
+    few output tiles to fill the part)."""
+    import numpy as np
+    out = {}
+    P4 = aexq.LAYOUT_PACK4_LINEAR
+    for tag, bits, group in (("q4", 4, 32), ("q8", 8, 0), ("q4g16", 4, 16)):
+        layers = []
+        wbytes = 0
+        for c in range(copies):
+            ws = {}
+            for i, (name, n, k) in enumerate(synth.LAYER_LINEARS):
+                if bits == 4:
+                    sdt = np.float32 if group == 16 else np.float16
+                    words, scales, _ = synth.q4_weights(n, k, 900 + i, group=group,
+                                                        code=synth.NIBBLE_OFFSET8, scale_dtype=sdt)
+                    qt = aexq.QuantizedTensor(n * k, group, words, scales, bits=4,
+                                              nibble_code=synth.NIBBLE_OFFSET8)
+                    if c == 0:
+                        wbytes += n * k // 2 + scales.nbytes
+                else:
+                    words, scales, _ = synth.q8_weights(n, k, 900 + i)
+                    qt = aexq.QuantizedTensor(n * k, k, words, scales, bits=8)
+                    if c == 0:
+                        wbytes += n * k + scales.nbytes
+                ws[name] = ctx.weight(qt, n, k)
+            layers.append(ws)
+        gamma = torch.as_tensor(synth.rms_gamma(1024, 801)).cuda()
+        for m in (16, 64, 512):
+            xs = {k: torch.as_tensor(synth.activations(m, k, 800 + k)).cuda() for k in (1024, 2048, 3584)}
+            ys = {name: torch.zeros(m * n, dtype=torch.float16, device="cuda")
+                  for name, n, _ in synth.LAYER_LINEARS}
+            d = aexq.describe
+            yd = {name: d(ys[name], m, n, P4) for name, n, _ in synth.LAYER_LINEARS}
+            xd = {k: d(v, m, k) for k, v in xs.items()}
+            it = [0]
+
+            def step():
+                ws = layers[it[0] % copies]
+                it[0] += 1
+                ctx.linear_group([ws["q_proj"], ws["k_proj"], ws["v_proj"]], xd[1024],
+                                 [yd["q_proj"], yd["k_proj"], yd["v_proj"]],
+                                 rmsnorm=True, rms_gamma=gamma, rms_eps=1e-6)
+                ctx.linear(ws["gate_proj"], xd[1024], yd["gate_proj"], rmsnorm=True,
+                           rms_gamma=gamma, rms_eps=1e-6, up=ws["up_proj"])
+                ctx.linear(ws["o_proj"], xd[2048], yd["o_proj"])
+                ctx.linear(ws["down_proj"], xd[3584], yd["down_proj"])
+            for _ in range(copies):
+                step()   # plans and scratch sized before the capture
+            torch.cuda.synchronize()
+            stream = torch.cuda.Stream()
+            ctx.set_stream(stream)
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                step()
+            stream.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for _ in range(copies):
+                    step()
+            ctx.set_stream(torch.cuda.current_stream())
+            g.replay()
+            torch.cuda.synchronize()
+            avg, med = time_launches(torch, g.replay, 10)
+            us = med * 1e3 / copies
+            b = wbytes + m * 46_080
+            out[f"config4_single_{tag}_m{m}"] = {
+                "us_per_layer": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                "TFLOPs": round(2 * m * 16_252_928 / us / 1e6, 1), "copies_rotated": copies}
+            log(f"config4 single {tag} m={m}: {out[f'config4_single_{tag}_m{m}']}")
+            del g, xs, ys
+        for ws in layers:
+            for w in ws.values():
+                w.release()
+    return out
+
+
 def config3(torch, aexq, ctx, steps: int = 30):
     """Benchmark config 3: one full synthetic Qwen3.5-0.8B-shaped decode step
     (24 layers, 2048 cached positions, Q8 LM head with argmax), eager and as a
@@ -390,7 +474,9 @@ def main():
         print(json.dumps(config3(torch, aexq, ctx, steps=max(args.steps, 10))), flush=True)
         return
     if args.config4_only:
-        print(json.dumps(config4(torch, aexq, synth, ctx)), flush=True)
+        res = config4(torch, aexq, synth, ctx)
+        res.update(config4_single(torch, aexq, synth, ctx))
+        print(json.dumps(res), flush=True)
         return
     if args.calib:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
@@ -457,6 +543,7 @@ def main():
         result["extra"] = extras(torch, aexq, synth, ctx)
         result["extra"].update(config3(torch, aexq, ctx))
         result["extra"].update(config4(torch, aexq, synth, ctx))
+        result["extra"].update(config4_single(torch, aexq, synth, ctx))
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
