@@ -289,3 +289,61 @@ def test_batched_stack_keeps_whole_tiles(ctx, aexq, orc):
                                         batch_stride=m * n))
     assert _splitk(plan) == 1, plan
     st.release()
+
+
+def test_split_graph_replays_match_eager(ctx, aexq, orc):
+    """A layer's split launches (q/k/v group, gate/up pair, o_proj, down at M = 16
+    and 64) captured in a HIP graph: every replay, with eager work between
+    replays, equals the eager result bit for bit (the partial planes are fully
+    rewritten by each launch; nothing is cleared with a memset node)."""
+    _announce("splitk graph replays")
+    from aiimage_amd import synth
+    P4 = aexq.LAYOUT_PACK4_LINEAR
+    ws = {}
+    for i, (name, n, k) in enumerate(synth.LAYER_LINEARS):
+        ws[name] = _weight(ctx, aexq, orc, 4, n, k, 101 + i)[0]
+    gamma = dev(synth.rms_gamma(1024, 102))
+    for m in (16, 64):
+        xs = {k: dev(synth.activations(m, k, 103 + k)) for k in (1024, 2048, 3584)}
+        xd = {k: aexq.describe(v, m, k) for k, v in xs.items()}
+        ys = {name: torch.zeros(m * n, dtype=torch.float16, device="cuda")
+              for name, n, _ in synth.LAYER_LINEARS}
+        yd = {name: aexq.describe(ys[name], m, n, P4) for name, n, _ in synth.LAYER_LINEARS}
+
+        def step():
+            ctx.linear_group([ws["q_proj"], ws["k_proj"], ws["v_proj"]], xd[1024],
+                             [yd["q_proj"], yd["k_proj"], yd["v_proj"]],
+                             rmsnorm=True, rms_gamma=gamma, rms_eps=1e-6)
+            ctx.linear(ws["gate_proj"], xd[1024], yd["gate_proj"], rmsnorm=True,
+                       rms_gamma=gamma, rms_eps=1e-6, up=ws["up_proj"])
+            ctx.linear(ws["o_proj"], xd[2048], yd["o_proj"])
+            ctx.linear(ws["down_proj"], xd[3584], yd["down_proj"])
+
+        assert _splitk(ctx.plan_check(ws["down_proj"], xd[3584], yd["down_proj"])) > 1
+        step()
+        torch.cuda.synchronize()
+        eager = {k: v.clone() for k, v in ys.items()}
+        stream = torch.cuda.Stream()
+        ctx.set_stream(stream)
+        try:
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                step()
+            stream.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step()
+        finally:
+            ctx.set_stream(torch.cuda.current_stream())
+        for rep in range(3):
+            for v in ys.values():
+                v.zero_()
+            # eager work between replays: another launch through the same scratch
+            other = torch.zeros(m * 1024, dtype=torch.float16, device="cuda")
+            ctx.linear(ws["o_proj"], xd[2048], aexq.describe(other, m, 1024, P4))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            for name in ys:
+                assert torch.equal(ys[name], eager[name]), (m, rep, name)
+        del g
