@@ -1124,10 +1124,14 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     if (plan->grid < 1) plan->grid = 1;
   } else if (plan->fast) {
     // persistent grid: every wave resident, each owning a contiguous tile range
-    // Q4's heavier unpack streams best with twice the resident waves queued
-    // (8 workgroups of 4 waves per CU); Q8 with the resident count
+    // Workgroups queued beyond the resident count stream best: Q4 16 of 4
+    // waves per CU (config 2, against 6, 8, 12, 20, 24 and 32), Q8 12 (config
+    // 1, against the resident count, 8 and 16); an argmax launch keeps the
+    // resident count (each workgroup adds a partial to the merge: the LM head
+    // at 16 per CU runs 20% slower)
     int per_cu = qmv_blocks_per_cu(plan->entry);
-    if (fmt == kQ4 && per_cu < 8) per_cu = 8;
+    const int queued = argmax ? per_cu : (fmt == kQ4 ? 16 : 12);
+    if (per_cu < queued) per_cu = queued;
     const char* env = getenv("AEXQ_QMV_BLOCKS_PER_CU");
     if (env && atoi(env) > 0) per_cu = atoi(env);
     const long long need = ((long long)tiles_total + kWaves - 1) / kWaves;
