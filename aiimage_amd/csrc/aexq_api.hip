@@ -1120,7 +1120,13 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
                  &plan->sk_cs);
     const long long items = (long long)tiles_total * plan->sk_chunks;
     const long long need = wide ? items : (items + kWaves - 1) / kWaves;
-    plan->grid = (int)(need < cap ? need : cap);
+    // Q8 on the wide kernel streams best with 6 workgroups per CU queued
+    // (config 4, M = 16: 5.35 TB/s at the resident 2, 5.71 at 6); Q4 with the
+    // resident count (3.80 at 2, 3.36 at 6)
+    long long grid_cap = cap;
+    if (wide && fmt == kQ8 && !plan->mentry->cfg.argmax && !env && per_cu < 6)
+      grid_cap = 6LL * ctx->cus;
+    plan->grid = (int)(need < grid_cap ? need : grid_cap);
     if (plan->grid < 1) plan->grid = 1;
   } else if (plan->fast) {
     // persistent grid: every wave resident, each owning a contiguous tile range
