@@ -1128,6 +1128,22 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       grid_cap = 6LL * ctx->cus;
     plan->grid = (int)(need < grid_cap ? need : grid_cap);
     if (plan->grid < 1) plan->grid = 1;
+    // RMSNorm-in inside the wide kernel when every item has its own workgroup
+    // (the row pre-pass would be a launch of its own, ~4 us, next to a few
+    // microseconds of kernel): fp16 rows 16-byte aligned, K within the LDS
+    // gamma stage; AEXQ_RMS_PREPASS keeps the pre-pass
+    if (wide && plan->rms_prepass && !plan->mentry->cfg.argmax && items <= grid_cap && x_ok &&
+        K <= 4096 && K % 8 == 0 && getenv("AEXQ_RMS_PREPASS") == nullptr) {
+      QmmConfig rc = plan->mentry->cfg;
+      rc.rmsx = true;
+      const QmmEntry* re = qmm_find(rc);
+      if (re) {
+        plan->mentry = re;
+        plan->rms_prepass = false;
+        p.x_rstride = xv.rstride;
+        for (int i = 0; i < count; ++i) p.mat[i].x_bstride = xv.batch == 1 ? 0 : xv.bstride;
+      }
+    }
   } else if (plan->fast) {
     // persistent grid: every wave resident, each owning a contiguous tile range
     // Workgroups queued beyond the resident count stream best: Q4 16 of 4

@@ -123,6 +123,7 @@ struct QmmConfig {
   bool pair, sf16;  // SwiGLU pair; fp16 (else fp32) scales
   bool wide;        // 256-wide K steps (aexq_qmmw.hpp; K % 256 == 0, Q8 or Q4 group 32)
   bool argmax;      // fused argmax partials (wide kernel only)
+  bool rmsx;        // RMSNorm-in inside the kernel (wide kernel, one item per workgroup)
 };
 struct QmmEntry {
   QmmConfig cfg;

@@ -34,7 +34,7 @@ const QmmEntry* qmm_find(const QmmConfig& c) {
   for (int i = 0; i < n; ++i) {
     const QmmConfig& q = t[i].cfg;
     if (q.fmt == c.fmt && q.gmode == c.gmode && q.mt == c.mt && q.nt == c.nt &&
-        q.pair == c.pair && q.sf16 == c.sf16 && q.argmax == c.argmax)
+        q.pair == c.pair && q.sf16 == c.sf16 && q.argmax == c.argmax && q.rmsx == c.rmsx)
       return &t[i];
   }
   return nullptr;

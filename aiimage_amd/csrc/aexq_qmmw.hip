@@ -5,12 +5,14 @@
 
 namespace aexq {
 
-#define QMMWA(FMT, MT, NT, PAIR, SF16, AM)                                                    \
+#define QMMWX(FMT, MT, NT, PAIR, SF16, AM, RX)                                                \
   QmmEntry {                                                                                  \
-    QmmConfig{FMT, FMT == kQ8 ? kGRow : kG32, MT, NT, PAIR, SF16, true, AM},                  \
-        &qmmw_kernel<FMT, MT, NT, PAIR, SF16, AM>, kWaves * 16 * NT                           \
+    QmmConfig{FMT, FMT == kQ8 ? kGRow : kG32, MT, NT, PAIR, SF16, true, AM, RX},              \
+        &qmmw_kernel<FMT, MT, NT, PAIR, SF16, AM, RX>, kWaves * 16 * NT                       \
   }
+#define QMMWA(FMT, MT, NT, PAIR, SF16, AM) QMMWX(FMT, MT, NT, PAIR, SF16, AM, false)
 #define QMMWE(FMT, MT, NT, PAIR, SF16) QMMWA(FMT, MT, NT, PAIR, SF16, false)
+#define QMMWR(FMT, MT, NT, PAIR, SF16) QMMWX(FMT, MT, NT, PAIR, SF16, false, true)
 
 // Blocks per wave: 4 at M <= 16, 2 at M <= 32, halved for SwiGLU pairs; Q8
 // at M <= 16 half of that (its steps carry twice the code bytes, and the
@@ -22,12 +24,18 @@ namespace aexq {
   QMMWE(kQ8, 1, 2, false, SF16), QMMWE(kQ8, 2, 2, false, SF16), QMMWE(kQ8, 1, 1, true, SF16), \
       QMMWE(kQ8, 2, 1, true, SF16)
 
+// RMSNorm-in inside the kernel, for launches with one item per workgroup
+#define QMMW_R(FMT, SF16)                                                                     \
+  QMMWR(FMT, 1, FMT == kQ8 ? 2 : 4, false, SF16), QMMWR(FMT, 2, 2, false, SF16),              \
+      QMMWR(FMT, 1, FMT == kQ8 ? 1 : 2, true, SF16), QMMWR(FMT, 2, 1, true, SF16)
+
 // LM heads at M = 2..32 with the fused argmax partials (single weights)
 #define QMMW_AM(FMT, SF16) QMMWA(FMT, 1, 1, false, SF16, true), QMMWA(FMT, 2, 1, false, SF16, true)
 
-static const QmmEntry kTableW[] = {QMMW_Q4(true),      QMMW_Q4(false),      QMMW_Q8(true),
-                                   QMMW_Q8(false),     QMMW_AM(kQ4, true),  QMMW_AM(kQ4, false),
-                                   QMMW_AM(kQ8, true), QMMW_AM(kQ8, false)};
+static const QmmEntry kTableW[] = {
+    QMMW_Q4(true),       QMMW_Q4(false),       QMMW_Q8(true),       QMMW_Q8(false),
+    QMMW_AM(kQ4, true),  QMMW_AM(kQ4, false),  QMMW_AM(kQ8, true),  QMMW_AM(kQ8, false),
+    QMMW_R(kQ4, true),   QMMW_R(kQ4, false),   QMMW_R(kQ8, true),   QMMW_R(kQ8, false)};
 
 static constexpr int kCountW = (int)(sizeof(kTableW) / sizeof(kTableW[0]));
 

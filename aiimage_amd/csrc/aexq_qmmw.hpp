@@ -24,7 +24,7 @@
 
 namespace aexq {
 
-template <int FMT, int MT, int NT, bool PAIR, bool SF16, bool ARGMAX>
+template <int FMT, int MT, int NT, bool PAIR, bool SF16, bool ARGMAX, bool RMSX = false>
 struct QmmW {
   static constexpr int GM = FMT == kQ8 ? kGRow : kG32;
   using Base = Qmm<FMT, GM, MT, NT, PAIR, SF16>;
@@ -144,16 +144,69 @@ struct QmmW {
                        xr, (16 * m + row) * (int)rs2 + col + 16 * v, 0, 0));
   }
 
+  // RMSNorm-in inside the kernel (RMSX: launches with one item per workgroup,
+  // where the row pre-pass would be a launch of its own): gamma[0, K) staged in
+  // LDS and 1 / rms of the workgroup's 16 MT activation rows over all of K,
+  // as the pre-pass forms them (CC:4531-4557).
+  static constexpr int kMaxRmsK = 4096;
+  static __device__ __forceinline__ void rms_prologue(const QmvParams& p, const Cursor& cu,
+                                                      int lane, int wave, float* gs, float* inv) {
+    for (int i = threadIdx.x; i < p.k; i += kThreads)
+      gs[i] = p.gamma ? p.gamma[i < p.gamma_size - 1 ? i : p.gamma_size - 1] : 1.0f;
+    const QmvMat& mt = p.mat[cu.j];
+    const int rs2 = (int)(p.x_rstride * 2);
+    const char* xb = (const char*)mt.x + cu.b * mt.x_bstride * 2;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)xb, (short)0, p.m * rs2, kBufferRsrcWord3);  // rows past M read 0
+    constexpr int RPW = 16 * MT / kWaves;  // rows per wave: wave + kWaves r
+    float ss[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) ss[r] = 0.0f;
+    for (int c8 = lane; c8 < p.k / 8; c8 += 64) {
+      u32x4 v[RPW];
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+        v[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             xr, (wave + kWaves * r) * rs2 + c8 * 16, 0, 0));
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f16x2 h = as_h2(v[r][e]);
+          ss[r] = fmaf((float)h[0], (float)h[0], ss[r]);
+          ss[r] = fmaf((float)h[1], (float)h[1], ss[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const float t = wave_sum(ss[r]);
+      if (lane == 0) inv[wave + kWaves * r] = rsqrtf(fmaxf(t / (float)p.k + p.eps, 1e-20f));
+    }
+  }
+
   // Stores the slice; Q4 chunks of 8 activations go in the (p, p + 4) pair
   // order that q4_pairs gives the codes, once per workgroup rather than per
-  // MFMA.
-  static __device__ __forceinline__ void store_x(uint8_t* xs, const u32x4 (&xv)[XV]) {
+  // MFMA.  RMSX: each activation becomes fp16(x * inv[row] * gamma[k]) first.
+  static __device__ __forceinline__ void store_x(uint8_t* xs, const u32x4 (&xv)[XV],
+                                                 int step = 0, const float* gs = nullptr,
+                                                 const float* inv = nullptr) {
     const int row = threadIdx.x >> 4, col = (threadIdx.x & 15) * 32;
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
       for (int v = 0; v < 2; ++v) {
         u32x4 c = xv[2 * m + v];
+        if constexpr (RMSX) {
+          const float iv = inv[16 * m + row];
+          const float* g = gs + step * 256 + (col >> 1) + 8 * v;  // col counts bytes
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const f16x2 h = as_h2(c[e]);
+            const f16x2 o = {(f16)((float)h[0] * iv * g[2 * e]),
+                             (f16)((float)h[1] * iv * g[2 * e + 1])};
+            c[e] = as_u(o);
+          }
+        }
         if constexpr (FMT == kQ4) {
           uint32_t xp[4];
           q4_xpairs(c[0], c[1], c[2], c[3], xp);
@@ -347,10 +400,12 @@ struct QmmW {
   }
 };
 
-template <int FMT, int MT, int NT, bool PAIR, bool SF16, bool ARGMAX>
+template <int FMT, int MT, int NT, bool PAIR, bool SF16, bool ARGMAX, bool RMSX>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void qmmw_kernel(const QmvParams p) {
-  using Q = QmmW<FMT, MT, NT, PAIR, SF16, ARGMAX>;
+  using Q = QmmW<FMT, MT, NT, PAIR, SF16, ARGMAX, RMSX>;
+  __shared__ float rms_g[RMSX ? Q::kMaxRmsK : 1];   // gamma (RMSX)
+  __shared__ float rms_inv[RMSX ? 16 * MT : 1];      // 1 / rms per activation row (RMSX)
   __shared__ __align__(16) uint8_t lds_all[kWaves][Q::LDS_WAVE];
   __shared__ __align__(16) uint8_t xs_all[2][Q::XSL];
   const int lane = threadIdx.x & 63;
@@ -412,9 +467,11 @@ void qmmw_kernel(const QmvParams p) {
       Q::Base::spill(p, mine(c), lane, c.s / cs, acc);
     }
   };
+  if constexpr (RMSX) Q::rms_prologue(p, cu, lane, wave, rms_g, rms_inv);
   Q::load_x(p, cu, xv);
   Q::load(p, cu, lane, wave, A);
-  Q::store_x(xs_all[0], xv);
+  if constexpr (RMSX) __syncthreads();  // gamma and 1 / rms in LDS
+  Q::store_x(xs_all[0], xv, cu.s, rms_g, rms_inv);
   __syncthreads();
   int t = t0;
   int sl = 0;
@@ -436,7 +493,7 @@ void qmmw_kernel(const QmvParams p) {
       seg = cs;
     }
     if (!more) break;
-    Q::store_x(xs_all[sl ^ 1], xv);
+    Q::store_x(xs_all[sl ^ 1], xv, nx.s, rms_g, rms_inv);
     __syncthreads();
     ++t;
     cu = nx;
@@ -452,7 +509,7 @@ void qmmw_kernel(const QmvParams p) {
       seg = cs;
     }
     if (!more) break;
-    Q::store_x(xs_all[sl ^ 1], xv);
+    Q::store_x(xs_all[sl ^ 1], xv, nx.s, rms_g, rms_inv);
     __syncthreads();
     ++t;
     cu = nx;

@@ -585,9 +585,13 @@ def test_small_m_mfma_reference_q4_formats(ctx, aexq, orc, group, scale_f16, cod
     assert normwise(got, ref) <= 1e-5
 
 
-def test_small_m_mfma_swiglu_rmsnorm(ctx, aexq, orc):
-    """M=20 gate/up with RMSNorm-in (row pre-pass) and SwiGLU-out on the MFMA path."""
-    _announce("mfma swiglu rmsnorm m=20")
+@pytest.mark.parametrize("prepass", [False, True])
+def test_small_m_mfma_swiglu_rmsnorm(ctx, aexq, orc, monkeypatch, prepass):
+    """M=20 gate/up with RMSNorm-in and SwiGLU-out on the MFMA path: inside the
+    wide kernel (one item per workgroup) or as the row pre-pass."""
+    _announce(f"mfma swiglu rmsnorm m=20 prepass={prepass}")
+    if prepass:
+        monkeypatch.setenv("AEXQ_RMS_PREPASS", "1")
     from aiimage_amd import synth
     n, k, m, eps = 3584, 1024, 20, 1e-6
     wg, gw, gs = _q4_weight(ctx, aexq, n, k, 61)
@@ -599,7 +603,7 @@ def test_small_m_mfma_swiglu_rmsnorm(ctx, aexq, orc):
     yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
     kw = dict(rmsnorm=True, rms_gamma=dev(gamma), rms_eps=eps, up=wu)
     plan = ctx.plan_check(wg, xd, yd, **kw)
-    assert plan.startswith("kernel=qmm") and "rms_prepass=1" in plan, plan
+    assert plan.startswith("kernel=qmm") and f"rms_prepass={int(prepass)}" in plan, plan
     ctx.linear(wg, xd, yd, **kw)
     torch.cuda.synchronize()
     xn = orc.rmsnorm(x16.astype(np.float32), eps, gamma).astype(np.float16).astype(np.float32)

@@ -347,3 +347,58 @@ def test_split_graph_replays_match_eager(ctx, aexq, orc):
             for name in ys:
                 assert torch.equal(ys[name], eager[name]), (m, rep, name)
         del g
+
+
+@pytest.mark.parametrize("bits,m,pair,group", [
+    (4, 16, False, False), (4, 9, True, False), (8, 24, False, False), (8, 32, True, False),
+    (4, 16, False, True),   # a q/k/v group sharing one normalised input
+])
+def test_rmsnorm_in_kernel(ctx, aexq, orc, monkeypatch, bits, m, pair, group):
+    """RMSNorm-in inside the wide kernel (launches with one item per workgroup):
+    no pre-pass launch, the oracle's RMSNorm -> fp16 -> Gemm within the fp16 bar,
+    and the pre-pass path's result within one fp16 rounding of the inputs."""
+    _announce(f"rmsnorm in-kernel q{bits} m={m} pair={pair} group={group}")
+    from aiimage_amd import synth
+    k, eps = 1024, 1e-6
+    shapes = [2048, 512, 512] if group else [1024]
+    ws, wfs = [], []
+    for i, n in enumerate(shapes):
+        w, wf = _weight(ctx, aexq, orc, bits, n, k, 121 + i + m)
+        ws.append(w)
+        wfs.append(wf)
+    kw = dict(rmsnorm=True, rms_gamma=dev(synth.rms_gamma(k, 122)), rms_eps=eps)
+    if pair:
+        wu, uf = _weight(ctx, aexq, orc, bits, shapes[0], k, 123 + m)
+        kw["up"] = wu
+    x16 = synth.activations(m, k, 124)
+    xd = aexq.describe(dev(x16), m, k)
+    P4 = aexq.LAYOUT_PACK4_LINEAR
+
+    def run():
+        ys = [aexq.new_activation(m, n, torch.float16, P4) for n in shapes]
+        yds = [aexq.describe(y, m, n, P4) for y, n in zip(ys, shapes)]
+        if group:
+            ctx.linear_group(ws, xd, yds, **kw)
+        else:
+            ctx.linear(ws[0], xd, yds[0], **kw)
+        torch.cuda.synchronize()
+        return ys, ctx.plan_check(ws[0], xd, yds[0], **kw)
+
+    ys, plan = run()
+    assert "wide=1" in plan and "rms_prepass=0" in plan, plan
+    monkeypatch.setenv("AEXQ_RMS_PREPASS", "1")
+    ys_pre, plan_pre = run()
+    assert "rms_prepass=1" in plan_pre, plan_pre
+    xn = orc.rmsnorm(x16.astype(np.float32), eps, synth.rms_gamma(k, 122))
+    xn = xn.astype(np.float16).astype(np.float32)
+    for y, yp, wf, n in zip(ys, ys_pre, wfs, shapes):
+        g = orc.gemm_gpu_semantics(xn, wf)
+        if pair:
+            u = orc.gemm_gpu_semantics(xn, uf)
+            ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32))
+                            for r in range(m)])
+        else:
+            ref = g
+        got = y.cpu().numpy().astype(np.float64).reshape(m, n)
+        assert normwise(got, ref) <= TOL
+        assert normwise(got, yp.cpu().numpy().astype(np.float64).reshape(m, n)) <= TOL
