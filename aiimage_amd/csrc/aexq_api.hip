@@ -703,7 +703,10 @@ static void pick_split(long long units, int steps, long long slots, double step_
   if (steps < 2 || units < 1 || slots < 1) return;
   const char* env = getenv("AEXQ_SPLITK");
   if (env && atoi(env) >= 1) {
-    const int want = atoi(env) < steps ? atoi(env) : steps;
+    int want = atoi(env) < steps ? atoi(env) : steps;
+    // within the same partial-plane budget as the model's choice
+    const long long fit = plane_bytes > 0 ? (long long)(kMaxPartBytes / plane_bytes) : steps;
+    if (want > fit) want = fit > 1 ? (int)fit : 1;
     *cs = (steps + want - 1) / want;
     *chunks = (steps + *cs - 1) / *cs;
     if (*chunks < 2) *cs = steps;
