@@ -151,7 +151,8 @@ struct QmmW {
   static constexpr int kMaxRmsK = 4096;
   static __device__ __forceinline__ void rms_prologue(const QmvParams& p, const Cursor& cu,
                                                       int lane, int wave, float* gs, float* inv) {
-    for (int i = threadIdx.x; i < p.k; i += kThreads)
+    const int kg = p.k < kMaxRmsK ? p.k : kMaxRmsK;  // the plan keeps K <= kMaxRmsK
+    for (int i = threadIdx.x; i < kg; i += kThreads)
       gs[i] = p.gamma ? p.gamma[i < p.gamma_size - 1 ? i : p.gamma_size - 1] : 1.0f;
     const QmvMat& mt = p.mat[cu.j];
     const int rs2 = (int)(p.x_rstride * 2);
