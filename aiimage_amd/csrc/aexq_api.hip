@@ -961,7 +961,7 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     const int mt = M <= 16 ? 1 : 2;
     // 256-wide K steps whose code fetches cover 128 contiguous bytes of 8 rows
     // per instruction, where K and the scale layout allow
-    const bool wide = K % 256 == 0 && (fmt == kQ8 || gmode == kG32) &&
+    const bool wide = K % 256 == 0 && (fmt == kQ8 || gmode == kG32 || gmode == kG16) &&
                       getenv("AEXQ_QMM_NARROW") == nullptr;
     const int nt = swiglu ? (mt == 1 ? 2 : 1) : (mt == 1 ? 4 : 2);
     QmmConfig mc{fmt, gmode, mt, nt, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16, false, false};
@@ -969,6 +969,7 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       QmmConfig wc = mc;
       wc.wide = true;
       if (fmt == kQ8 && mt == 1) wc.nt = nt > 1 ? nt / 2 : 1;
+      if (gmode == kG16) wc.nt = nt > 1 ? nt / 2 : 1;  // twice the scales per block
       if (argmax) {
         // the LM head: argmax partials fused, one 16-row block per wave (more,
         // shorter workgroups over the vocabulary measured faster)

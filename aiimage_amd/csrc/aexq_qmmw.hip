@@ -5,11 +5,12 @@
 
 namespace aexq {
 
-#define QMMWX(FMT, MT, NT, PAIR, SF16, AM, RX)                                                \
+#define QMMWG(FMT, MT, NT, PAIR, SF16, AM, RX, G16)                                           \
   QmmEntry {                                                                                  \
-    QmmConfig{FMT, FMT == kQ8 ? kGRow : kG32, MT, NT, PAIR, SF16, true, AM, RX},              \
-        &qmmw_kernel<FMT, MT, NT, PAIR, SF16, AM, RX>, kWaves * 16 * NT                       \
+    QmmConfig{FMT, FMT == kQ8 ? kGRow : (G16 ? kG16 : kG32), MT, NT, PAIR, SF16, true, AM, RX}, \
+        &qmmw_kernel<FMT, MT, NT, PAIR, SF16, AM, RX, G16>, kWaves * 16 * NT                  \
   }
+#define QMMWX(FMT, MT, NT, PAIR, SF16, AM, RX) QMMWG(FMT, MT, NT, PAIR, SF16, AM, RX, false)
 #define QMMWA(FMT, MT, NT, PAIR, SF16, AM) QMMWX(FMT, MT, NT, PAIR, SF16, AM, false)
 #define QMMWE(FMT, MT, NT, PAIR, SF16) QMMWA(FMT, MT, NT, PAIR, SF16, false)
 #define QMMWR(FMT, MT, NT, PAIR, SF16) QMMWX(FMT, MT, NT, PAIR, SF16, false, true)
@@ -29,13 +30,21 @@ namespace aexq {
   QMMWR(FMT, 1, FMT == kQ8 ? 2 : 4, false, SF16), QMMWR(FMT, 2, 2, false, SF16),              \
       QMMWR(FMT, 1, FMT == kQ8 ? 1 : 2, true, SF16), QMMWR(FMT, 2, 1, true, SF16)
 
+// Q4 with one scale per 16 codes (the reference's shipping Q4), plain and with
+// RMSNorm-in inside the kernel
+// (half the blocks per wave of group 32: a block carries twice the scales)
+#define QMMW_G16(SF16, RX)                                                                    \
+  QMMWG(kQ4, 1, 2, false, SF16, false, RX, true), QMMWG(kQ4, 2, 1, false, SF16, false, RX, true), \
+      QMMWG(kQ4, 1, 1, true, SF16, false, RX, true), QMMWG(kQ4, 2, 1, true, SF16, false, RX, true)
+
 // LM heads at M = 2..32 with the fused argmax partials (single weights)
 #define QMMW_AM(FMT, SF16) QMMWA(FMT, 1, 1, false, SF16, true), QMMWA(FMT, 2, 1, false, SF16, true)
 
 static const QmmEntry kTableW[] = {
     QMMW_Q4(true),       QMMW_Q4(false),       QMMW_Q8(true),       QMMW_Q8(false),
     QMMW_AM(kQ4, true),  QMMW_AM(kQ4, false),  QMMW_AM(kQ8, true),  QMMW_AM(kQ8, false),
-    QMMW_R(kQ4, true),   QMMW_R(kQ4, false),   QMMW_R(kQ8, true),   QMMW_R(kQ8, false)};
+    QMMW_R(kQ4, true),   QMMW_R(kQ4, false),   QMMW_R(kQ8, true),   QMMW_R(kQ8, false),
+    QMMW_G16(true, false), QMMW_G16(false, false), QMMW_G16(true, true), QMMW_G16(false, true)};
 
 static constexpr int kCountW = (int)(sizeof(kTableW) / sizeof(kTableW[0]));
 

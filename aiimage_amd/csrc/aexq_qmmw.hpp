@@ -24,9 +24,16 @@
 
 namespace aexq {
 
-template <int FMT, int MT, int NT, bool PAIR, bool SF16, bool ARGMAX, bool RMSX = false>
+template <int FMT, int MT, int NT, bool PAIR, bool SF16, bool ARGMAX, bool RMSX = false,
+          bool G16 = false>
 struct QmmW {
-  static constexpr int GM = FMT == kQ8 ? kGRow : kG32;
+  // G16: Q4 with one scale per 16 codes (the reference's shipping Q4): an MFMA
+  // K extent holds two groups, lane quarters kb = 0, 1 the first and 2, 3 the
+  // second, so two MFMAs with the other group's quarters zeroed give each
+  // group's product, scaled in fp32 like a 32-code group's
+  static_assert(!G16 || FMT == kQ4, "16-code groups are a Q4 form");
+  static constexpr int GM = FMT == kQ8 ? kGRow : (G16 ? kG16 : kG32);
+  static constexpr int GPS = G16 ? 16 : 8;  // scale groups per 256-wide step
   using Base = Qmm<FMT, GM, MT, NT, PAIR, SF16>;
   using Cursor = typename Base::Cursor;  // s = 256-wide K step
   using Acc = typename Base::Acc;
@@ -41,7 +48,7 @@ struct QmmW {
   static constexpr int RS = RB + 32;                 // LDS row stride (padded against conflicts)
   static constexpr int BLK = 16 * RS;                // LDS bytes of one 16-row block
   static constexpr int LDS_WAVE = NW * NT * BLK;
-  static constexpr int SV = FMT == kQ8 ? 0 : (SF16 ? 1 : 2);  // 16-byte scale loads per block
+  static constexpr int SV = FMT == kQ8 ? 0 : (SF16 ? 1 : 2) * (G16 ? 2 : 1);  // 16-byte scale loads per block
 
   struct Buf {
     u32x4 w[NW][NT][WI];
@@ -90,7 +97,7 @@ struct QmmW {
     const int rows = mt.n > r0 ? mt.n - r0 : 0;
     const int wnum = rows > 0 ? rows * row_bytes - cu.s * RB : 0;
     const int sper = FMT == kQ8 ? 1 : p.groups_per_row;
-    const int snum = rows > 0 ? (rows * sper - cu.s * 8) * sb + 16 : 0;
+    const int snum = rows > 0 ? (rows * sper - cu.s * GPS) * sb + 16 : 0;
 #pragma unroll
     for (int h = 0; h < NW; ++h) {
       const char* wb = (const char*)(h == 0 ? mt.w : mt.w2) + (cu.b * mt.w_bstride) * 4 +
@@ -110,7 +117,7 @@ struct QmmW {
         }
       if constexpr (SV > 0) {
         const char* sbp = (const char*)(h == 0 ? mt.s : mt.s2) +
-                          (cu.b * mt.s_bstride + (long long)r0 * sper + cu.s * 8) * sb;
+                          (cu.b * mt.s_bstride + (long long)r0 * sper + cu.s * GPS) * sb;
         const __amdgpu_buffer_rsrc_t sr =
             __builtin_amdgcn_make_buffer_rsrc((void*)sbp, (short)0, snum, kBufferRsrcWord3);
 #pragma unroll
@@ -384,6 +391,27 @@ struct QmmW {
             if constexpr (FMT == kQ8) {
               acc.v[h][m][nt] =
                   __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[h][nt], acc.v[h][m][nt], 0, 0, 0);
+            } else if constexpr (G16) {
+              const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+              const f16x8 zb = {};
+              const bool first = kb < 2;
+              const f32x4 t0 =
+                  __builtin_amdgcn_mfma_f32_16x16x32_f16(af, first ? bf[h][nt] : zb, z, 0, 0, 0);
+              const f32x4 t1 =
+                  __builtin_amdgcn_mfma_f32_16x16x32_f16(af, first ? zb : bf[h][nt], z, 0, 0, 0);
+              float s0, s1;
+              if constexpr (SF16) {
+                s0 = Base::scale16(buf.s[h][nt][g >> 2], (2 * g) & 7);
+                s1 = Base::scale16(buf.s[h][nt][g >> 2], (2 * g + 1) & 7);
+              } else {
+                s0 = as_f32(buf.s[h][nt][g >> 1][(2 * g) & 3]);
+                s1 = as_f32(buf.s[h][nt][g >> 1][(2 * g + 1) & 3]);
+              }
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                acc.v[h][m][nt][r] = fmaf(s0, t0[r], acc.v[h][m][nt][r]);
+                acc.v[h][m][nt][r] = fmaf(s1, t1[r], acc.v[h][m][nt][r]);
+              }
             } else {
               const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
               const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[h][nt], z, 0, 0, 0);
@@ -401,10 +429,10 @@ struct QmmW {
   }
 };
 
-template <int FMT, int MT, int NT, bool PAIR, bool SF16, bool ARGMAX, bool RMSX>
+template <int FMT, int MT, int NT, bool PAIR, bool SF16, bool ARGMAX, bool RMSX, bool G16>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void qmmw_kernel(const QmvParams p) {
-  using Q = QmmW<FMT, MT, NT, PAIR, SF16, ARGMAX, RMSX>;
+  using Q = QmmW<FMT, MT, NT, PAIR, SF16, ARGMAX, RMSX, G16>;
   __shared__ float rms_g[RMSX ? Q::kMaxRmsK : 1];   // gamma (RMSX)
   __shared__ float rms_inv[RMSX ? 16 * MT : 1];      // 1 / rms per activation row (RMSX)
   __shared__ __align__(16) uint8_t lds_all[kWaves][Q::LDS_WAVE];

@@ -131,10 +131,11 @@ def test_split_matches_oracle(ctx, aexq, orc, monkeypatch, bits, scale_f16, n, k
     (4, 16, 1024, 3584, 32, True),    # ... gate/up pair at M = 32
     (8, 0, 1024, 1152, 16, False),    # K = 9 x 128: not a multiple of the wide step
 ])
-def test_split_narrow_kernel(ctx, aexq, orc, bits, group, n, k, m, pair):
-    """The 128-wide-slice MFMA kernel (group-16 scales, or K not a multiple of
-    256) splits K per wave tile the same way."""
+def test_split_narrow_kernel(ctx, aexq, orc, monkeypatch, bits, group, n, k, m, pair):
+    """The 128-wide-slice MFMA kernel (K not a multiple of 256, or switched to
+    with AEXQ_QMM_NARROW) splits K per wave tile the same way."""
     _announce(f"splitk narrow q{bits} g={group} n={n} k={k} m={m} pair={pair}")
+    monkeypatch.setenv("AEXQ_QMM_NARROW", "1")
     from aiimage_amd import synth
     w, wf = _weight(ctx, aexq, orc, bits, n, k, 91 + m, group=group or k, scale_f16=False,
                     code=0)
@@ -159,6 +160,48 @@ def test_split_narrow_kernel(ctx, aexq, orc, bits, group, n, k, m, pair):
     else:
         ref = g
     assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
+
+
+@pytest.mark.parametrize("scale_f16,m,pair,rms", [
+    (False, 16, False, False),   # the reference's shipping Q4: group 16, fp32 scales
+    (False, 32, True, True),     # gate/up pair at M = 32 with RMSNorm-in in the kernel
+    (True, 9, False, True),      # fp16 scales, RMSNorm-in
+])
+def test_wide_kernel_group16(ctx, aexq, orc, scale_f16, m, pair, rms):
+    """Group-16 Q4 on the wide kernel: two MFMAs per 32-code extent, each
+    group's product scaled in fp32 (exact float(q) * scale)."""
+    _announce(f"wide group16 f16={scale_f16} m={m} pair={pair} rms={rms}")
+    from aiimage_amd import synth
+    n, k, eps = 1024, 2048, 1e-6
+    w, wf = _weight(ctx, aexq, orc, 4, n, k, 131 + m, group=16, scale_f16=scale_f16, code=0)
+    kw = {}
+    if pair:
+        wu, uf = _weight(ctx, aexq, orc, 4, n, k, 132 + m, group=16, scale_f16=scale_f16, code=0)
+        kw["up"] = wu
+    gamma = synth.rms_gamma(k, 133)
+    if rms:
+        kw.update(rmsnorm=True, rms_gamma=dev(gamma), rms_eps=eps)
+    x16 = synth.activations(m, k, 134)
+    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    plan = ctx.plan_check(w, xd, yd, **kw)
+    assert plan.startswith("kernel=qmm") and "wide=1" in plan, plan
+    ctx.linear(w, xd, yd, **kw)
+    torch.cuda.synchronize()
+    xr = x16.astype(np.float32)
+    if rms:
+        xr = orc.rmsnorm(xr, eps, gamma).astype(np.float16).astype(np.float32)
+    g = orc.gemm_gpu_semantics(xr, wf)
+    if pair:
+        u = orc.gemm_gpu_semantics(xr, uf)
+        ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32))
+                        for r in range(m)])
+    else:
+        ref = g
+    # RMSNorm-in rounds the normalised input to fp16 as the pre-pass does; with
+    # it the fp32 output meets the fp16 bar (1 / rms may differ in the last bit)
+    assert normwise(y.cpu().numpy().reshape(m, n), ref) <= (TOL if rms else TOL32)
 
 
 @pytest.mark.parametrize("chunks", ["2", "3", "5", "64"])
