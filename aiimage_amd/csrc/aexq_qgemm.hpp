@@ -111,29 +111,35 @@ struct QGemm {
     return s;
   }
 
-  // Issues the global loads of step st (rows past M or N read 0).
-  static __device__ __forceinline__ void load(const QmvParams& p, const Src& s, int st, int tid,
-                                              Regs& r) {
+  // Issues the global loads of step st (rows past M or N read 0).  A step
+  // past the thread's range (live false) is still issued, at an offset past
+  // every resource's end, so it reads zeros without a memory access: loads
+  // issued on every path keep the compiler's wait counts exact, where a
+  // skipped load makes the wait before a store also cover the loads issued
+  // after it (the prefetch distance would drop to one step).
+  static __device__ __forceinline__ void load(const QmvParams& p, const Src& s, int st, bool live,
+                                              int tid, Regs& r) {
+    const int oob = live ? 0 : (1 << 30);
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       const int c = tid + kThreads * v;
       r.x[v] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                     s.xr, (c >> 3) * s.rs2 + (st * BK + (c & 7) * 8) * 2, 0, 0));
+                     s.xr, oob + (c >> 3) * s.rs2 + (st * BK + (c & 7) * 8) * 2, 0, 0));
     }
     if constexpr (FMT == kQ8) {
 #pragma unroll
       for (int i = 0; i < CV; ++i)
         r.c[i] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       s.wr, s.brl * s.rb + st * BK + 32 * s.sub + 16 * i, 0, 0));
+                       s.wr, oob + s.brl * s.rb + st * BK + 32 * s.sub + 16 * i, 0, 0));
       r.s[0] = 0;
     } else {
       r.c[0] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(s.wr, s.brl * s.rb + st * 32 + 16 * s.sub,
-                                                       0, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     s.wr, oob + s.brl * s.rb + st * 32 + 16 * s.sub, 0, 0));
       const int g = (st * BK + 32 * s.sub) / p.group;
-      const int si = s.brl * p.groups_per_row + g;
+      const int si = oob / 4 + s.brl * p.groups_per_row + g;
       if constexpr (G16) {
         // the two 16-code groups of the thread's 32 codes (si even: aligned)
         if constexpr (SF16) {
@@ -254,31 +260,28 @@ struct QGemm {
             acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bq[tn], acc[tm][tn], 0, 0, 0);
       } else if constexpr (G16) {
         // group 2 kk in lanes lk < 2, group 2 kk + 1 in lanes lk >= 2
+        // one B block's two operands at a time (register budget)
         const bool first = lk < 2;
-        float s0[TN], s1[TN];
-        f16x8 b0[TN], b1[TN];
         const f16x8 zero = {};
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn) {
-          s0[tn] = ss[(brow(wn, tn) + l16) * 4 + 2 * kk];
-          s1[tn] = ss[(brow(wn, tn) + l16) * 4 + 2 * kk + 1];
-          b0[tn] = first ? bq[tn] : zero;
-          b1[tn] = first ? zero : bq[tn];
-        }
         const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
+        for (int tn = 0; tn < TN; ++tn) {
+          const float s0 = ss[(brow(wn, tn) + l16) * 4 + 2 * kk];
+          const float s1 = ss[(brow(wn, tn) + l16) * 4 + 2 * kk + 1];
+          const f16x8 b0 = first ? bq[tn] : zero;
+          const f16x8 b1 = first ? zero : bq[tn];
 #pragma unroll
-          for (int tn = 0; tn < TN; ++tn) {
-            const f32x4 t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], b0[tn], z, 0, 0, 0);
-            const f32x4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], b1[tn], z, 0, 0, 0);
+          for (int tm = 0; tm < TM; ++tm) {
+            const f32x4 t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], b0, z, 0, 0, 0);
+            const f32x4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], b1, z, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              acc[tm][tn][r] = fmaf(s0[tn], t0[r], acc[tm][tn][r]);
-              acc[tm][tn][r] = fmaf(s1[tn], t1[r], acc[tm][tn][r]);
+              acc[tm][tn][r] = fmaf(s0, t0[r], acc[tm][tn][r]);
+              acc[tm][tn][r] = fmaf(s1, t1[r], acc[tm][tn][r]);
             }
           }
-        __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       } else {
         float sc[TN];
 #pragma unroll
@@ -417,27 +420,55 @@ void qgemm_kernel(const QmvParams p, int mtiles) {
 #pragma unroll
     for (int c = 0; c < G::TN; ++c) acc[a][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Two register sets rotate: while LDS buffer (st & 1) is consumed, step
-  // st + 1 waits in one set (stored after the MFMAs) and step st + 2 is being
-  // fetched into the other, so a load has two steps of MFMAs to land.
   typename G::Regs ra, rb;
-  G::load(p, src, s0, tid, ra);
-  if (s0 + 1 < s1) G::load(p, src, s0 + 1, tid, rb);
-  G::store(tid, ra, xs[0], ws[0], ss[0]);
-  __syncthreads();
-  for (int st = s0;;) {
-    if (st + 2 < s1) G::load(p, src, st + 2, tid, ra);
-    __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the MFMAs
-    G::compute(lane, wm, wn, xs[0], ws[0], ss[0], acc);
-    if (st + 1 < s1) G::store(tid, rb, xs[1], ws[1], ss[1]);
+  if constexpr (!G16) {
+    // Two register sets rotate: while LDS buffer (st & 1) is consumed, step
+    // st + 1 waits in one set (stored after the MFMAs) and step st + 2 is being
+    // fetched into the other, so a load has two steps of MFMAs to land.
+    G::load(p, src, s0, true, tid, ra);
+    if (s0 + 1 < s1) G::load(p, src, s0 + 1, true, tid, rb);
+    G::store(tid, ra, xs[0], ws[0], ss[0]);
     __syncthreads();
-    if (++st >= s1) break;
-    if (st + 2 < s1) G::load(p, src, st + 2, tid, rb);
-    __builtin_amdgcn_sched_barrier(0);
-    G::compute(lane, wm, wn, xs[1], ws[1], ss[1], acc);
-    if (st + 1 < s1) G::store(tid, ra, xs[0], ws[0], ss[0]);
+    for (int st = s0;;) {
+      if (st + 2 < s1) G::load(p, src, st + 2, true, tid, ra);
+      __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the MFMAs
+      G::compute(lane, wm, wn, xs[0], ws[0], ss[0], acc);
+      if (st + 1 < s1) G::store(tid, rb, xs[1], ws[1], ss[1]);
+      __syncthreads();
+      if (++st >= s1) break;
+      if (st + 2 < s1) G::load(p, src, st + 2, true, tid, rb);
+      __builtin_amdgcn_sched_barrier(0);
+      G::compute(lane, wm, wn, xs[1], ws[1], ss[1], acc);
+      if (st + 1 < s1) G::store(tid, ra, xs[0], ws[0], ss[0]);
+      __syncthreads();
+      if (++st >= s1) break;
+    }
+  } else {
+    // Group 16: the same rotation in a counted loop, two steps per
+    // iteration, with loads and stores on every path (past the range they
+    // move zeros into the buffer that is no longer read): the compiler then
+    // needs 128 registers here instead of 236 (four workgroups per CU
+    // instead of two), and no wait before a store covers the loads issued
+    // after it.  Buffer 0 holds step st and rb step st + 1 at the loop head.
+    G::load(p, src, s0, true, tid, ra);
+    G::load(p, src, s0 + 1, s0 + 1 < s1, tid, rb);
+    G::store(tid, ra, xs[0], ws[0], ss[0]);
     __syncthreads();
-    if (++st >= s1) break;
+    int st = s0;
+    for (int it = (s1 - s0) >> 1; it > 0; --it) {
+      G::load(p, src, st + 2, st + 2 < s1, tid, ra);
+      __builtin_amdgcn_sched_barrier(0);
+      G::compute(lane, wm, wn, xs[0], ws[0], ss[0], acc);
+      G::store(tid, rb, xs[1], ws[1], ss[1]);
+      __syncthreads();
+      G::load(p, src, st + 3, st + 3 < s1, tid, rb);
+      __builtin_amdgcn_sched_barrier(0);
+      G::compute(lane, wm, wn, xs[1], ws[1], ss[1], acc);
+      G::store(tid, ra, xs[0], ws[0], ss[0]);
+      __syncthreads();
+      st += 2;
+    }
+    if ((s1 - s0) & 1) G::compute(lane, wm, wn, xs[0], ws[0], ss[0], acc);
   }
   if (S == 1)
     G::finish(p, mt, b, n0, m0, lane, wm, wn, acc);

@@ -203,11 +203,17 @@ def test_gemm_stacked_copies_batched_x_match_single(ctx, aexq, orc, monkeypatch,
     (False, 1000, 2048, 300, False),  # ragged N, three 64-row tiles and a partial one
     (True, 1024, 3584, 64, False),    # fp16 scales, down_proj shape
     (False, 1024, 1024, 128, True),   # gate/up pair
+    (False, 640, 1088, 96, False),    # 17 K steps: the two-step loop's odd tail
+    (True, 384, 1216, 80, True),      # 19 K steps, gate/up pair
 ])
-def test_gemm_group16(ctx, aexq, orc, scale_f16, n, k, m, swiglu):
+@pytest.mark.parametrize("splitk", ["", "3"])
+def test_gemm_group16(ctx, aexq, orc, monkeypatch, scale_f16, n, k, m, swiglu, splitk):
     """Q4 with one scale per 16 codes on the tiled GEMM: two MFMAs per 32-code
-    extent, each group's product scaled in fp32 (exact float(q) * scale)."""
-    _announce(f"qgemm group16 f16={scale_f16} n={n} k={k} m={m} swiglu={swiglu}")
+    extent, each group's product scaled in fp32 (exact float(q) * scale).  With
+    three forced K chunks the chunks' step counts are odd and even alike."""
+    if splitk:
+        monkeypatch.setenv("AEXQ_SPLITK", splitk)
+    _announce(f"qgemm group16 f16={scale_f16} n={n} k={k} m={m} swiglu={swiglu} splitk={splitk}")
     from aiimage_amd import synth
     w, wf = _weight(ctx, aexq, orc, 4, n, k, 91 + m, group=16, scale_f16=scale_f16, code=0)
     x16 = synth.activations(m, k, 92)
