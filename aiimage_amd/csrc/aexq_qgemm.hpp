@@ -21,8 +21,10 @@
 // significant bits), so two MFMAs accumulate x * (q * s) exactly in the fp32
 // accumulator with no per-output scaling -- the B expansion is shared by the
 // tile's BM / 32 A blocks, where the per-group FMAs were per output.  Global
-// loads run two steps ahead of the MFMAs (two register sets); LDS is
-// double-buffered with one barrier per step.
+// loads are issued two steps ahead of the MFMAs (two register sets); LDS is
+// double-buffered with one barrier per step.  (In the conditional loop the
+// compiler's wait before each LDS store also covers the loads issued just
+// before it; the exact-wait form measured slower for these tiles.)
 //
 // G16 (Q4 with one scale per 16 codes, the reference's shipping format): an
 // MFMA K extent holds two groups, lanes l / 16 = 0, 1 the first and 2, 3 the
