@@ -461,7 +461,8 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the matvec would shard by output rows; see DESIGN.md)", file=sys.stderr)
+              "(the matvec would shard by output rows, one slice of the weight rows "
+              "per GPU)", file=sys.stderr)
         sys.exit(2)
     import torch
 
