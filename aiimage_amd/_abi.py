@@ -161,6 +161,9 @@ def _declare(L):
         "aexq_attention_decode": (i32, [P, P, P, P, i32, i32, i32, i32, i32, f32, P]),
         "aexq_attention_decode_rope": (i32, [P, P, P, P, P, P, i32, i32, i32, i32, i32, P, P,
                                              f32, P]),
+        "aexq_attention_decode_rope_at": (i32, [P, P, P, P, P, P, i32, i32, i32, i32, P, P, P,
+                                                f32, P]),
+        "aexq_decode_advance": (i32, [P, P, P, P, P, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

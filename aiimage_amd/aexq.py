@@ -319,6 +319,29 @@ class Context:
                                                    capacity, length, P(cos_t), P(sin_t), scale,
                                                    P(out)), "aexq_attention_decode_rope")
 
+    def attention_decode_rope_at(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                 k_cache: torch.Tensor, v_cache: torch.Tensor, heads_q: int,
+                                 heads_kv: int, head_dim: int, capacity: int,
+                                 position: torch.Tensor, cos_table: torch.Tensor,
+                                 sin_table: torch.Tensor, scale: float, out: torch.Tensor):
+        """attention_decode_rope at the device-side position (int32 tensor of one
+        element); cos/sin tables are [capacity][head_dim/2] fp32."""
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        check(self._lib.aexq_attention_decode_rope_at(self.handle, P(q), P(k), P(v), P(k_cache),
+                                                      P(v_cache), heads_q, heads_kv, head_dim,
+                                                      capacity, P(position), P(cos_table),
+                                                      P(sin_table), scale, P(out)),
+              "aexq_attention_decode_rope_at")
+
+    def decode_advance(self, position: torch.Tensor, token: torch.Tensor, argmax: torch.Tensor,
+                       tokens_out: Optional[torch.Tensor] = None):
+        """Device-side end of a generated token (DEC:1160-1237)."""
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        check(self._lib.aexq_decode_advance(
+            self.handle, P(position), P(token), P(argmax),
+            P(tokens_out) if tokens_out is not None else None,
+            tokens_out.numel() if tokens_out is not None else 0), "aexq_decode_advance")
+
     def dequant(self, w: "QuantWeight") -> torch.Tensor:
         info = w.info()
         out = torch.empty((info.n, info.k), dtype=torch.float32, device=f"cuda:{self.device}")

@@ -49,14 +49,15 @@ struct aexq_ctx {
   int device = 0;
   int cus = 256;  // compute units of the device
   hipStream_t stream = nullptr;
-  // argmax partial buffers, grown on demand
+  // Scratch buffers, grown on demand (capacities in bytes).
+  // argmax partials
   float* part_best = nullptr;
   int* part_index = nullptr;
   float* part_second = nullptr;
-  long long part_cap = 0;
+  long long part_best_cap = 0, part_index_cap = 0, part_second_cap = 0;
   float* logits_scratch = nullptr;
   long long logits_cap = 0;
-  // RMS-normalised activation rows of the MFMA path, grown on demand
+  // RMS-normalised activation rows of the MFMA path
   void* act_scratch = nullptr;
   long long act_cap = 0;
   void* gather_scratch = nullptr;  // dense rows of a head-packed x
@@ -65,14 +66,19 @@ struct aexq_ctx {
   float* attn_part = nullptr;
   long long attn_cap = 0;
   int* attn_count = nullptr;  // per kv head: splits finished in the running launch
-  int attn_count_cap = 0;
-  // split-K partial planes of the MFMA kernels (floats), grown on demand
+  long long attn_count_cap = 0;
+  // split-K partial planes of the MFMA kernels
   float* sk_part = nullptr;
   long long sk_cap = 0;
+  // scratch buffers replaced by larger ones: a HIP graph captured before the
+  // growth still holds their addresses, so they live until aexq_destroy
+  std::vector<void*> retired;
 };
 
 struct aexq_weight {
-  aexq_ctx* ctx = nullptr;
+  // the device holding the buffers; a weight may outlive the context that
+  // made it, so release never reaches back into the context
+  int device = 0;
   int bits = 8;
   int n = 0, k = 0;
   int block = 0;        // scale block in flat elements (k for per-row)
@@ -90,6 +96,33 @@ struct aexq_weight {
 };
 
 static long long round_up(long long v, long long a) { return (v + a - 1) / a * a; }
+
+// Makes the context scratch buffer *buf hold at least `bytes`.  A buffer that
+// is replaced is retired, not freed (a HIP graph captured earlier may still
+// hold its address), and growth while the context's stream is capturing is
+// refused: hipMalloc cannot be recorded into a graph, so every scratch size a
+// captured sequence needs is reached by running it once before the capture.
+// `zero` clears a new buffer (the attention split counters start at zero).
+static aexq_status grow_scratch(aexq_ctx* ctx, void** buf, long long* cap, long long bytes,
+                                const char* op, const char* what, bool zero = false) {
+  if (bytes <= *cap) return AEXQ_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return fail(AEXQ_ERR_UNSUPPORTED, op,
+                "%s scratch must grow from %lld to %lld bytes while the stream is capturing | "
+                "run the same calls once before the capture", what, *cap, bytes);
+  void* nb = nullptr;
+  hipError_t e = hipMalloc(&nb, (size_t)bytes);
+  if (e == hipSuccess && zero) e = hipMemset(nb, 0, (size_t)bytes);
+  if (e != hipSuccess) {
+    (void)hipFree(nb);
+    return hip_fail(e, op, what);
+  }
+  if (*buf) ctx->retired.push_back(*buf);
+  *buf = nb;
+  *cap = bytes;
+  return AEXQ_OK;
+}
 static int scale_bytes(int dtype) { return dtype == AEXQ_DTYPE_F16 ? 2 : 4; }
 
 extern "C" int aexq_abi_version(void) { return AEXQ_ABI_VERSION; }
@@ -124,6 +157,7 @@ extern "C" void aexq_destroy(aexq_ctx* ctx) {
   (void)hipFree(ctx->attn_part);
   (void)hipFree(ctx->attn_count);
   (void)hipFree(ctx->sk_part);
+  for (void* b : ctx->retired) (void)hipFree(b);
   delete ctx;
 }
 
@@ -148,7 +182,7 @@ extern "C" aexq_status aexq_synchronize(aexq_ctx* ctx) {
 static aexq_status alloc_weight(aexq_ctx* ctx, const char* op, int bits, int scale_dtype, int n,
                                 int k, int block, int nibble_code, aexq_weight** out) {
   aexq_weight* w = new aexq_weight();
-  w->ctx = ctx;
+  w->device = ctx->device;
   w->bits = bits;
   w->n = n;
   w->k = k;
@@ -492,9 +526,12 @@ extern "C" aexq_status aexq_weight_replicate(aexq_ctx* ctx, const aexq_weight* s
                                              aexq_weight** out) {
   const char* op = "aexq_weight_replicate";
   if (!ctx || !src || !out) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (src->device != ctx->device)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "weight on device %d, context on device %d",
+                src->device, ctx->device);
   if (batch <= 0) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "batch=%d", batch);
   aexq_weight* w = new aexq_weight(*src);
-  w->ctx = ctx;
+  w->device = ctx->device;
   w->batch = batch;
   w->owns = true;
   w->codes = nullptr;
@@ -523,8 +560,10 @@ extern "C" aexq_status aexq_weight_alias(aexq_ctx* ctx, const aexq_weight* share
                                          aexq_weight** out) {
   if (!ctx || !shared || !out)
     return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_weight_alias", "NULL argument");
+  if (shared->device != ctx->device)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_weight_alias",
+                "weight on device %d, context on device %d", shared->device, ctx->device);
   aexq_weight* w = new aexq_weight(*shared);
-  w->ctx = ctx;
   w->owns = false;
   *out = w;
   return AEXQ_OK;
@@ -533,7 +572,7 @@ extern "C" aexq_status aexq_weight_alias(aexq_ctx* ctx, const aexq_weight* share
 extern "C" void aexq_weight_release(aexq_weight* w) {
   if (!w) return;
   if (w->owns) {
-    (void)hipSetDevice(w->ctx->device);
+    (void)hipSetDevice(w->device);
     (void)hipFree(w->codes);
     (void)hipFree(w->scales);
   }
@@ -808,6 +847,13 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   if (a.flags & ~known) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "flags=0x%x", a.flags);
   const aexq_weight* w0 = ws[0];
   if (!w0) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "weight is NULL");
+  for (int i = 0; i < count; ++i)
+    if (ws[i] && ws[i]->device != ctx->device)
+      return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "weight %d is on device %d, context on device %d",
+                  i, ws[i]->device, ctx->device);
+  if (args && args->up && args->up->device != ctx->device)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "up weight is on device %d, context on device %d",
+                args->up->device, ctx->device);
   for (int i = 1; i < count; ++i) {
     if (!ws[i]) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "weight %d is NULL", i);
     if (ws[i]->bits != w0->bits || ws[i]->k != w0->k || ws[i]->batch != w0->batch ||
@@ -1077,9 +1123,10 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   p.total_tiles = tiles_total;
   p.y_rows = M;
   // M = 1 RMSNorm-in over one activation row (not batched; a group shares x):
-  // each workgroup stages the normalised row once in LDS (K <= 8192 always
-  // holds there)
-  if (plan->kind == kPlanStream && M == 1 && xv.batch == 1 && K <= 8192 && (p.flags & kFlagRms))
+  // each workgroup stages the normalised row once in LDS (rows up to
+  // kQmvStageMaxK; longer ones are normalised by every wave in registers)
+  if (plan->kind == kPlanStream && M == 1 && xv.batch == 1 && K <= kQmvStageMaxK &&
+      (p.flags & kFlagRms))
     p.flags |= kFlagXShared;
   plan->x_f32 = xv.dtype == AEXQ_DTYPE_F32;
   plan->x_batch = xv.batch;
@@ -1176,13 +1223,9 @@ static aexq_status launch_mfma(aexq_ctx* ctx, Plan& plan, const char* op) {
   const int M = p.m, K = p.k;
   if (plan.rms_prepass) {
     const long long need = (long long)plan.x_batch * M * K * 2;
-    if (need > ctx->act_cap) {
-      (void)hipFree(ctx->act_scratch);
-      ctx->act_scratch = nullptr;
-      ctx->act_cap = 0;
-      HIP_TRY(op, hipMalloc(&ctx->act_scratch, need));
-      ctx->act_cap = need;
-    }
+    aexq_status st = grow_scratch(ctx, &ctx->act_scratch, &ctx->act_cap, need, op,
+                                  "RMSNorm-in rows");
+    if (st) return st;
     hipError_t e = rmsnorm_rows_launch(p.mat[0].x, plan.x_f32, plan.x_rstride_in,
                                        plan.x_bstride_in, plan.x_batch, M, K, plan.p.gamma,
                                        plan.p.gamma_size, plan.p.eps, ctx->act_scratch,
@@ -1199,13 +1242,9 @@ static aexq_status launch_mfma(aexq_ctx* ctx, Plan& plan, const char* op) {
     QmvParams q = p;
     q.m = plan.kind == kPlanGemm || M < plan.mblock ? M : plan.mblock;
     const long long need = (long long)plan.sk_chunks * splitk_layout(q, plan.sk_nw);
-    if (need > ctx->sk_cap) {
-      (void)hipFree(ctx->sk_part);
-      ctx->sk_part = nullptr;
-      ctx->sk_cap = 0;
-      HIP_TRY(op, hipMalloc((void**)&ctx->sk_part, need * sizeof(float)));
-      ctx->sk_cap = need;
-    }
+    aexq_status st = grow_scratch(ctx, (void**)&ctx->sk_part, &ctx->sk_cap,
+                                  need * (long long)sizeof(float), op, "split-K partial planes");
+    if (st) return st;
     p.sk_part = ctx->sk_part;
     p.sk_chunks = plan.sk_chunks;
     p.sk_cs = plan.sk_cs;
@@ -1249,13 +1288,9 @@ static aexq_status gather_x(aexq_ctx* ctx, Plan& plan, const char* op) {
   const int width = plan.xg_heads * plan.xg_hd;
   const long long need =
       (long long)plan.xg_batch * plan.xg_rows * width * (plan.xg_f32 ? 4 : 2);
-  if (need > ctx->gather_cap) {
-    (void)hipFree(ctx->gather_scratch);
-    ctx->gather_scratch = nullptr;
-    ctx->gather_cap = 0;
-    HIP_TRY(op, hipMalloc(&ctx->gather_scratch, need));
-    ctx->gather_cap = need;
-  }
+  aexq_status st = grow_scratch(ctx, &ctx->gather_scratch, &ctx->gather_cap, need, op,
+                                "head-packed x rows");
+  if (st) return st;
   hipError_t e = head_gather_launch(plan.xg_src, plan.xg_f32, plan.xg_rows, plan.xg_heads,
                                     plan.xg_hd, plan.xg_batch, plan.xg_bstride,
                                     ctx->gather_scratch, ctx->stream);
@@ -1332,19 +1367,15 @@ extern "C" aexq_status aexq_linear_group(aexq_ctx* ctx, int count, const aexq_we
 }
 
 static aexq_status ensure_parts(aexq_ctx* ctx, long long need, const char* op) {
-  if (need <= ctx->part_cap) return AEXQ_OK;
-  (void)hipFree(ctx->part_best);
-  (void)hipFree(ctx->part_index);
-  (void)hipFree(ctx->part_second);
-  ctx->part_best = nullptr;
-  ctx->part_index = nullptr;
-  ctx->part_second = nullptr;
-  ctx->part_cap = 0;
-  HIP_TRY(op, hipMalloc((void**)&ctx->part_best, need * sizeof(float)));
-  HIP_TRY(op, hipMalloc((void**)&ctx->part_index, need * sizeof(int)));
-  HIP_TRY(op, hipMalloc((void**)&ctx->part_second, need * sizeof(float)));
-  ctx->part_cap = need;
-  return AEXQ_OK;
+  aexq_status st = grow_scratch(ctx, (void**)&ctx->part_best, &ctx->part_best_cap,
+                                need * (long long)sizeof(float), op, "argmax partials");
+  if (!st)
+    st = grow_scratch(ctx, (void**)&ctx->part_index, &ctx->part_index_cap,
+                      need * (long long)sizeof(int), op, "argmax partials");
+  if (!st)
+    st = grow_scratch(ctx, (void**)&ctx->part_second, &ctx->part_second_cap,
+                      need * (long long)sizeof(float), op, "argmax partials");
+  return st;
 }
 
 static aexq_status argmax_over_logits(aexq_ctx* ctx, const float* logits, int m, int n,
@@ -1416,13 +1447,9 @@ extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
     lg = (float*)logits->data;
   } else {
     const long long need = (long long)M * w->n;
-    if (need > ctx->logits_cap) {
-      (void)hipFree(ctx->logits_scratch);
-      ctx->logits_scratch = nullptr;
-      ctx->logits_cap = 0;
-      HIP_TRY(op, hipMalloc((void**)&ctx->logits_scratch, need * sizeof(float)));
-      ctx->logits_cap = need;
-    }
+    st = grow_scratch(ctx, (void**)&ctx->logits_scratch, &ctx->logits_cap,
+                      need * (long long)sizeof(float), op, "logits");
+    if (st) return st;
     lg = ctx->logits_scratch;
     plan.p.mat[0].y = lg;
     plan.p.mat[0].y_rstride = w->n;
@@ -1451,6 +1478,9 @@ extern "C" aexq_status aexq_argmax(aexq_ctx* ctx, const aexq_tensor* logits, int
 extern "C" aexq_status aexq_dequant(aexq_ctx* ctx, const aexq_weight* w, float* out) {
   const char* op = "aexq_dequant";
   if (!ctx || !w || !out) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (w->device != ctx->device)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "weight on device %d, context on device %d",
+                w->device, ctx->device);
   HIP_TRY(op, hipSetDevice(ctx->device));
   const int fmt = w->bits == 8 ? kQ8 : kQ4;
   hipError_t e = dequant_launch(fmt, w->codes, w->scales, w->scale_dtype == AEXQ_DTYPE_F16, w->n,
@@ -1493,6 +1523,9 @@ extern "C" aexq_status aexq_embed_q8(aexq_ctx* ctx, const aexq_weight* table,
                                      const int32_t* tokens, int m, void* out) {
   const char* op = "aexq_embed_q8";
   if (!ctx || !table || !tokens || !out) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (table->device != ctx->device)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "table on device %d, context on device %d",
+                table->device, ctx->device);
   if (table->bits != 8 || table->block != table->k)
     return fail(AEXQ_ERR_UNSUPPORTED, op, "embedding table must be Q8 with one scale per row");
   if (m <= 0) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "m=%d", m);
@@ -1542,24 +1575,13 @@ static aexq_status attn_prepare(aexq_ctx* ctx, const char* op, int heads_q, int 
                 splits, attn_max_splits());
   const long long need = (long long)heads_q * splits * attn_part_stride();
   HIP_TRY(op, hipSetDevice(ctx->device));
-  if (need > ctx->attn_cap) {
-    (void)hipFree(ctx->attn_part);
-    ctx->attn_part = nullptr;
-    ctx->attn_cap = 0;
-    HIP_TRY(op, hipMalloc((void**)&ctx->attn_part, need * sizeof(float)));
-    ctx->attn_cap = need;
-  }
-  if (heads_kv > ctx->attn_count_cap) {
-    // split counters start at zero; every launch leaves them at zero
-    (void)hipFree(ctx->attn_count);
-    ctx->attn_count = nullptr;
-    ctx->attn_count_cap = 0;
-    const size_t bytes = (size_t)heads_kv * attn_counter_stride() * sizeof(int);
-    HIP_TRY(op, hipMalloc((void**)&ctx->attn_count, bytes));
-    HIP_TRY(op, hipMemset(ctx->attn_count, 0, bytes));
-    ctx->attn_count_cap = heads_kv;
-  }
-  return AEXQ_OK;
+  aexq_status st = grow_scratch(ctx, (void**)&ctx->attn_part, &ctx->attn_cap,
+                                need * (long long)sizeof(float), op, "attention split partials");
+  if (st) return st;
+  // split counters start at zero; every launch leaves them at zero
+  return grow_scratch(ctx, (void**)&ctx->attn_count, &ctx->attn_count_cap,
+                      (long long)heads_kv * attn_counter_stride() * (long long)sizeof(int), op,
+                      "attention split counters", true);
 }
 
 extern "C" aexq_status aexq_attention_decode(aexq_ctx* ctx, const void* q, const void* k_cache,
@@ -1573,7 +1595,7 @@ extern "C" aexq_status aexq_attention_decode(aexq_ctx* ctx, const void* q, const
   if (st) return st;
   hipError_t e = attn_decode_launch(q, k_cache, v_cache, heads_q, heads_kv, capacity, length,
                                     scale, ctx->attn_part, ctx->attn_count, out, nullptr, nullptr,
-                                    nullptr, nullptr, ctx->stream);
+                                    nullptr, nullptr, nullptr, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, op, "attention launch");
   return AEXQ_OK;
 }
@@ -1590,7 +1612,44 @@ extern "C" aexq_status aexq_attention_decode_rope(aexq_ctx* ctx, const void* q, 
   if (st) return st;
   hipError_t e = attn_decode_launch(q, k_cache, v_cache, heads_q, heads_kv, capacity, length,
                                     scale, ctx->attn_part, ctx->attn_count, out, k, v, cos_table,
-                                    sin_table, ctx->stream);
+                                    sin_table, nullptr, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, op, "attention launch");
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_attention_decode_rope_at(aexq_ctx* ctx, const void* q, const void* k,
+                                                     const void* v, void* k_cache, void* v_cache,
+                                                     int heads_q, int heads_kv, int head_dim,
+                                                     int capacity, const int32_t* position,
+                                                     const float* cos_table,
+                                                     const float* sin_table, float scale,
+                                                     void* out) {
+  const char* op = "aexq_attention_decode_rope_at";
+  if (!ctx || !q || !k || !v || !k_cache || !v_cache || !position || !cos_table || !sin_table ||
+      !out)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  // sized for the whole cache: the launch covers every position the device
+  // counter may name
+  aexq_status st = attn_prepare(ctx, op, heads_q, heads_kv, head_dim, capacity, capacity);
+  if (st) return st;
+  hipError_t e = attn_decode_launch(q, k_cache, v_cache, heads_q, heads_kv, capacity, capacity,
+                                    scale, ctx->attn_part, ctx->attn_count, out, k, v, cos_table,
+                                    sin_table, position, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "attention launch");
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_decode_advance(aexq_ctx* ctx, int32_t* position, int32_t* token,
+                                           const int32_t* argmax, int32_t* tokens_out,
+                                           int tokens_cap) {
+  const char* op = "aexq_decode_advance";
+  if (!ctx || !position || !token || !argmax)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (tokens_out && tokens_cap <= 0)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "tokens_cap=%d", tokens_cap);
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  hipError_t e = decode_advance_launch(position, token, argmax, tokens_out,
+                                       tokens_out ? tokens_cap : 0, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "advance launch");
   return AEXQ_OK;
 }

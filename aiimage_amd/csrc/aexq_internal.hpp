@@ -112,6 +112,9 @@ const QmvEntry* qmv_table_q4(int* count);
 const QmvEntry* qmv_find(const QmvConfig& cfg);
 // resident workgroups of an entry per CU (occupancy query, cached)
 int qmv_blocks_per_cu(const QmvEntry* e);
+// Longest activation row a streaming launch stages in LDS (kFlagXShared):
+// two passes of 8 elements per thread of a 256-thread workgroup.
+constexpr int kQmvStageMaxK = 2 * kThreads * 8;
 // Dynamic LDS of a streaming launch with kFlagXShared: the fp16 activation row
 // and one fp32 partial per wave.
 inline size_t qmv_stage_bytes(int k) { return (((size_t)k * 2 + 15) & ~(size_t)15) + kWaves * 4; }
@@ -196,9 +199,17 @@ int attn_counter_stride();  // ints between the kv heads' split counters
 // part: hq * splits * (128 + 2) floats; counters: hkv ints, zero before the
 // first launch (every launch leaves them zero).  knew/vnew/cosv/sinv non-null:
 // RoPE of q and of the new k row plus the K/V append at position len - 1.
+// posp non-null: the position is *posp (clamped to the capacity), read on the
+// device, the grid is sized for `cap` positions and cosv/sinv are [cap][64]
+// tables whose row *posp is used; `len` is ignored.
 hipError_t attn_decode_launch(const void* q, const void* kcache, const void* vcache, int hq,
                               int hkv, int cap, int len, float scale, float* part, int* counters,
                               void* out, const void* knew, const void* vnew, const float* cosv,
-                              const float* sinv, hipStream_t stream);
+                              const float* sinv, const int* posp, hipStream_t stream);
+// One decode step's bookkeeping on the device: tokens_out[*position] (when
+// non-null and the position is below out_cap) and *token take *argmax, then
+// *position advances by one.
+hipError_t decode_advance_launch(int* position, int* token, const int* argmax, int* tokens_out,
+                                 int out_cap, hipStream_t stream);
 
 }  // namespace aexq

@@ -12,8 +12,9 @@
 // activations, which stay in registers while the activation row is unchanged,
 // in v_dot2_f32_f16 with fp32 accumulation.  Scales are applied in fp32: once
 // per row for Q8, once per 16- or 32-code group for Q4.  Rows are reduced
-// across their LPR lanes with DPP.  Epilogues (alpha/beta/C, RMSNorm-in,
-// SwiGLU-out, residual, argmax partials) run before the single store.
+// across their LPR lanes with DPP.  RMSNorm-in normalises the activation
+// registers before the first tile; the epilogues (alpha/beta/C, SwiGLU-out,
+// residual, argmax partials) run before the single store.
 #pragma once
 
 #include <math.h>
@@ -185,79 +186,95 @@ struct Qmv {
   }
 
   // Activation rows of one batch entry into registers.  With the RMSNorm-in
-  // epilogue the registers hold fp16(x * gamma) and xinv[m] = rsqrt(mean x^2 +
-  // eps), which the epilogue applies to the row's dot product (exact algebra:
-  // the norm is a scalar per activation row).  sum(x^2) comes from the same
-  // registers -- the LPR lanes of a slot hold the whole row -- so x, gamma and
-  // the weight codes are all in flight at once and no wave waits on another
-  // (x * gamma must be fp16-representable, as the normalised row is).
+  // epilogue the registers hold fp16(x * inv * gamma), inv = rsqrt(max(mean x^2
+  // + eps, 1e-20)), rounded once as the reference's separate RMSNorm dispatch
+  // rounds into its fp16 texture (CC:4548-4561): the raw row lands in the
+  // registers first, sum(x^2) is reduced from them -- the LPR lanes of a slot
+  // hold the whole row -- and only then is each element normalised, so the
+  // fp16 value stays bounded by sqrt(K) * |gamma| whatever the row's scale.
   static __device__ __forceinline__ void load_x(const QmvParams& p, const f16* xb, int sub,
-                                                XRegs& xr, float (&xinv)[MMAX]) {
+                                                XRegs& xr) {
     const bool rms = (p.flags & kFlagRms) != 0;
     const __amdgpu_buffer_rsrc_t grsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void*)p.gamma, (short)0, p.gamma ? p.k * 4 : 0, kBufferRsrcWord3);
 #pragma unroll
     for (int m = 0; m < MMAX; ++m) {
-      xinv[m] = 1.0f;
       if (m < p.m) {
         const f16* row = xb + (long long)m * p.x_rstride;
         float ss = 0.0f;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
           const int ci = sub + c * LPR;
-          uint32_t raw[XW];
           if (ci < p.chunks) {
             const u32x4* src = (const u32x4*)(row + (long long)ci * (XW * 2));
 #pragma unroll
             for (int v = 0; v < XW / 4; ++v) {
               const u32x4 t = src[v];
-              raw[4 * v + 0] = t[0];
-              raw[4 * v + 1] = t[1];
-              raw[4 * v + 2] = t[2];
-              raw[4 * v + 3] = t[3];
-            }
-            if (rms) {
-              // gamma through a buffer resource: one offset register per chunk,
-              // the rest are immediate offsets (the streaming kernels require
-              // gamma to cover K; shorter affine vectors take the generic path)
-              const int goff = ci * XW * 2 * 4;
-#pragma unroll
-              for (int d = 0; d < XW; d += 2) {
-                float g[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-                if (p.gamma) {
-                  const f32x4 t = __builtin_bit_cast(
-                      f32x4, __builtin_amdgcn_raw_buffer_load_b128(grsrc, goff + d * 8, 0, 0));
-                  g[0] = t[0];
-                  g[1] = t[1];
-                  g[2] = t[2];
-                  g[3] = t[3];
-                }
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                  const f16x2 h = as_h2(raw[d + e]);
-                  const float a = (float)h[0], b = (float)h[1];
-                  ss = fmaf(a, a, ss);
-                  ss = fmaf(b, b, ss);
-                  const f16x2 o = {(f16)(a * g[2 * e]), (f16)(b * g[2 * e + 1])};
-                  raw[d + e] = as_u(o);
-                }
-              }
+              xr[m][c][4 * v + 0] = t[0];
+              xr[m][c][4 * v + 1] = t[1];
+              xr[m][c][4 * v + 2] = t[2];
+              xr[m][c][4 * v + 3] = t[3];
             }
           } else {
 #pragma unroll
-            for (int d = 0; d < XW; ++d) raw[d] = 0u;
+            for (int d = 0; d < XW; ++d) xr[m][c][d] = 0u;
           }
-          if constexpr (FMT == kQ8) {
+          if (rms) {
 #pragma unroll
-            for (int d = 0; d < XW; ++d) xr[m][c][d] = raw[d];
-          } else {
-#pragma unroll
-            for (int d = 0; d < 4; ++d)
-              q4_xpairs(raw[4 * d], raw[4 * d + 1], raw[4 * d + 2], raw[4 * d + 3],
-                        &xr[m][c][4 * d]);
+            for (int d = 0; d < XW; ++d) {
+              const f16x2 h = as_h2(xr[m][c][d]);
+              const float a = (float)h[0], b = (float)h[1];
+              ss = fmaf(a, a, ss);
+              ss = fmaf(b, b, ss);
+            }
           }
         }
-        if (rms) xinv[m] = rsqrtf(fmaxf(group_sum<LPR>(ss) / (float)p.k + p.eps, 1e-20f));
+        if (rms) {
+          const float inv = rsqrtf(fmaxf(group_sum<LPR>(ss) / (float)p.k + p.eps, 1e-20f));
+          const bool use_gamma = p.gamma != nullptr;
+          // the registers are re-read below: without this the compiler keeps
+          // the sum's fp32 conversions of every element live across the
+          // reduction instead of converting again (64 more registers)
+#pragma unroll
+          for (int c = 0; c < CPL; ++c)
+#pragma unroll
+            for (int d = 0; d < XW; ++d) __asm__("" : "+v"(xr[m][c][d]));
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) {
+            // gamma through a buffer resource: one offset register per chunk,
+            // the rest are immediate offsets (the streaming kernels require
+            // gamma to cover K; shorter affine vectors take the generic path).
+            // A chunk past K reads gamma 0 against x 0, without a branch.
+            const int goff = (sub + c * LPR) * XW * 2 * 4;
+#pragma unroll
+            for (int d = 0; d < XW; d += 2) {
+              const f32x4 t = __builtin_bit_cast(
+                  f32x4, __builtin_amdgcn_raw_buffer_load_b128(grsrc, goff + d * 8, 0, 0));
+#pragma unroll
+              for (int e = 0; e < 2; ++e) {
+                const f16x2 h = as_h2(xr[m][c][d + e]);
+                const float a = (float)h[0] * inv, b = (float)h[1] * inv;
+                const float g0 = use_gamma ? t[2 * e] : 1.0f;
+                const float g1 = use_gamma ? t[2 * e + 1] : 1.0f;
+                const f16x2 o = {(f16)(a * g0), (f16)(b * g1)};
+                xr[m][c][d + e] = as_u(o);
+              }
+              // one gamma vector in flight at a time: hoisting them all would
+              // need 4 * XW * CPL more registers next to the tile buffers
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        }
+        if constexpr (FMT == kQ4) {
+#pragma unroll
+          for (int c = 0; c < CPL; ++c)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const uint32_t a = xr[m][c][4 * d], b = xr[m][c][4 * d + 1],
+                             e = xr[m][c][4 * d + 2], f = xr[m][c][4 * d + 3];
+              q4_xpairs(a, b, e, f, &xr[m][c][4 * d]);
+            }
+        }
       } else {
 #pragma unroll
         for (int c = 0; c < CPL; ++c)
@@ -268,15 +285,16 @@ struct Qmv {
   }
 
   // M = 1 RMSNorm-in with one activation row for the whole launch
-  // (kFlagXShared): the workgroup's 256 threads stage fp16(x * gamma) into
-  // LDS, 8 elements each per pass, and reduce sum(x^2) through LDS -- one
-  // memory round trip and one barrier for every wave of the workgroup,
-  // instead of each wave walking its chunks' activations and gamma.
-  // stage_issue() issues every pass's x and gamma loads (before the tile's
-  // weight loads, so that waiting for them does not wait for the weights);
-  // stage_finish() forms the row, and returns its factor.  Every thread of
-  // the workgroup calls both.
-  static constexpr int kStagePasses = 4;  // K <= 4 * 256 * 8
+  // (kFlagXShared): the workgroup's 256 threads stage fp16(x * inv * gamma)
+  // into LDS, 8 elements each per pass -- one memory round trip and two
+  // barriers for every wave of the workgroup, instead of each wave walking its
+  // chunks' activations and gamma.  stage_issue() issues every pass's x and
+  // gamma loads (before the tile's weight loads, so that waiting for them does
+  // not wait for the weights); stage_finish() stores the raw row and reduces
+  // sum(x^2) through LDS, then each thread normalises the elements it stored.
+  // Every thread of the workgroup calls both.
+  static constexpr int kStagePasses = 2;
+  static_assert(kStagePasses * kThreads * 8 == kQmvStageMaxK, "staged row length");
   struct Stage {
     u32x4 x[kStagePasses];
     f32x4 g[kStagePasses][2];
@@ -293,6 +311,10 @@ struct Qmv {
       const int e0 = (it * kThreads + (int)threadIdx.x) * 8;  // past K: reads 0
       st.x[it] =
           __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, e0 * 2, 0, 0));
+    }
+#pragma unroll
+    for (int it = 0; it < kStagePasses; ++it) {
+      const int e0 = (it * kThreads + (int)threadIdx.x) * 8;
       st.g[it][0] =
           __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(grs, e0 * 4, 0, 0));
       st.g[it][1] =
@@ -300,8 +322,8 @@ struct Qmv {
     }
   }
 
-  static __device__ __forceinline__ float stage_finish(const QmvParams& p, const Stage& st,
-                                                       int lane, int wave) {
+  static __device__ __forceinline__ void stage_finish(const QmvParams& p, const Stage& st,
+                                                      int lane, int wave) {
     extern __shared__ __align__(16) uint8_t qmv_stage[];
     f16* xs = (f16*)qmv_stage;
     float* red = (float*)(qmv_stage + (((size_t)p.k * 2 + 15) & ~(size_t)15));
@@ -310,19 +332,14 @@ struct Qmv {
 #pragma unroll
     for (int it = 0; it < kStagePasses; ++it) {
       const int e0 = (it * kThreads + (int)threadIdx.x) * 8;
-      u32x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const f16x2 h = as_h2(st.x[it][e]);
         const float a = (float)h[0], b = (float)h[1];
         ss = fmaf(a, a, ss);
         ss = fmaf(b, b, ss);
-        const float g0 = use_gamma ? st.g[it][e / 2][2 * (e % 2)] : 1.0f;
-        const float g1 = use_gamma ? st.g[it][e / 2][2 * (e % 2) + 1] : 1.0f;
-        const f16x2 r = {(f16)(a * g0), (f16)(b * g1)};
-        o[e] = as_u(r);
       }
-      if (e0 < p.k) *(u32x4*)(xs + e0) = o;
+      if (e0 < p.k) *(u32x4*)(xs + e0) = st.x[it];
     }
     ss = wave_sum(ss);
     if (lane == 0) red[wave] = ss;
@@ -330,7 +347,27 @@ struct Qmv {
     float tot = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) tot += red[w];
-    return rsqrtf(fmaxf(tot / (float)p.k + p.eps, 1e-20f));
+    const float inv = rsqrtf(fmaxf(tot / (float)p.k + p.eps, 1e-20f));
+#pragma unroll
+    for (int it = 0; it < kStagePasses; ++it) {
+      const int e0 = (it * kThreads + (int)threadIdx.x) * 8;
+      if (e0 < p.k) {
+        // the thread's own elements: no barrier between its store and this load
+        const u32x4 x = *(const u32x4*)(xs + e0);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f16x2 h = as_h2(x[e]);
+          const float a = (float)h[0] * inv, b = (float)h[1] * inv;
+          const float g0 = use_gamma ? st.g[it][e / 2][2 * (e % 2)] : 1.0f;
+          const float g1 = use_gamma ? st.g[it][e / 2][2 * (e % 2) + 1] : 1.0f;
+          const f16x2 r = {(f16)(a * g0), (f16)(b * g1)};
+          o[e] = as_u(r);
+        }
+        *(u32x4*)(xs + e0) = o;
+      }
+    }
+    __syncthreads();
   }
 
   // A wave's activation registers from the staged row.
@@ -369,8 +406,7 @@ struct Qmv {
   // Dot products, row reduction, epilogue and store of one tile.
   static __device__ __forceinline__ void compute(const QmvParams& p, const Cursor& cu,
                                                  const Offsets& o, const Buf& buf,
-                                                 const XRegs& xr, const float (&xinv)[MMAX],
-                                                 int sub, int slot, float (&bv)[MMAX],
+                                                 const XRegs& xr, int sub, int slot, float (&bv)[MMAX],
                                                  int (&bi)[MMAX],
                                                  float (&bs)[MMAX]) {
     const QmvMat& mt = p.mat[cu.j];
@@ -451,7 +487,7 @@ struct Qmv {
           float v = group_sum<LPR>(acc[h][u][m]);
           if constexpr (FMT == kQ8)
             v *= scale_at(buf.s[h][u][0], toff + u_scale_bytes(p, u) + o.s[0], scl16);
-          acc[h][u][m] = v * xinv[m];
+          acc[h][u][m] = v;
         }
 
     const bool yf32 = (p.flags & kFlagYf32) != 0;
@@ -529,7 +565,6 @@ void qmv_kernel(const QmvParams p) {
   typename Q::Cursor cu = Q::locate(p, has_tiles ? t0 : 0);
   typename Q::Buf A, B;
   typename Q::XRegs xr;
-  float xinv[MMAX];
   const f16* xcur = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
   bool staged = false;
   if constexpr (MMAX == 1) {
@@ -538,14 +573,14 @@ void qmv_kernel(const QmvParams p) {
       Q::stage_issue(p, st);
       __builtin_amdgcn_sched_barrier(0);  // the staging loads go out before the codes
       Q::load(p, cu, o, A, has_tiles, slot);
-      xinv[0] = Q::stage_finish(p, st, lane, wave);
+      Q::stage_finish(p, st, lane, wave);
       Q::load_x_staged(p, sub, xr);
       staged = true;
     }
   }
   if (!staged) {
     Q::load(p, cu, o, A, has_tiles, slot);
-    if (has_tiles) Q::load_x(p, xcur, sub, xr, xinv);
+    if (has_tiles) Q::load_x(p, xcur, sub, xr);
   }
 
   if (has_tiles) {
@@ -558,14 +593,14 @@ void qmv_kernel(const QmvParams p) {
       bool more = t + 1 < t1;
       typename Q::Cursor nx = more ? Q::advance(p, cu) : cu;
       Q::load(p, nx, o, B, more, slot);
-      Q::compute(p, cu, o, A, xr, xinv, sub, slot, bv, bi, bs);
+      Q::compute(p, cu, o, A, xr, sub, slot, bv, bi, bs);
       if (!more) break;
       ++t;
       cu = nx;
       {
         const f16* xp = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
         if (__builtin_expect(xp != xcur, 0)) {
-          Q::load_x(p, xp, sub, xr, xinv);
+          Q::load_x(p, xp, sub, xr);
           xcur = xp;
         }
       }
@@ -573,14 +608,14 @@ void qmv_kernel(const QmvParams p) {
       more = t + 1 < t1;
       nx = more ? Q::advance(p, cu) : cu;
       Q::load(p, nx, o, A, more, slot);
-      Q::compute(p, cu, o, B, xr, xinv, sub, slot, bv, bi, bs);
+      Q::compute(p, cu, o, B, xr, sub, slot, bv, bi, bs);
       if (!more) break;
       ++t;
       cu = nx;
       {
         const f16* xp = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
         if (__builtin_expect(xp != xcur, 0)) {
-          Q::load_x(p, xp, sub, xr, xinv);
+          Q::load_x(p, xp, sub, xr);
           xcur = xp;
         }
       }

@@ -18,6 +18,12 @@ heads of 128, 4 key/value heads (k/v_proj 1024 -> 512), SwiGLU 3584, 24
 layers, Q4 offset-8 linears with fp16 scales per 32, RMSNorm eps 1e-6 with
 weights 1 + N(0, 0.02), RoPE base 1e6, a Q8 per-row LM head 1024 -> 151936
 with fp16 scales (also the embedding), and an fp16 KV cache filled with N(0, 1).
+
+The decode position lives in device memory: the attention launches read it
+and take their RoPE row from [capacity][head_dim/2] tables built once, and a
+step that advances ends by writing the argmax into the input token and moving
+the position on (Generate, DEC:1160-1237), so one captured step replays token
+after token.
 """
 from __future__ import annotations
 
@@ -89,6 +95,24 @@ def host_weights(cfg: ModelConfig, layer: int):
     return out, g_attn, g_mlp
 
 
+def rope_tables(capacity: int, head_dim: int, base: float):
+    """(cos, sin) float32 [capacity][head_dim/2]: row p is CreateRopeTextures'
+    row for position p (DEC:1660-1675), evaluated in the reference's float32
+    steps: e = j * (2f / (half * 2f)), p = (float)pow(theta, e), inverse = 1f /
+    p, angle = position * inverse, then (float)cos / sin of the float angle
+    (UnityEngine's Mathf.Pow/Cos/Sin round System.Math's double results)."""
+    half = head_dim // 2
+    theta = np.float32(base)
+    step = np.float32(2.0) / (np.float32(half) * np.float32(2.0))
+    e = (np.arange(half, dtype=np.float32) * step).astype(np.float32)
+    pw = np.power(np.float64(theta), e.astype(np.float64)).astype(np.float32)
+    inverse = (np.float32(1.0) / pw).astype(np.float32)
+    pos = np.arange(capacity, dtype=np.float32)[:, None]
+    angle = (pos * inverse[None, :]).astype(np.float32)
+    a64 = angle.astype(np.float64)
+    return np.cos(a64).astype(np.float32), np.sin(a64).astype(np.float32)
+
+
 def host_lm_head(cfg: ModelConfig):
     return synth.q8_weights(cfg.vocab, cfg.hidden, cfg.seed + 7)
 
@@ -130,17 +154,24 @@ class DecodeSession:
         words, scales, _ = host_lm_head(c)
         self.lm = ctx.weight(aexq.QuantizedTensor(c.vocab * c.hidden, c.hidden, words, scales, bits=8),
                              c.vocab, c.hidden)
+        # the embedding reads the LM head's device copy through a non-owning
+        # alias (Qwen35SharedTokenEmbeddingWeights, EMB:95-120; GL:91-111)
+        self.embed = self.lm.alias()
         self.g_final = torch.as_tensor(host_final_gamma(c)).to(device)
         f16 = torch.float16
         z = lambda n, dt=f16: torch.zeros(n, dtype=dt, device=device)
         self.token = torch.zeros(1, dtype=torch.int32, device=device)
         self.next_token = torch.zeros(1, dtype=torch.int32, device=device)
+        # the decode position (device), and the token generated at each position
+        self.pos = torch.zeros(1, dtype=torch.int32, device=device)
+        self.history = torch.full((c.capacity,), -1, dtype=torch.int32, device=device)
         self.xa, self.xb, self.xn = z(c.hidden), z(c.hidden), z(c.hidden)
         self.q, self.k, self.v = z(c.q_width), z(c.kv_width), z(c.kv_width)
         self.attn = z(c.q_width)
         self.h = z(c.intermediate)
-        self.cos = z(c.head_dim // 2, torch.float32)
-        self.sin = z(c.head_dim // 2, torch.float32)
+        ct, st = rope_tables(c.capacity, c.head_dim, c.rope_base)
+        self.cos = torch.as_tensor(ct).to(device).reshape(-1)
+        self.sin = torch.as_tensor(st).to(device).reshape(-1)
         d = aexq.describe
         self.d = {
             "xa": d(self.xa, 1, c.hidden, P4), "xb": d(self.xb, 1, c.hidden, P4),
@@ -153,38 +184,39 @@ class DecodeSession:
         self.scale = 1.0 / math.sqrt(c.head_dim)
 
     def set_position(self, position: int):
-        """Uploads the RoPE table of `position` (as the reference uploads its
-        per-step cos/sin textures, DEC:1585-1687)."""
-        c = self.cfg
-        j = np.arange(c.head_dim // 2, dtype=np.float64)
-        ang = position * np.power(c.rope_base, -2.0 * j / c.head_dim)
-        self.cos.copy_(torch.as_tensor(np.cos(ang).astype(np.float32)))
-        self.sin.copy_(torch.as_tensor(np.sin(ang).astype(np.float32)))
+        """Sets the device decode position (the new token's cache row)."""
+        if not 0 <= position < self.cfg.capacity:
+            raise ValueError(f"position {position} outside the cache capacity {self.cfg.capacity}")
+        self.pos.fill_(position)
         self.position = position
 
-    def step(self):
-        """One decode step for self.token at self.position -> self.next_token."""
+    def step(self, advance: bool = False):
+        """One decode step for self.token at the device position ->
+        self.next_token.  With `advance` the step also stores the argmax as the
+        next input token (and in self.history) and moves the position on."""
         c, ctx, d = self.cfg, self.ctx, self.d
-        pos = self.position
-        ctx.embed_q8(self.lm, self.token, self.xa)
+        ctx.embed_q8(self.embed, self.token, self.xa)
         for L in self.layers:
             w = L["w"]
             ctx.linear_group([w["q_proj"], w["k_proj"], w["v_proj"]], d["xa"],
                              [d["q"], d["k"], d["v"]], rmsnorm=True, rms_gamma=L["g_attn"],
                              rms_eps=c.eps)
-            ctx.attention_decode_rope(self.q, self.k, self.v, L["k_cache"], L["v_cache"],
-                                      c.heads_q, c.heads_kv, c.head_dim, c.capacity, pos + 1,
-                                      self.cos, self.sin, self.scale, self.attn)
+            ctx.attention_decode_rope_at(self.q, self.k, self.v, L["k_cache"], L["v_cache"],
+                                         c.heads_q, c.heads_kv, c.head_dim, c.capacity, self.pos,
+                                         self.cos, self.sin, self.scale, self.attn)
             ctx.linear(w["o_proj"], d["attn"], d["xb"], residual=d["xa"])
             ctx.linear(w["gate_proj"], d["xb"], d["h"], rmsnorm=True, rms_gamma=L["g_mlp"],
                        rms_eps=c.eps, up=w["up_proj"])
             ctx.linear(w["down_proj"], d["h"], d["xa"], residual=d["xb"])
         ctx.rmsnorm(d["xa"], d["xn"], self.g_final, c.eps)
         ctx.lmhead_argmax(self.lm, d["xn"], None, self.next_token)
+        if advance:
+            ctx.decode_advance(self.pos, self.token, self.next_token, self.history)
 
-    def capture(self, warmup: int = 2) -> torch.cuda.CUDAGraph:
-        """Captures step() into a HIP graph on a side stream (scratch buffers are
-        sized by the warm-up steps first, so nothing allocates while capturing)."""
+    def capture(self, warmup: int = 2, advance: bool = False) -> torch.cuda.CUDAGraph:
+        """Captures step(advance) into a HIP graph on a side stream.  The warm-up
+        steps (which do not advance) size the context's scratch first, so
+        nothing allocates while capturing."""
         stream = torch.cuda.Stream()
         old = self.ctx.stream
         self.ctx.set_stream(stream)
@@ -196,8 +228,29 @@ class DecodeSession:
             stream.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
-                self.step()
+                self.step(advance=advance)
         finally:
             self.ctx.set_stream(old)
         torch.cuda.synchronize()
         return g
+
+    def generate(self, start_token: int, position: int, count: int,
+                 graph: torch.cuda.CUDAGraph = None) -> list:
+        """Greedy decoding of `count` tokens from `start_token` at `position`
+        (Qwen35DecoderSession.Generate, DEC:1160-1237): each step's argmax is the
+        next step's input.  With `graph` (from capture(advance=True)) every
+        token is one replay of the same graph; otherwise eager steps.  Returns
+        the generated token ids."""
+        if count < 0 or position + count > self.cfg.capacity:
+            raise ValueError(f"{count} tokens from position {position} exceed the cache "
+                             f"capacity {self.cfg.capacity}")
+        self.token.fill_(start_token)
+        self.set_position(position)
+        for _ in range(count):
+            if graph is not None:
+                graph.replay()
+            else:
+                self.step(advance=True)
+        torch.cuda.synchronize()
+        self.position = position + count
+        return [int(t) for t in self.history[position:position + count].cpu().tolist()]

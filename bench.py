@@ -369,20 +369,45 @@ def config3(torch, aexq, ctx, steps: int = 30):
     e1.record()
     torch.cuda.synchronize()
     graph_ms = e0.elapsed_time(e1) / steps
+    # the Generate loop: one graph that ends by feeding the argmax back and
+    # advancing the device position, replayed once per token over the last
+    # `steps` positions of the cache
+    ga = sess.capture(advance=True)
+    start = cfg.capacity - steps
+    sess.generate(1, start - 3, 3, graph=ga)          # warm replays
+    sess.token.fill_(1)
+    sess.set_position(start)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        ga.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    gen_ms = e0.elapsed_time(e1) / steps
+    assert int(sess.pos.item()) == cfg.capacity
     b = cfg.bytes_per_token(cfg.capacity)
     roof = HBM_PEAK_GBS * 1e9 / b["total"]
+    # BASELINE.json's "8 kv heads" reading: twice the cached K/V bytes
+    roof8 = HBM_PEAK_GBS * 1e9 / (b["total"] + b["kv_read"])
+    mean_len = start + (steps + 1) / 2.0
+    b_gen = cfg.bytes_per_token(int(round(mean_len)))["total"]
     out = {"config3_decode": {
         "tokens_per_s_graph": round(1000.0 / graph_ms, 1), "ms_per_token_graph": round(graph_ms, 4),
         "tokens_per_s_eager": round(1000.0 / eager_ms, 1), "ms_per_token_eager": round(eager_ms, 4),
+        "tokens_per_s_generate": round(1000.0 / gen_ms, 1),
+        "ms_per_token_generate": round(gen_ms, 4),
+        "generate_positions": [start, cfg.capacity - 1],
+        "generate_frac_of_roofline": round(b_gen / (gen_ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
         "bytes_per_token": b, "roofline_tokens_per_s": round(roof, 1),
+        "roofline_tokens_per_s_8kv_heads": round(roof8, 1),
         "frac_of_roofline": round(1000.0 / graph_ms / roof, 4),
         "GBps_graph": round(b["total"] / (graph_ms * 1e-3) / 1e9, 1),
         "kv_heads": cfg.heads_kv, "positions": cfg.capacity, "layers": cfg.layers,
         # embedding; per layer q/k/v, attention, o_proj, gate/up, down; final
-        # norm, LM head and argmax finalize
+        # norm, LM head and argmax finalize (+ the advance in the Generate loop)
         "launches_per_token": 1 + cfg.layers * 5 + 3}}
     log(f"config3: {out['config3_decode']}")
-    del g, sess
+    del g, ga, sess
     torch.cuda.empty_cache()
     return out
 

@@ -24,6 +24,11 @@
  *   - nothing falls back: a shape, layout or dtype without a kernel returns
  *     AEXQ_ERR_UNSUPPORTED, as the strict plan does (TEP:389-407).
  *   - one context per host thread; a context is not thread-safe.
+ *   - a context's scratch (argmax partials, split-K planes, normalised rows,
+ *     attention partials) grows on demand.  A replaced buffer is kept until
+ *     aexq_destroy, because a HIP graph captured before the growth still holds
+ *     its address; growth while the context's stream is capturing fails with
+ *     AEXQ_ERR_UNSUPPORTED, so run a sequence once before capturing it.
  */
 #ifndef AEXQ_H
 #define AEXQ_H
@@ -279,6 +284,27 @@ aexq_status aexq_attention_decode_rope(aexq_ctx* ctx, const void* q, const void*
                                        int head_dim, int capacity, int length,
                                        const float* cos_table, const float* sin_table,
                                        float scale, void* out);
+
+/* aexq_attention_decode_rope with the decode position in device memory, so a
+ * captured HIP graph advances from token to token (Qwen35DecoderSession.Generate
+ * feeds each argmax back at the next position, DEC:1160-1237, with the RoPE
+ * rows of that position, DEC:1660-1675).  *position (read on the device and
+ * clamped to [0, capacity - 1]) is the position of the new row; attention runs
+ * over *position + 1 cached positions.  cos_table / sin_table are device fp32
+ * [capacity][head_dim / 2]: row p holds position p's entries.  The launch is
+ * sized for the whole capacity. */
+aexq_status aexq_attention_decode_rope_at(aexq_ctx* ctx, const void* q, const void* k,
+                                          const void* v, void* k_cache, void* v_cache,
+                                          int heads_q, int heads_kv, int head_dim, int capacity,
+                                          const int32_t* position, const float* cos_table,
+                                          const float* sin_table, float scale, void* out);
+
+/* The end of one generated token on the device (DEC:1160-1237: the greedy
+ * argmax becomes the next input token): tokens_out[*position] = *argmax when
+ * tokens_out is non-NULL and *position < tokens_cap, *token = *argmax, then
+ * *position += 1.  All pointers are device int32. */
+aexq_status aexq_decode_advance(aexq_ctx* ctx, int32_t* position, int32_t* token,
+                                const int32_t* argmax, int32_t* tokens_out, int tokens_cap);
 
 #ifdef __cplusplus
 }

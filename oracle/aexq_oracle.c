@@ -662,18 +662,25 @@ void orc_argmax_rows(const float* logits, int rows, int width, int64_t row_strid
 /* ---------------------------------------------------------------------- */
 
 /*
- * RoPE table of one position for the rotate-half layout: angle_j =
- * position * base^(-2j/d), j < d/2, evaluated in float64 and rounded to
- * float32 (the reference uploads per-position cos/sin tables of the same
- * [position][d/2] shape, DEC:1585-1687, and PN:414-473 indexes them by j).
+ * DEC:1660-1675 CreateRopeTextures, the row of one position, in the float32
+ * steps the C# evaluates: e = j * (2f / (half * 2f)); p = Mathf.Pow(theta, e);
+ * inverse = 1f / p; angle = position * inverse (float multiply); entries
+ * Mathf.Cos(angle), Mathf.Sin(angle).  UnityEngine's Mathf.Pow/Cos/Sin take
+ * and return float and evaluate System.Math's double routines in between,
+ * i.e. (float)pow((double)a, (double)b) and (float)cos((double)a).  theta is
+ * the float constant RopeTheta (DEC:172), hence the cast of `base`.
  */
 void orc_rope_table(int position, int head_dim, double base, float* cos_out, float* sin_out) {
   int half = head_dim / 2;
+  float theta = (float)base;
+  float step = 2.0f / ((float)half * 2.0f);
   for (int j = 0; j < half; ++j) {
-    double inv = pow(base, -2.0 * (double)j / (double)head_dim);
-    double a = (double)position * inv;
-    cos_out[j] = (float)cos(a);
-    sin_out[j] = (float)sin(a);
+    float e = (float)j * step;
+    float p = (float)pow((double)theta, (double)e);
+    float inverse = 1.0f / p;
+    float angle = (float)position * inverse;
+    cos_out[j] = (float)cos((double)angle);
+    sin_out[j] = (float)sin((double)angle);
   }
 }
 

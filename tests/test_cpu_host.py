@@ -114,3 +114,17 @@ def test_archive_header_checks_match_the_reader(orc):
     for bad in bad_cases:
         with pytest.raises(_abi.InvalidDataError):
             aexq.archive_header(bad)
+
+
+@pytest.mark.parametrize("head_dim,base,capacity", [(128, 1e6, 2048), (64, 1e7, 300)])
+def test_decoder_rope_tables_equal_oracle_rows(orc, head_dim, base, capacity):
+    """The decode session's [capacity][d/2] RoPE tables (built once on the host,
+    indexed on the device by the decode position) hold, row for row and bit for
+    bit, the oracle's table of that position, which the oracle tests pin
+    against the frequency schedule and the rotation direction."""
+    from aiimage_amd import decoder
+    ct, st = decoder.rope_tables(capacity, head_dim, base)
+    assert ct.shape == (capacity, head_dim // 2) and ct.dtype == np.float32
+    for p in (0, 1, 2, 37, capacity // 2, capacity - 1):
+        c, s = orc.rope_table(p, head_dim, base)
+        assert np.array_equal(ct[p], c) and np.array_equal(st[p], s), p

@@ -449,6 +449,55 @@ def test_rope_table_and_rotation_properties(orc):
     assert abs(dot_at(10, 3) - dot_at(107, 100)) < 1e-3 * abs(dot_at(10, 3)) + 1e-3
 
 
+def test_rope_rotation_direction_closed_form(orc):
+    """PN:414-473 (non-interleaved): first = x0 cos - x1 sin, second = x0 sin +
+    x1 cos for the pair (j, j + d/2).  A quarter turn (cos 0, sin 1) sends e_j
+    to e_{j+d/2} and e_{j+d/2} to -e_j; a sign flip of either sin term, or the
+    pair partner taken as j + 1 (interleaved), fails one of these."""
+    d, half = 8, 4
+    c = np.zeros(half, np.float32)
+    s = np.ones(half, np.float32)
+    for j in (0, 1, half - 1):
+        e_j = np.zeros((1, d), np.float32)
+        e_j[0, j] = 1.0
+        want = np.zeros((1, d), np.float32)
+        want[0, j + half] = 1.0
+        assert np.array_equal(orc.rope_rotate_half(e_j, c, s), want), j
+        e_p = np.zeros((1, d), np.float32)
+        e_p[0, j + half] = 1.0
+        want = np.zeros((1, d), np.float32)
+        want[0, j] = -1.0
+        assert np.array_equal(orc.rope_rotate_half(e_p, c, s), want), j
+    # a half turn negates every element whatever the sin convention
+    assert np.array_equal(orc.rope_rotate_half(np.arange(1, d + 1, dtype=np.float32)[None],
+                                               -np.ones(half, np.float32), np.zeros(half, np.float32)),
+                          -np.arange(1, d + 1, dtype=np.float32)[None])
+
+
+@pytest.mark.parametrize("head_dim,base", [(128, 1e6), (64, 1e7)])
+def test_rope_table_frequency_schedule(orc, head_dim, base):
+    """DEC:1660-1675: pair j turns by position / base^(2j/d).  Position 1 gives
+    the inverse frequency itself (below pi, so atan2 recovers it); it is
+    checked at j = 1, d/4 and d/2 - 1 against exp(-2j/d * ln base) evaluated
+    here in float64 (float32 rounding of the reference's steps is within
+    2e-6 relative).  A larger position checks that angles scale with it."""
+    half = head_dim // 2
+    c1, s1 = orc.rope_table(1, head_dim, base)
+    for j in (1, head_dim // 4, half - 1):
+        want = math.exp(-2.0 * j / head_dim * math.log(base))
+        got = math.atan2(float(s1[j]), float(c1[j]))
+        assert abs(got - want) <= 2e-6 * want + 1e-9, (j, got, want)
+    pos = 1537
+    cp, sp = orc.rope_table(pos, head_dim, base)
+    for j in (1, head_dim // 4, half - 1):
+        ang = pos * math.exp(-2.0 * j / head_dim * math.log(base))
+        # the angle is formed in float32: its rounding (<= 2^-24 relative) bounds the error
+        tol = abs(ang) * 2.0 ** -22 + 1e-6
+        assert abs(float(cp[j]) - math.cos(ang)) <= tol and abs(float(sp[j]) - math.sin(ang)) <= tol, j
+    # j = 0 turns by exactly `position` radians (float(position) is exact)
+    assert float(cp[0]) == np.float32(math.cos(pos)) and float(sp[0]) == np.float32(math.sin(pos))
+
+
 def test_sdpa_decode_properties(orc):
     """SDPA (MM:420-544) without retyping it: equal keys give the mean of the
     values, one position gives its value row, a dominant score selects its row,
