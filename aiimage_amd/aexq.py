@@ -267,6 +267,14 @@ class Context:
             ctypes.c_void_p(top2_gap.data_ptr()) if top2_gap is not None else None),
             "aexq_lmhead_argmax")
 
+    def lmhead_argmax_noalloc(self, w: "QuantWeight", x: _abi.Tensor, argmax: torch.Tensor,
+                              top2_gap: Optional[torch.Tensor] = None):
+        """lmhead_argmax that allocates nothing (a fixed device scratch)."""
+        check(self._lib.aexq_lmhead_argmax_noalloc(
+            self.handle, w.handle, ctypes.byref(x), ctypes.c_void_p(argmax.data_ptr()),
+            ctypes.c_void_p(top2_gap.data_ptr()) if top2_gap is not None else None),
+            "aexq_lmhead_argmax_noalloc")
+
     def argmax(self, logits: _abi.Tensor, argmax: torch.Tensor,
                top2_gap: Optional[torch.Tensor] = None):
         check(self._lib.aexq_argmax(self.handle, ctypes.byref(logits),

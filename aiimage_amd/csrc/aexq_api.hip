@@ -8,6 +8,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -73,6 +74,8 @@ struct aexq_ctx {
   // scratch buffers replaced by larger ones: a HIP graph captured before the
   // growth still holds their addresses, so they live until aexq_destroy
   std::vector<void*> retired;
+  // the device address of the no-allocation entry point's `scratch` array
+  float* noalloc = nullptr;
 };
 
 struct aexq_weight {
@@ -96,6 +99,41 @@ struct aexq_weight {
 };
 
 static long long round_up(long long v, long long a) { return (v + a - 1) / a * a; }
+
+// ---------------------------------------------------------------------------
+// Scratch of aexq_lmhead_argmax_noalloc: the argmax partials of one launch
+// (best value, index, second best; kNoAllocParts entries each, i.e. workgroups
+// x activation rows), in a file-scope device array instead of memory the
+// library allocates.  Each GPU holds its own copy from module load to process
+// exit; its address on a device comes from hipGetSymbolAddress, taken once per
+// device when the first context on that device is created.  Every entry the
+// argmax merge reads is written by the same call, so nothing in it has to
+// start at zero; calls that overlap on one GPU (other streams or contexts)
+// share the array and race.
+// ---------------------------------------------------------------------------
+constexpr long long kNoAllocParts = 32768;  // 3 x 128 KiB
+static __device__ __align__(256) float scratch[3 * kNoAllocParts];
+constexpr int kMaxDevices = 64;
+static std::mutex g_noalloc_mu;
+static float* g_noalloc_ptr[kMaxDevices];      // device address of `scratch` per device
+static hipError_t g_noalloc_err[kMaxDevices];  // why it is missing, if it is
+
+// With `device` current: the device address of `scratch` on it (once).
+static float* noalloc_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_ptr[device] && g_noalloc_err[device] == hipSuccess) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && p) {
+      g_noalloc_ptr[device] = (float*)p;
+    } else {
+      g_noalloc_err[device] = e != hipSuccess ? e : hipErrorInvalidSymbol;
+      (void)hipGetLastError();  // leave no sticky error for the caller's next launch
+    }
+  }
+  return g_noalloc_ptr[device];
+}
 
 // Makes the context scratch buffer *buf hold at least `bytes`.  A buffer that
 // is replaced is retired, not freed (a HIP graph captured earlier may still
@@ -141,6 +179,7 @@ extern "C" aexq_status aexq_create(int device, void* hip_stream, aexq_ctx** out)
   c->device = device;
   c->cus = cus > 0 ? cus : 1;
   c->stream = (hipStream_t)hip_stream;
+  c->noalloc = noalloc_scratch(device);  // null: aexq_lmhead_argmax_noalloc reports why
   *out = c;
   return AEXQ_OK;
 }
@@ -1393,6 +1432,61 @@ static aexq_status argmax_over_logits(aexq_ctx* ctx, const float* logits, int m,
   return AEXQ_OK;
 }
 
+// Where one LM-head launch writes its argmax partials: the context's growing
+// scratch, or a fixed buffer of `cap` entries per array.
+struct Partials {
+  float* best = nullptr;
+  int* index = nullptr;
+  float* second = nullptr;
+  long long cap = 0;
+};
+
+static bool lmhead_fused(const Plan& plan) {
+  return (plan.fast && plan.entry->cfg.argmax) ||
+         (plan.kind == kPlanMfma && plan.mentry->cfg.argmax);
+}
+
+// The LM head with the argmax fused into the matvec: M = 1 on the streaming
+// kernel, M = 2..32 on the wide MFMA kernel; one (best, index, second)
+// partial per workgroup and row, then the merge.  `fixed` null: the
+// partials go to the context's scratch (grown as needed).
+static aexq_status lmhead_fused_launch(aexq_ctx* ctx, Plan& plan, const char* op,
+                                       int32_t* argmax, float* top2_gap, const Partials* fixed) {
+  const int M = plan.p.m;
+  const int parts = plan.grid;  // one partial per workgroup and row
+  const long long need = (long long)parts * M;
+  Partials pt;
+  if (fixed) {
+    if (need > fixed->cap)
+      return fail(AEXQ_ERR_UNSUPPORTED, op,
+                  "%d workgroups x %d rows = %lld argmax partials exceed the fixed scratch of "
+                  "%lld | rejectedFallback=allocation",
+                  parts, M, need, fixed->cap);
+    pt = *fixed;
+  } else {
+    aexq_status st = ensure_parts(ctx, need, op);
+    if (st) return st;
+    pt.best = ctx->part_best;
+    pt.index = ctx->part_index;
+    pt.second = ctx->part_second;
+  }
+  plan.p.part_best = pt.best;
+  plan.p.part_index = pt.index;
+  plan.p.part_second = pt.second;
+  plan.p.parts = parts;
+  if (plan.fast) {
+    hipError_t e = qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, op, "lm head launch");
+  } else {
+    aexq_status st = launch_plan(ctx, plan, op);
+    if (st) return st;
+  }
+  ArgmaxParams ap{pt.best, pt.index, pt.second, parts, M, argmax, top2_gap};
+  hipError_t e = argmax_finalize_launch(ap, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
+  return AEXQ_OK;
+}
+
 extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
                                           const aexq_tensor* x, const aexq_tensor* logits,
                                           int32_t* argmax, float* top2_gap) {
@@ -1405,42 +1499,9 @@ extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
   aexq_status st = make_plan(ctx, 1, ws, x, ys, nullptr, true, &plan);
   if (st) return st;
   HIP_TRY(op, hipSetDevice(ctx->device));
-  const int M = plan.p.m;
-  if (plan.fast && plan.entry->cfg.argmax) {
-    const int parts = plan.grid;  // one partial per workgroup
-    st = ensure_parts(ctx, (long long)parts * M, op);
-    if (st) return st;
-    plan.p.part_best = ctx->part_best;
-    plan.p.part_index = ctx->part_index;
-    plan.p.part_second = ctx->part_second;
-    plan.p.parts = parts;
-    hipError_t e = qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream);
-    if (e != hipSuccess) return hip_fail(e, op, "lm head launch");
-    ArgmaxParams ap{ctx->part_best, ctx->part_index, ctx->part_second, parts, M, argmax,
-                    top2_gap};
-    e = argmax_finalize_launch(ap, ctx->stream);
-    if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
-    return AEXQ_OK;
-  }
-  if (plan.kind == kPlanMfma && plan.mentry->cfg.argmax) {
-    // M = 2..32 rows per launch on the wide MFMA kernel, one partial per
-    // workgroup and row, then the same merge
-    const int parts = plan.grid;
-    st = ensure_parts(ctx, (long long)parts * M, op);
-    if (st) return st;
-    plan.p.part_best = ctx->part_best;
-    plan.p.part_index = ctx->part_index;
-    plan.p.part_second = ctx->part_second;
-    plan.p.parts = parts;
-    st = launch_plan(ctx, plan, op);
-    if (st) return st;
-    ArgmaxParams ap{ctx->part_best, ctx->part_index, ctx->part_second, parts, M, argmax,
-                    top2_gap};
-    hipError_t e = argmax_finalize_launch(ap, ctx->stream);
-    if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
-    return AEXQ_OK;
-  }
+  if (lmhead_fused(plan)) return lmhead_fused_launch(ctx, plan, op, argmax, top2_gap, nullptr);
   // logits first (into the caller's tensor or a scratch buffer), then the argmax pass
+  const int M = plan.p.m;
   float* lg = nullptr;
   long long rstride = plan.p.mat[0].y_rstride;
   if (logits) {
@@ -1459,6 +1520,37 @@ extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
   st = launch_plan(ctx, plan, op);
   if (st) return st;
   return argmax_over_logits(ctx, lg, M, w->n, rstride, argmax, top2_gap, op);
+}
+
+extern "C" aexq_status aexq_lmhead_argmax_noalloc(aexq_ctx* ctx, const aexq_weight* w,
+                                                  const aexq_tensor* x, int32_t* argmax,
+                                                  float* top2_gap) {
+  const char* op = "aexq_lmhead_argmax_noalloc";
+  if (!argmax) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "argmax is NULL");
+  if (w && w->batch != 1) return fail(AEXQ_ERR_UNSUPPORTED, op, "stacked LM head");
+  Plan plan;
+  const aexq_weight* ws[1] = {w};
+  const aexq_tensor* ys[1] = {nullptr};
+  aexq_status st = make_plan(ctx, 1, ws, x, ys, nullptr, true, &plan);
+  if (st) return st;
+  if (!lmhead_fused(plan))
+    return fail(AEXQ_ERR_UNSUPPORTED, op,
+                "no fused-argmax kernel for M=%d K=%d (the logits pass needs a buffer of its "
+                "own) | rejectedFallback=allocation",
+                plan.p.m, plan.p.k);
+  if (!ctx->noalloc)
+    return fail(AEXQ_ERR_DEVICE, op, "no device address for the fixed scratch on device %d | hip=%s",
+                ctx->device,
+                hipGetErrorString(ctx->device >= 0 && ctx->device < kMaxDevices
+                                      ? g_noalloc_err[ctx->device]
+                                      : hipErrorInvalidDevice));
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  Partials fixed;
+  fixed.best = ctx->noalloc;
+  fixed.index = (int*)(ctx->noalloc + kNoAllocParts);
+  fixed.second = ctx->noalloc + 2 * kNoAllocParts;
+  fixed.cap = kNoAllocParts;
+  return lmhead_fused_launch(ctx, plan, op, argmax, top2_gap, &fixed);
 }
 
 extern "C" aexq_status aexq_argmax(aexq_ctx* ctx, const aexq_tensor* logits, int32_t* argmax,

@@ -229,6 +229,20 @@ aexq_status aexq_linear_group(aexq_ctx* ctx, int count, const aexq_weight* const
 aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
                                const aexq_tensor* logits, int32_t* argmax, float* top2_gap);
 
+/* aexq_lmhead_argmax without logits for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference: it exists for those
+ * callers only.  It allocates nothing: the argmax partials go to a fixed
+ * device array of the library (3 x 32768 entries, 384 KiB per GPU, held until
+ * the process ends) instead of the context's growing scratch.  Only the
+ * fused-argmax launches qualify (K a multiple of 16 at M = 1, of 128 above);
+ * a launch needing more than 32768 (workgroup, row) partials, or the separate
+ * logits pass, returns AEXQ_ERR_UNSUPPORTED.  Every call on one GPU shares the
+ * array: calls that overlap on a GPU (other streams or contexts) race.
+ * Results equal aexq_lmhead_argmax's. */
+aexq_status aexq_lmhead_argmax_noalloc(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
+                                       int32_t* argmax, float* top2_gap);
+
 /* Row-wise argmax of an existing logits tensor (OPS:9982-10004, MM:645-686). */
 aexq_status aexq_argmax(aexq_ctx* ctx, const aexq_tensor* logits, int32_t* argmax,
                         float* top2_gap);
