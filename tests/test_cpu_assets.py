@@ -121,3 +121,25 @@ def test_sharded_archive_walk(tmp_path, orc):
     with a.open_read("model.aqs") as s:              # more layers than records
         with pytest.raises(assets.InvalidDataError):
             assets.load_archive_weights(_RecordCtx(), s, shapes + [(8, 8, 4)])
+
+
+def test_sharded_file_random_slices(tmp_path):
+    """Every (offset, length) window of a logical file cut into uneven shards,
+    some of one byte, reads the same bytes as the concatenation."""
+    root = str(tmp_path)
+    rng = np.random.default_rng(11)
+    blob = rng.integers(0, 256, 97, dtype=np.uint8).tobytes()
+    cuts = [0, 1, 2, 30, 31, 64, 96, 97]
+    parts = [_part(root, "s/%d" % i, blob[a:b]) for i, (a, b) in enumerate(zip(cuts, cuts[1:]))]
+    _manifest(root, {"f": {"stored_bytes": len(blob), "parts": parts}})
+    a = assets.MobileAssetSet.try_load(root, verify_hashes=True)
+    with a.open_read("f") as s:
+        assert len(s) == len(blob)
+        for off in range(len(blob) + 1):
+            for n in (0, 1, 2, 33, 200):
+                s.seek(off)
+                assert s.read(n) == blob[off:off + n]
+                assert s.tell() == min(off + n, len(blob))
+        s.seek(90)
+        with pytest.raises(assets.InvalidDataError):
+            s.read_exact(8)
