@@ -102,6 +102,22 @@ class WeightInfo(ctypes.Structure):
                 ("code_bytes", ctypes.c_int64), ("scale_bytes", ctypes.c_int64)]
 
 
+class DecoderLayer(ctypes.Structure):
+    _fields_ = [("q_proj", ctypes.c_void_p), ("k_proj", ctypes.c_void_p),
+                ("v_proj", ctypes.c_void_p), ("o_proj", ctypes.c_void_p),
+                ("gate_proj", ctypes.c_void_p), ("up_proj", ctypes.c_void_p),
+                ("down_proj", ctypes.c_void_p), ("attn_norm", ctypes.c_void_p),
+                ("mlp_norm", ctypes.c_void_p), ("k_cache", ctypes.c_void_p),
+                ("v_cache", ctypes.c_void_p)]
+
+
+class DecoderConfig(ctypes.Structure):
+    _fields_ = [("heads_q", ctypes.c_int), ("heads_kv", ctypes.c_int), ("head_dim", ctypes.c_int),
+                ("capacity", ctypes.c_int), ("rms_eps", ctypes.c_float),
+                ("attn_scale", ctypes.c_float), ("rope_cos", ctypes.c_void_p),
+                ("rope_sin", ctypes.c_void_p), ("workgroups", ctypes.c_int)]
+
+
 _lib = None
 
 
@@ -165,6 +181,13 @@ def _declare(L):
         "aexq_attention_decode_rope_at": (i32, [P, P, P, P, P, P, i32, i32, i32, i32, P, P, P,
                                                 f32, P]),
         "aexq_decode_advance": (i32, [P, P, P, P, P, i32]),
+        "aexq_decoder_create": (i32, [P, ctypes.POINTER(DecoderConfig), ctypes.POINTER(DecoderLayer),
+                                      i32, P, PP]),
+        "aexq_decoder_run": (i32, [P, P, P, P]),
+        "aexq_decoder_error": (i32, [P, ctypes.POINTER(i32)]),
+        "aexq_decoder_info": (i32, [P, ctypes.POINTER(i32), ctypes.POINTER(i32),
+                                    ctypes.POINTER(i32)]),
+        "aexq_decoder_release": (None, [P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -350,6 +350,15 @@ class Context:
             P(tokens_out) if tokens_out is not None else None,
             tokens_out.numel() if tokens_out is not None else 0), "aexq_decode_advance")
 
+    def decoder(self, layers, embedding: "QuantWeight", heads_q: int, heads_kv: int,
+                head_dim: int, capacity: int, rms_eps: float, attn_scale: float,
+                rope_cos: torch.Tensor, rope_sin: torch.Tensor, workgroups: int = 0) -> "Decoder":
+        """The decoder layers of a decode step as one launch (aexq_decoder_create).
+        `layers` is a sequence of dicts with the seven Q4 weights (q_proj ...
+        down_proj), the two gammas (attn_norm, mlp_norm) and the fp16 caches."""
+        return Decoder(self, layers, embedding, heads_q, heads_kv, head_dim, capacity, rms_eps,
+                       attn_scale, rope_cos, rope_sin, workgroups)
+
     def dequant(self, w: "QuantWeight") -> torch.Tensor:
         info = w.info()
         out = torch.empty((info.n, info.k), dtype=torch.float32, device=f"cuda:{self.device}")
@@ -495,3 +504,61 @@ class HipGemmLayer:
                         describe(y, rows, self.n, y_layout), alpha=self.alpha, beta=self.beta,
                         c=self.c, broadcast_c=self.broadcast_c if self.c is not None else -1)
         return y, y_layout
+
+
+class Decoder:
+    """aexq_decoder: every decoder layer of a decode step in one persistent
+    launch (DecodeCore, DEC:463-585).  Keeps references to the tensors and
+    weights it points at, which must outlive it."""
+
+    _WEIGHTS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+    def __init__(self, ctx: Context, layers, embedding, heads_q, heads_kv, head_dim, capacity,
+                 rms_eps, attn_scale, rope_cos, rope_sin, workgroups=0):
+        self._lib = ctx._lib
+        self.ctx = ctx
+        self._keep = (list(layers), embedding, rope_cos, rope_sin)
+        arr = (_abi.DecoderLayer * len(layers))()
+        for i, L in enumerate(layers):
+            for name in self._WEIGHTS:
+                setattr(arr[i], name, L[name].handle)
+            arr[i].attn_norm = L["attn_norm"].data_ptr()
+            arr[i].mlp_norm = L["mlp_norm"].data_ptr()
+            arr[i].k_cache = L["k_cache"].data_ptr()
+            arr[i].v_cache = L["v_cache"].data_ptr()
+        cfg = _abi.DecoderConfig(heads_q, heads_kv, head_dim, capacity, rms_eps, attn_scale,
+                                 rope_cos.data_ptr(), rope_sin.data_ptr(), workgroups)
+        h = ctypes.c_void_p()
+        check(self._lib.aexq_decoder_create(ctx.handle, ctypes.byref(cfg), arr, len(layers),
+                                            embedding.handle, ctypes.byref(h)),
+              "aexq_decoder_create")
+        self.handle = h
+
+    def run(self, token: torch.Tensor, position: torch.Tensor, hidden_out: torch.Tensor):
+        check(self._lib.aexq_decoder_run(self.handle, ctypes.c_void_p(token.data_ptr()),
+                                         ctypes.c_void_p(position.data_ptr()),
+                                         ctypes.c_void_p(hidden_out.data_ptr())),
+              "aexq_decoder_run")
+
+    def error(self) -> int:
+        """Synchronizes; 1 when a run gave up a bounded wait since the last call."""
+        f = ctypes.c_int(0)
+        check(self._lib.aexq_decoder_error(self.handle, ctypes.byref(f)), "aexq_decoder_error")
+        return f.value
+
+    def info(self):
+        g, s, sp = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        check(self._lib.aexq_decoder_info(self.handle, ctypes.byref(g), ctypes.byref(s),
+                                          ctypes.byref(sp)), "aexq_decoder_info")
+        return {"workgroups": g.value, "splits": s.value, "split_positions": sp.value}
+
+    def close(self):
+        if self.handle:
+            self._lib.aexq_decoder_release(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

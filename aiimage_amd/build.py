@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libaexq.so")
 SOURCES = ["aexq_qmv_q8.hip", "aexq_qmv_q4.hip", "aexq_qmm.hip", "aexq_qmmw.hip", "aexq_qgemm.hip",
            "aexq_kernels.hip",
-           "aexq_decode.hip", "aexq_api.hip"]
+           "aexq_decode.hip", "aexq_step.hip", "aexq_api.hip"]
 ARCH = "gfx950"
 
 

@@ -1745,3 +1745,221 @@ extern "C" aexq_status aexq_decode_advance(aexq_ctx* ctx, int32_t* position, int
   if (e != hipSuccess) return hip_fail(e, op, "advance launch");
   return AEXQ_OK;
 }
+
+// ---------------------------------------------------------------------------
+// The decoder layers of a decode step as one persistent launch
+// (DecodeCore, DEC:463-585; the per-layer loop LF:996-1136).  The decoder
+// object holds the layers' device pointers and the tagged exchange buffers;
+// aexq_decoder_run allocates nothing, so a graph may capture it.
+// ---------------------------------------------------------------------------
+struct aexq_decoder {
+  aexq_ctx* ctx = nullptr;
+  int device = 0;
+  int grid = 0;
+  StepParams p{};
+  void* mem = nullptr;  // layer table + exchange buffers
+};
+
+// Workgroups of the fused step: 128 (one per CU on half of the part) when the
+// cache fits their attention splits, else 256.
+static int decoder_grid(int hkv, int cap, int requested) {
+  if (requested > 0) return requested;
+  for (int g = 128; g <= 256; g *= 2) {
+    int s = g / hkv;
+    if (s > kStepMaxSplits) s = kStepMaxSplits;
+    if (s > 0 && (long long)s * kStepMaxSplitPos >= cap) return g;
+  }
+  return 256;
+}
+
+extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_config* cfg,
+                                           const aexq_decoder_layer* layers, int count,
+                                           const aexq_weight* embedding, aexq_decoder** out) {
+  const char* op = "aexq_decoder_create";
+  if (!ctx || !cfg || !layers || !embedding || !out)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  if (count <= 0) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "count=%d", count);
+  if (!cfg->rope_cos || !cfg->rope_sin)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "rope tables are NULL");
+  const int hq = cfg->heads_q, hkv = cfg->heads_kv, cap = cfg->capacity;
+  if (cfg->head_dim != kStepHeadDim)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "head_dim=%d (the fused step takes %d) | "
+                "rejectedFallback=per-operator step", cfg->head_dim, kStepHeadDim);
+  if (hq <= 0 || hkv <= 0 || hq % hkv != 0 || cap <= 0)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "heads_q=%d heads_kv=%d capacity=%d", hq, hkv,
+                cap);
+  const aexq_weight* l0q = layers[0].q_proj;
+  if (!l0q) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "layer 0 q_proj is NULL");
+  const int hid = l0q->k, qw = hq * kStepHeadDim, kvw = hkv * kStepHeadDim;
+  const int inter = layers[0].gate_proj ? layers[0].gate_proj->n : 0;
+  const int sdt = l0q->scale_dtype;
+  // every layer: Q4, one scale per 32 codes, the model's shapes, one scale dtype
+  for (int l = 0; l < count; ++l) {
+    const aexq_decoder_layer& L = layers[l];
+    const aexq_weight* ws[7] = {L.q_proj, L.k_proj, L.v_proj, L.o_proj, L.gate_proj, L.up_proj,
+                                L.down_proj};
+    const int nn[7] = {qw, kvw, kvw, hid, inter, inter, hid};
+    const int kk[7] = {hid, hid, hid, qw, hid, hid, inter};
+    for (int i = 0; i < 7; ++i) {
+      const aexq_weight* w = ws[i];
+      if (!w) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "layer %d weight %d is NULL", l, i);
+      if (w->bits != 4 || w->block != 32 || w->batch != 1 || w->scale_dtype != sdt)
+        return fail(AEXQ_ERR_UNSUPPORTED, op,
+                    "layer %d weight %d: bits=%d block=%d batch=%d scale_dtype=%d (the fused step "
+                    "takes unstacked Q4 with one scale per 32 codes) | rejectedFallback=per-operator "
+                    "step", l, i, w->bits, w->block, w->batch, w->scale_dtype);
+      if (w->n != nn[i] || w->k != kk[i])
+        return fail(AEXQ_ERR_SHAPE, op, "layer %d weight %d is %dx%d, expected %dx%d", l, i,
+                    w->n, w->k, nn[i], kk[i]);
+      if (w->device != ctx->device)
+        return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "layer %d weight %d lives on device %d", l, i,
+                    w->device);
+    }
+    if (!L.attn_norm || !L.mlp_norm || !L.k_cache || !L.v_cache)
+      return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "layer %d: NULL norm or cache", l);
+  }
+  if (embedding->bits != 8 || embedding->k != hid || embedding->batch != 1)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "embedding bits=%d k=%d batch=%d (Q8 of width %d)",
+                embedding->bits, embedding->k, embedding->batch, hid);
+  if (hid % 32 || hid > kStepMaxHidden || inter % 32 || inter > kStepMaxInter ||
+      !decode_layers_supported(hq / hkv, hid / 32, qw / 32, inter / 32))
+    return fail(AEXQ_ERR_UNSUPPORTED, op,
+                "hidden=%d q width=%d intermediate=%d, %d q heads per kv head: no fused-step "
+                "kernel for these shapes | rejectedFallback=per-operator step",
+                hid, qw, inter, hq / hkv);
+  const int grid = decoder_grid(hkv, cap, cfg->workgroups);
+  int splits = grid / hkv;
+  if (splits > kStepMaxSplits) splits = kStepMaxSplits;
+  const int sp = (int)round_up((cap + splits - 1) / splits, 8);
+  const int merge = hq * kStepHeadDim / grid;
+  const int rq = (int)round_up((qw + 2 * kvw + grid - 1) / grid, 4);
+  const int rh = (int)round_up((hid + grid - 1) / grid, 2);
+  const int ri = (int)round_up((inter + grid - 1) / grid, 4);
+  if (grid < hkv || splits < 1 || sp > kStepMaxSplitPos || merge < 1 || merge > kStepMaxMerge ||
+      kStepHeadDim % merge || merge * grid != hq * kStepHeadDim || merge % 8 ||
+      splits * (merge / 8) > 64 || rq > 4 * kStepComputeWaves || rh > kStepComputeWaves ||
+      ri > 4 * kStepComputeWaves || rq > kStepOutWords || ri > kStepOutWords ||
+      (hq / hkv) * kStepPartStride > kStepOutWords)
+    return fail(AEXQ_ERR_UNSUPPORTED, op,
+                "capacity=%d on %d workgroups: %d splits of %d positions, %d merged dims, rows "
+                "%d/%d/%d per workgroup | rejectedFallback=per-operator step",
+                cap, grid, splits, sp, merge, rq, rh, ri);
+  HIP_TRY(op, hipSetDevice(ctx->device));
+  int per_cu = 0;
+  HIP_TRY(op, decode_layers_occupancy(&per_cu));
+  if ((long long)per_cu * ctx->cus < grid)
+    return fail(AEXQ_ERR_UNSUPPORTED, op,
+                "%d workgroups are not co-resident (%d per CU x %d CUs) | rejectedFallback="
+                "per-operator step", grid, per_cu, ctx->cus);
+
+  // one allocation: layer table, then the exchange buffers (256-byte aligned)
+  std::vector<StepLayer> table((size_t)count);
+  for (int l = 0; l < count; ++l) {
+    const aexq_decoder_layer& L = layers[l];
+    const aexq_weight* ws[7] = {L.q_proj, L.k_proj, L.v_proj, L.o_proj, L.gate_proj, L.up_proj,
+                                L.down_proj};
+    for (int i = 0; i < 7; ++i) {
+      table[l].w[i] = ws[i]->codes;
+      table[l].s[i] = ws[i]->scales;
+    }
+    table[l].g_attn = L.attn_norm;
+    table[l].g_mlp = L.mlp_norm;
+    table[l].kc = (uint16_t*)L.k_cache;
+    table[l].vc = (uint16_t*)L.v_cache;
+  }
+  const long long words[8] = {hid, qw + 2 * kvw, (long long)hq * splits * kStepPartStride, qw, hid,
+                              inter, 1, 1};
+  long long off[9];
+  off[0] = round_up((long long)count * sizeof(StepLayer), 256);
+  for (int i = 0; i < 8; ++i) off[i + 1] = off[i] + round_up(words[i] * 4, 256);
+  aexq_decoder* d = new aexq_decoder();
+  hipError_t e = hipMalloc(&d->mem, (size_t)off[8]);
+  if (e == hipSuccess) e = hipMemset(d->mem, 0, (size_t)off[8]);
+  if (e == hipSuccess)
+    e = hipMemcpy(d->mem, table.data(), (size_t)count * sizeof(StepLayer), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(d->mem);
+    delete d;
+    return hip_fail(e, op, "decoder buffers");
+  }
+  char* base = (char*)d->mem;
+  StepParams& p = d->p;
+  p.layers = (const StepLayer*)base;
+  p.nlayers = count;
+  p.hidden = hid;
+  p.qw = qw;
+  p.kvw = kvw;
+  p.inter = inter;
+  p.hq = hq;
+  p.hkv = hkv;
+  p.cap = cap;
+  p.sf16 = sdt == AEXQ_DTYPE_F16;
+  p.eps = cfg->rms_eps;
+  p.scale = cfg->attn_scale;
+  p.emb_codes = embedding->codes;
+  p.emb_scales = embedding->scales;
+  p.emb_sf16 = embedding->scale_dtype == AEXQ_DTYPE_F16;
+  p.vocab = embedding->n;
+  p.cos_t = cfg->rope_cos;
+  p.sin_t = cfg->rope_sin;
+  p.xa_t = (uint32_t*)(base + off[0]);
+  p.qkv_t = (uint32_t*)(base + off[1]);
+  p.part_t = (uint32_t*)(base + off[2]);
+  p.attn_t = (uint32_t*)(base + off[3]);
+  p.xb_t = (uint32_t*)(base + off[4]);
+  p.h_t = (uint32_t*)(base + off[5]);
+  p.epoch = (uint32_t*)(base + off[6]);
+  p.err = (int*)(base + off[7]);
+  p.rows_qkv = rq;
+  p.rows_hid = rh;
+  p.rows_inter = ri;
+  p.splits = splits;
+  p.split_pos = sp;
+  p.merge_dims = merge;
+  d->ctx = ctx;
+  d->device = ctx->device;
+  d->grid = grid;
+  *out = d;
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_decoder_run(aexq_decoder* d, const int32_t* token,
+                                        const int32_t* position, void* hidden_out) {
+  const char* op = "aexq_decoder_run";
+  if (!d || !token || !position || !hidden_out)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  HIP_TRY(op, hipSetDevice(d->device));
+  StepParams p = d->p;
+  p.token = token;
+  p.pos = position;
+  p.out = (uint16_t*)hidden_out;
+  hipError_t e = decode_layers_launch(p, d->grid, d->ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, op, "fused step launch");
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_decoder_error(aexq_decoder* d, int* flag) {
+  const char* op = "aexq_decoder_error";
+  if (!d || !flag) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
+  HIP_TRY(op, hipSetDevice(d->device));
+  HIP_TRY(op, hipStreamSynchronize(d->ctx->stream));
+  HIP_TRY(op, hipMemcpy(flag, d->p.err, sizeof(int), hipMemcpyDeviceToHost));
+  HIP_TRY(op, hipMemset(d->p.err, 0, sizeof(int)));
+  return AEXQ_OK;
+}
+
+extern "C" aexq_status aexq_decoder_info(const aexq_decoder* d, int* workgroups, int* splits,
+                                         int* split_positions) {
+  if (!d) return fail(AEXQ_ERR_INVALID_ARGUMENT, "aexq_decoder_info", "NULL decoder");
+  if (workgroups) *workgroups = d->grid;
+  if (splits) *splits = d->p.splits;
+  if (split_positions) *split_positions = d->p.split_pos;
+  return AEXQ_OK;
+}
+
+extern "C" void aexq_decoder_release(aexq_decoder* d) {
+  if (!d) return;
+  (void)hipSetDevice(d->device);
+  (void)hipFree(d->mem);
+  delete d;
+}

@@ -131,7 +131,10 @@ def host_kv_cache(cfg: ModelConfig, layer: int):
 class DecodeSession:
     """Device state of the synthetic model and one decode step (eager or graph)."""
 
-    def __init__(self, ctx: aexq.Context, cfg: ModelConfig, device: str = "cuda"):
+    def __init__(self, ctx: aexq.Context, cfg: ModelConfig, device: str = "cuda",
+                 fused: bool = False, workgroups: int = 0):
+        """fused: the layers run as one launch (aexq_decoder_run) instead of
+        five launches per layer."""
         self.ctx, self.cfg, self.device = ctx, cfg, device
         P4 = aexq.LAYOUT_PACK4_LINEAR
         c = cfg
@@ -182,6 +185,13 @@ class DecodeSession:
         }
         self.position = None
         self.scale = 1.0 / math.sqrt(c.head_dim)
+        self.fused = None
+        if fused:
+            layers = [dict(L["w"], attn_norm=L["g_attn"], mlp_norm=L["g_mlp"],
+                           k_cache=L["k_cache"], v_cache=L["v_cache"]) for L in self.layers]
+            self.fused = ctx.decoder(layers, self.embed, c.heads_q, c.heads_kv, c.head_dim,
+                                     c.capacity, c.eps, self.scale, self.cos, self.sin,
+                                     workgroups)
 
     def set_position(self, position: int):
         """Sets the device decode position (the new token's cache row)."""
@@ -195,6 +205,13 @@ class DecodeSession:
         self.next_token.  With `advance` the step also stores the argmax as the
         next input token (and in self.history) and moves the position on."""
         c, ctx, d = self.cfg, self.ctx, self.d
+        if self.fused is not None:
+            self.fused.run(self.token, self.pos, self.xa)
+            ctx.rmsnorm(d["xa"], d["xn"], self.g_final, c.eps)
+            ctx.lmhead_argmax(self.lm, d["xn"], None, self.next_token)
+            if advance:
+                ctx.decode_advance(self.pos, self.token, self.next_token, self.history)
+            return
         ctx.embed_q8(self.embed, self.token, self.xa)
         for L in self.layers:
             w = L["w"]

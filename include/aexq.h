@@ -320,6 +320,52 @@ aexq_status aexq_attention_decode_rope_at(aexq_ctx* ctx, const void* q, const vo
 aexq_status aexq_decode_advance(aexq_ctx* ctx, int32_t* position, int32_t* token,
                                 const int32_t* argmax, int32_t* tokens_out, int tokens_cap);
 
+/* ---- the decoder layers of a decode step in one launch -------------------- */
+/* Qwen35DecoderSession.DecodeCore's per-layer chain (DEC:463-585: RMSNorm,
+ * q/k/v, RoPE, K/V append, SDPA, o_proj + residual, RMSNorm, gate/up + SwiGLU,
+ * down + residual; the per-layer dispatch loop LF:996-1136) for every layer of
+ * the model, run as one persistent launch.  Each linear's outputs equal
+ * aexq_linear's at M = 1 bit for bit; attention follows MM:420-544 with its
+ * positions split over workgroups.  The decoder keeps the layers' device
+ * pointers (the weights, norms and caches must outlive it) and its own
+ * exchange buffers: aexq_decoder_run allocates nothing and may be captured
+ * into a HIP graph.  Runs of one decoder must not overlap (one stream). */
+typedef struct aexq_decoder aexq_decoder;
+typedef struct aexq_decoder_layer {
+  const aexq_weight *q_proj, *k_proj, *v_proj, *o_proj, *gate_proj, *up_proj, *down_proj;
+  const float* attn_norm; /* RMSNorm gamma before q/k/v, device fp32 [hidden] */
+  const float* mlp_norm;  /* RMSNorm gamma before gate/up, device fp32 [hidden] */
+  void* k_cache;          /* device fp16 [heads_kv][capacity][head_dim] */
+  void* v_cache;
+} aexq_decoder_layer;
+typedef struct aexq_decoder_config {
+  int heads_q, heads_kv, head_dim, capacity;
+  float rms_eps;
+  float attn_scale;        /* scores = q.k * attn_scale */
+  const float* rope_cos;   /* device fp32 [capacity][head_dim / 2] (DEC:1660-1675 rows) */
+  const float* rope_sin;
+  int workgroups;          /* 0: chosen from the capacity */
+} aexq_decoder_config;
+/* Checks every layer (Q4 with one scale per 32 codes, one scale dtype, the
+ * model's shapes; head_dim 128; the shapes the fused kernel takes) and the
+ * tied Q8 embedding table; AEXQ_ERR_UNSUPPORTED names what it does not take. */
+aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_config* cfg,
+                                const aexq_decoder_layer* layers, int count,
+                                const aexq_weight* embedding, aexq_decoder** out);
+/* One step: the embedding row of *token (device int32), every layer at
+ * position *position (device int32, clamped to the capacity; K/V rows are
+ * appended there), the final hidden state (before the final norm) into
+ * hidden_out (device fp16 [hidden]).  On the context's stream. */
+aexq_status aexq_decoder_run(aexq_decoder* d, const int32_t* token, const int32_t* position,
+                             void* hidden_out);
+/* Synchronizes the stream, returns in *flag whether any run since the last
+ * call gave up a bounded wait (its results are then invalid), and clears it. */
+aexq_status aexq_decoder_error(aexq_decoder* d, int* flag);
+/* Workgroups, attention splits per kv head and positions per split (nullable). */
+aexq_status aexq_decoder_info(const aexq_decoder* d, int* workgroups, int* splits,
+                              int* split_positions);
+void aexq_decoder_release(aexq_decoder* d);
+
 #ifdef __cplusplus
 }
 #endif
