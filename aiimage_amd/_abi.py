@@ -170,6 +170,7 @@ def _declare(L):
         "aexq_linear_group": (i32, [P, i32, PP, TP, ctypes.POINTER(TP), AP]),
         "aexq_lmhead_argmax": (i32, [P, P, TP, TP, P, P]),
         "aexq_lmhead_argmax_noalloc": (i32, [P, P, TP, P, P]),
+        "aexq_lmhead_argmax_ex": (i32, [P, P, TP, TP, AP, P, P]),
         "aexq_argmax": (i32, [P, TP, P, P]),
         "aexq_dequant": (i32, [P, P, P]),
         "aexq_rmsnorm": (i32, [P, TP, TP, P, i32, f32]),

@@ -259,13 +259,22 @@ class Context:
         return buf.value.decode()
 
     def lmhead_argmax(self, w: "QuantWeight", x: _abi.Tensor, logits: Optional[_abi.Tensor],
-                      argmax: torch.Tensor, top2_gap: Optional[torch.Tensor] = None):
+                      argmax: torch.Tensor, top2_gap: Optional[torch.Tensor] = None, *,
+                      rms_gamma: Optional[torch.Tensor] = None, rms_eps: float = 1e-3,
+                      rmsnorm: bool = False):
+        """Greedy token of the LM head; with rmsnorm=True the final RMSNorm
+        (gamma rms_gamma) is applied to x inside the same launch."""
+        gap = ctypes.c_void_p(top2_gap.data_ptr()) if top2_gap is not None else None
+        lg = ctypes.byref(logits) if logits is not None else None
+        if rmsnorm:
+            args = make_args(rms_gamma=rms_gamma, rms_eps=rms_eps, rmsnorm=True)
+            check(self._lib.aexq_lmhead_argmax_ex(
+                self.handle, w.handle, ctypes.byref(x), lg, ctypes.byref(args),
+                ctypes.c_void_p(argmax.data_ptr()), gap), "aexq_lmhead_argmax_ex")
+            return
         check(self._lib.aexq_lmhead_argmax(
-            self.handle, w.handle, ctypes.byref(x),
-            ctypes.byref(logits) if logits is not None else None,
-            ctypes.c_void_p(argmax.data_ptr()),
-            ctypes.c_void_p(top2_gap.data_ptr()) if top2_gap is not None else None),
-            "aexq_lmhead_argmax")
+            self.handle, w.handle, ctypes.byref(x), lg,
+            ctypes.c_void_p(argmax.data_ptr()), gap), "aexq_lmhead_argmax")
 
     def lmhead_argmax_noalloc(self, w: "QuantWeight", x: _abi.Tensor, argmax: torch.Tensor,
                               top2_gap: Optional[torch.Tensor] = None):

@@ -71,6 +71,10 @@ struct aexq_ctx {
   // split-K partial planes of the MFMA kernels
   float* sk_part = nullptr;
   long long sk_cap = 0;
+  // arrival counters of the in-kernel argmax merge (zeroed at allocation;
+  // every launch leaves them zero)
+  int* am_count = nullptr;
+  long long am_count_cap = 0;
   // scratch buffers replaced by larger ones: a HIP graph captured before the
   // growth still holds their addresses, so they live until aexq_destroy
   std::vector<void*> retired;
@@ -103,16 +107,17 @@ static long long round_up(long long v, long long a) { return (v + a - 1) / a * a
 // ---------------------------------------------------------------------------
 // Scratch of aexq_lmhead_argmax_noalloc: the argmax partials of one launch
 // (best value, index, second best; kNoAllocParts entries each, i.e. workgroups
-// x activation rows), in a file-scope device array instead of memory the
-// library allocates.  Each GPU holds its own copy from module load to process
+// x activation rows) and the merge's arrival counters, in a file-scope device
+// array instead of memory the library allocates.  Each GPU holds its own copy from module load to process
 // exit; its address on a device comes from hipGetSymbolAddress, taken once per
 // device when the first context on that device is created.  Every entry the
-// argmax merge reads is written by the same call, so nothing in it has to
-// start at zero; calls that overlap on one GPU (other streams or contexts)
-// share the array and race.
+// argmax merge reads is written by the same call; the counters start at zero
+// (the array is zero-initialised at load) and every call leaves them zero.
+// Calls that overlap on one GPU (other streams or contexts) share the array
+// and race.
 // ---------------------------------------------------------------------------
 constexpr long long kNoAllocParts = 32768;  // 3 x 128 KiB
-static __device__ __align__(256) float scratch[3 * kNoAllocParts];
+static __device__ __align__(256) float scratch[3 * kNoAllocParts + kArgCounterInts];
 constexpr int kMaxDevices = 64;
 static std::mutex g_noalloc_mu;
 static float* g_noalloc_ptr[kMaxDevices];      // device address of `scratch` per device
@@ -196,6 +201,7 @@ extern "C" void aexq_destroy(aexq_ctx* ctx) {
   (void)hipFree(ctx->attn_part);
   (void)hipFree(ctx->attn_count);
   (void)hipFree(ctx->sk_part);
+  (void)hipFree(ctx->am_count);
   for (void* b : ctx->retired) (void)hipFree(b);
   delete ctx;
 }
@@ -1238,9 +1244,8 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     // persistent grid: every wave resident, each owning a contiguous tile range
     // Workgroups queued beyond the resident count stream best: Q4 16 of 4
     // waves per CU (config 2, against 6, 8, 12, 20, 24 and 32), Q8 12 (config
-    // 1, against the resident count, 8 and 16); an argmax launch keeps the
-    // resident count (each workgroup adds a partial to the merge: the LM head
-    // at 16 per CU runs 20% slower)
+    // 1, against the resident count, 8 and 16); argmax launches too, now that
+    // their partials merge in the last workgroup instead of a finalize launch
     int per_cu = qmv_blocks_per_cu(plan->entry);
     const int queued = argmax ? per_cu : (fmt == kQ4 ? 16 : 12);
     if (per_cu < queued) per_cu = queued;
@@ -1438,6 +1443,7 @@ struct Partials {
   float* best = nullptr;
   int* index = nullptr;
   float* second = nullptr;
+  int* count = nullptr;  // the merge's arrival counters (kArgCounterInts)
   long long cap = 0;
 };
 
@@ -1465,15 +1471,28 @@ static aexq_status lmhead_fused_launch(aexq_ctx* ctx, Plan& plan, const char* op
     pt = *fixed;
   } else {
     aexq_status st = ensure_parts(ctx, need, op);
+    if (!st)
+      st = grow_scratch(ctx, (void**)&ctx->am_count, &ctx->am_count_cap,
+                        kArgCounterInts * (long long)sizeof(int), op, "argmax counters", true);
     if (st) return st;
     pt.best = ctx->part_best;
     pt.index = ctx->part_index;
     pt.second = ctx->part_second;
+    pt.count = ctx->am_count;
   }
   plan.p.part_best = pt.best;
   plan.p.part_index = pt.index;
   plan.p.part_second = pt.second;
   plan.p.parts = parts;
+  // M = 1: the last workgroup to finish merges the partials (no finalize
+  // launch).  More rows keep the finalize launch, which merges them all in
+  // one round trip; the in-kernel merge would take one per row.
+  const bool in_kernel = M == 1;
+  if (in_kernel) {
+    plan.p.am_count = pt.count;
+    plan.p.am_out = argmax;
+    plan.p.am_gap = top2_gap;
+  }
   if (plan.fast) {
     hipError_t e = qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, op, "lm head launch");
@@ -1481,22 +1500,23 @@ static aexq_status lmhead_fused_launch(aexq_ctx* ctx, Plan& plan, const char* op
     aexq_status st = launch_plan(ctx, plan, op);
     if (st) return st;
   }
-  ArgmaxParams ap{pt.best, pt.index, pt.second, parts, M, argmax, top2_gap};
-  hipError_t e = argmax_finalize_launch(ap, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
+  if (!in_kernel) {
+    ArgmaxParams ap{pt.best, pt.index, pt.second, parts, M, argmax, top2_gap};
+    hipError_t e = argmax_finalize_launch(ap, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
+  }
   return AEXQ_OK;
 }
 
-extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
-                                          const aexq_tensor* x, const aexq_tensor* logits,
-                                          int32_t* argmax, float* top2_gap) {
-  const char* op = "aexq_lmhead_argmax";
+static aexq_status lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
+                                 const aexq_tensor* logits, const aexq_linear_args* args,
+                                 int32_t* argmax, float* top2_gap, const char* op) {
   if (!argmax) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "argmax is NULL");
   if (w && w->batch != 1) return fail(AEXQ_ERR_UNSUPPORTED, op, "stacked LM head");
   Plan plan;
   const aexq_weight* ws[1] = {w};
   const aexq_tensor* ys[1] = {logits};
-  aexq_status st = make_plan(ctx, 1, ws, x, ys, nullptr, true, &plan);
+  aexq_status st = make_plan(ctx, 1, ws, x, ys, args, true, &plan);
   if (st) return st;
   HIP_TRY(op, hipSetDevice(ctx->device));
   if (lmhead_fused(plan)) return lmhead_fused_launch(ctx, plan, op, argmax, top2_gap, nullptr);
@@ -1520,6 +1540,24 @@ extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
   st = launch_plan(ctx, plan, op);
   if (st) return st;
   return argmax_over_logits(ctx, lg, M, w->n, rstride, argmax, top2_gap, op);
+}
+
+extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
+                                          const aexq_tensor* x, const aexq_tensor* logits,
+                                          int32_t* argmax, float* top2_gap) {
+  return lmhead_argmax(ctx, w, x, logits, nullptr, argmax, top2_gap, "aexq_lmhead_argmax");
+}
+
+extern "C" aexq_status aexq_lmhead_argmax_ex(aexq_ctx* ctx, const aexq_weight* w,
+                                             const aexq_tensor* x, const aexq_tensor* logits,
+                                             const aexq_linear_args* args, int32_t* argmax,
+                                             float* top2_gap) {
+  const char* op = "aexq_lmhead_argmax_ex";
+  if (args && (args->flags & ~(unsigned)AEXQ_EPI_RMSNORM_IN))
+    return fail(AEXQ_ERR_UNSUPPORTED, op,
+                "epilogue flags 0x%x: the LM head takes RMSNorm-in only | rejectedFallback=epilogue",
+                args->flags);
+  return lmhead_argmax(ctx, w, x, logits, args, argmax, top2_gap, op);
 }
 
 extern "C" aexq_status aexq_lmhead_argmax_noalloc(aexq_ctx* ctx, const aexq_weight* w,
@@ -1549,6 +1587,7 @@ extern "C" aexq_status aexq_lmhead_argmax_noalloc(aexq_ctx* ctx, const aexq_weig
   fixed.best = ctx->noalloc;
   fixed.index = (int*)(ctx->noalloc + kNoAllocParts);
   fixed.second = ctx->noalloc + 2 * kNoAllocParts;
+  fixed.count = (int*)(ctx->noalloc + 3 * kNoAllocParts);
   fixed.cap = kNoAllocParts;
   return lmhead_fused_launch(ctx, plan, op, argmax, top2_gap, &fixed);
 }

@@ -146,6 +146,96 @@ __device__ __forceinline__ void argmax_wave_reduce(float& bv, int& bi, float& bs
   }
 }
 
+// One (best, index, second) argmax partial of a workgroup; with the in-kernel
+// merge the stores are agent-coherent (written through to the level every
+// XCD reads), since the merging workgroup may run on another XCD.
+__device__ __forceinline__ void argmax_partial_store(const QmvParams& p, long long o, float v, int i,
+                                                     float s) {
+  if (p.am_count) {
+    __hip_atomic_store(p.part_best + o, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.part_index + o, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.part_second + o, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    p.part_best[o] = v;
+    p.part_index[o] = i;
+    p.part_second[o] = s;
+  }
+}
+
+// In-kernel merge of the argmax partials (p.am_count non-null), called by every
+// thread of every workgroup after its partial stores.  Each workgroup counts
+// in on its group's counter (workgroup b in group b % groups); the last of a
+// group counts in on the top counter, and the last of those merges all
+// partials of every row with the argmax comparator (the first-maximum rule of
+// MM:645-686; the merge order is free) and writes the index and top-2 gap.
+// The last arrivals reset the counters, so the launch replays without
+// clearing.  The merge result equals argmax_finalize_kernel's.
+__device__ __forceinline__ void argmax_tail(const QmvParams& p) {
+  if (!p.am_count) return;
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  __syncthreads();
+  const int parts = p.parts;
+  if (threadIdx.x == 0) {
+    const int groups = parts < kArgGroups ? parts : kArgGroups;
+    const int g = blockIdx.x % groups;
+    const int members = (parts - 1 - g) / groups + 1;
+    int* gc = p.am_count + g * kArgCounterStride;
+    int* top = p.am_count + kArgGroups * kArgCounterStride;
+    int last = 0;
+    if (atomicAdd(gc, 1) == members - 1) {
+      atomicExch(gc, 0);
+      if (atomicAdd(top, 1) == groups - 1) {
+        atomicExch(top, 0);
+        last = 1;
+      }
+    }
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __shared__ float mv[kWaves], ms[kWaves];
+  __shared__ int mi[kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int kBatch = 8;
+  for (int m = 0; m < p.m; ++m) {
+    const long long base = (long long)(p.m_base + m) * parts;
+    float bv = __builtin_nanf("");
+    int bi = 0x7fffffff;
+    float bs = -INFINITY;
+    for (int i0 = threadIdx.x; i0 < parts; i0 += kThreads * kBatch) {
+      float v[kBatch], sv[kBatch];
+      int ix[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int i = i0 + j * kThreads;
+        const bool in = i < parts;
+        v[j] = in ? __hip_atomic_load(p.part_best + base + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                  : __builtin_nanf("");
+        ix[j] = in ? __hip_atomic_load(p.part_index + base + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : 0x7fffffff;
+        sv[j] = in ? __hip_atomic_load(p.part_second + base + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : -INFINITY;
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) argmax_merge(bv, bi, bs, v[j], ix[j], sv[j]);
+    }
+    argmax_wave_reduce(bv, bi, bs);
+    if (lane == 0) {
+      mv[wave] = bv;
+      mi[wave] = bi;
+      ms[wave] = bs;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < kWaves; ++w) argmax_merge(bv, bi, bs, mv[w], mi[w], ms[w]);
+      p.am_out[p.m_base + m] = bi == 0x7fffffff ? 0 : bi;
+      if (p.am_gap) p.am_gap[p.m_base + m] = bs == -INFINITY ? INFINITY : bv - bs;
+    }
+    __syncthreads();
+  }
+}
+
 __device__ __forceinline__ float load_scale(const void* s, long long i, bool f16_scale) {
   return f16_scale ? (float)((const f16*)s)[i] : ((const float*)s)[i];
 }

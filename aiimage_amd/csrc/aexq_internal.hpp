@@ -73,6 +73,12 @@ struct QmvParams {
   int* part_index;
   float* part_second;
   int parts;
+  // in-kernel argmax merge (null: a separate finalize launch merges): arrival
+  // counters (kArgGroups lines, then the top counter; zero before the launch,
+  // left zero after it) and the merged index / top-2 gap per row
+  int* am_count;
+  int32_t* am_out;
+  float* am_gap;
   // split K (MFMA kernels): the K steps of every tile run as sk_chunks chunks
   // of sk_cs steps whose fp32 partials go to plane c of sk_part (plane c at
   // c * sk_plane floats; element (b, row, h, n) of matrix j at sk_off +
@@ -84,6 +90,13 @@ struct QmvParams {
   int sk_chunks;
   int sk_cs;
 };
+
+// Arrival counters of the in-kernel argmax merge: kArgGroups groups of
+// workgroups, each counter on its own 256-byte line (device-scope atomics to
+// one line serialise), then one top counter.
+constexpr int kArgGroups = 64;
+constexpr int kArgCounterStride = 64;  // ints
+constexpr int kArgCounterInts = (kArgGroups + 1) * kArgCounterStride;
 
 struct ArgmaxParams {
   const float* pv;

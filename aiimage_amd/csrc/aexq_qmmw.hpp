@@ -302,10 +302,7 @@ struct QmmW {
       int ix = li[row][0];
 #pragma unroll
       for (int w = 1; w < kWaves; ++w) argmax_merge(v, ix, sv, lv[row][w], li[row][w], ls[row][w]);
-      const long long o = (long long)(p.m_base + row) * p.parts + blockIdx.x;
-      p.part_best[o] = v;
-      p.part_index[o] = ix;
-      p.part_second[o] = sv;
+      argmax_partial_store(p, (long long)(p.m_base + row) * p.parts + blockIdx.x, v, ix, sv);
     }
   }
 
@@ -544,7 +541,10 @@ void qmmw_kernel(const QmvParams p) {
     cu = nx;
     sl ^= 1;
   }
-  if constexpr (ARGMAX) Q::best_write(p, lane, wave, best);
+  if constexpr (ARGMAX) {
+    Q::best_write(p, lane, wave, best);
+    argmax_tail(p);
+  }
 }
 
 }  // namespace aexq

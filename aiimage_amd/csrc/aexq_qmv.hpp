@@ -645,11 +645,9 @@ void qmv_kernel(const QmvParams p) {
       int i = li[m][0];
 #pragma unroll
       for (int w = 1; w < kWaves; ++w) argmax_merge(v, i, s, lv[m][w], li[m][w], ls[m][w]);
-      const long long o = (long long)m * p.parts + blockIdx.x;
-      p.part_best[o] = v;
-      p.part_index[o] = i;
-      p.part_second[o] = s;
+      argmax_partial_store(p, (long long)m * p.parts + blockIdx.x, v, i, s);
     }
+    argmax_tail(p);
   }
 }
 

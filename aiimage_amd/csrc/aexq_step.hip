@@ -38,8 +38,10 @@
 // the next workgroup barrier; they also do the work between a poll and the
 // next linear: RMSNorm-in (bit-exact with the streaming kernel's staged path),
 // RoPE of q and the new k row, and the RMSNorm gammas.  The compute waves load
-// each phase's weights (and the split's cached K/V rows) two or three phases
-// ahead into registers and leave their outputs in LDS; the store wave writes
+// each phase's weights (and the split's cached K/V rows) one to three phases
+// ahead into registers, issuing them at the start of a phase so that the
+// grid-wide burst drains while they compute, before the phase's outputs are
+// handed over, and leave their outputs in LDS; the store wave writes
 // them (and the K/V append) to device memory.  On this part loads and stores
 // share one vector-memory counter, which counts in issue order and, once both
 // kinds are in flight, makes any wait a wait for everything: so the compute
@@ -515,7 +517,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
     qkv_mat(s_layers[l], w1.live ? w1.r0 : 0, w, s, n, lr);
     issue_slot<L1, C1, 1>(wqkv, w, s, nullptr, nullptr, n, lr, ch1, sf16, w1.live, t);
   };
-  auto issue_kv = [&](int l, int t) {
+  auto issue_kv = [&](int l, int t, bool want_k, bool want_v) {
     const long long head_off = (long long)ag * p.cap * kHd;
     const int lim = live_split ? ap0 + sl_len : 0;
     const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
@@ -528,8 +530,10 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
     const int off = pl < sp ? ((ap0 + pl) * kHd + j * 16) * 2 : kNoOff;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      kreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, off + 16 * i, 0, kStreamAux));
-      vreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, off + 16 * i, 0, kStreamAux));
+      if (want_k)
+        kreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, off + 16 * i, 0, kStreamAux));
+      if (want_v)
+        vreg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, off + 16 * i, 0, kStreamAux));
     }
   };
   auto issue_o = [&](int l, int t) {
@@ -571,7 +575,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
     {
       const int t = opaque_tid();
       issue_qkv(0, t);
-      issue_kv(0, t);
+      issue_kv(0, t, true, true);
     }
     __syncthreads();
     for (int l = 0; l < nl; ++l) {
@@ -580,6 +584,8 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       // ---------------- P1: q/k/v
       {
         const int t = opaque_tid(), lane = t & 63;
+        issue_o(l, t);
+        issue_d(l, t);
         if (w1.live) {
           const uint32_t* w; const void* s; int n, lr;
           qkv_mat(L, w1.r0, w, s, n, lr);
@@ -589,12 +595,12 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
             s_out[w1.r0 + lane / L1 - b * p.rows_qkv] = tag_f16((f16)v, tg);
         }
         cw_signal(&s_done, lane);
-        issue_o(l, t);
       }
       __syncthreads();
       // ---------------- P2: attention splits
       {
         const int t = opaque_tid(), lane = t & 63, wave = t >> 6;
+        issue_gu(l, t);
         if (attn_wg) {
           const int pl = t >> 3, j = t & 7;  // position pl of the split, dims 16 j .. 16 j + 15
           if (live_split && wave < kAW) {
@@ -673,13 +679,12 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
           }
         }
         cw_signal(&s_done, lane);
-        issue_gu(l, t);
-        issue_d(l, t);
       }
       __syncthreads();
       // ---------------- P3: o_proj + residual
       {
         const int t = opaque_tid(), lane = t & 63;
+        if (l + 1 < nl) issue_qkv(l + 1, t);
         if (w3.live) {
           const int row = w3.r0 + lane / L2;
           float v = 0.0f + row_dot<L2, C2>(wo.w[0], wo.s[0], s_at, ch2, row, sf16, t);
@@ -687,12 +692,12 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
           if (lane % L2 == 0 && row < hid) s_out[row - b * p.rows_hid] = tag_f16((f16)v, tg + 3);
         }
         cw_signal(&s_done, lane);
-        if (l + 1 < nl) issue_qkv(l + 1, t);
       }
       __syncthreads();
       // ---------------- P4: gate/up + SwiGLU-out
       {
         const int t = opaque_tid(), lane = t & 63;
+        if (l + 1 < nl) issue_kv(l + 1, t, true, false);
         if (w4.live) {
           const int row = w4.r0 + lane / L1;
           const float g = 0.0f + row_dot<L1, C1>(wgu.w[0], wgu.s[0], s_xn, ch1, row, sf16, t);
@@ -702,12 +707,12 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
             s_out[row - b * p.rows_inter] = tag_f16((f16)v, tg + 4);
         }
         cw_signal(&s_done, lane);
-        if (l + 1 < nl) issue_kv(l + 1, t);
       }
       __syncthreads();
       // ---------------- P5: down + residual
       {
         const int t = opaque_tid(), lane = t & 63;
+        if (l + 1 < nl) issue_kv(l + 1, t, false, true);
         if (w5.live) {
           const int row = w5.r0 + lane / L3;
           float v = 0.0f + row_dot<L3, C3>(wd.w[0], wd.s[0], s_h, ch3, row, sf16, t);

@@ -3,8 +3,9 @@
 Mirrors the per-token work of Qwen35DecoderSession (paths relative to the
 reference root, DEC = Packages/com.aexis/Samples/AIImageApplicationExample/
 Runtime/Scripts/Qwen35DecoderSession.cs): EmbedTokens (DEC:402-428) from the
-tied Q8 table, the decoder layers (DecodeCore, DEC:463-585), the final norm,
-and SelectNextToken's LM head + greedy argmax (DEC:734-809).  Each layer:
+tied Q8 table, the decoder layers (DecodeCore, DEC:463-585), and the final
+norm fused into SelectNextToken's LM head + greedy argmax (DEC:734-809).  Each
+layer:
 
     x  -> RMSNorm-in + q/k/v (one grouped launch)
        -> RoPE on q, k; k/v appended to the fp16 cache; GQA decode attention
@@ -168,7 +169,7 @@ class DecodeSession:
         # the decode position (device), and the token generated at each position
         self.pos = torch.zeros(1, dtype=torch.int32, device=device)
         self.history = torch.full((c.capacity,), -1, dtype=torch.int32, device=device)
-        self.xa, self.xb, self.xn = z(c.hidden), z(c.hidden), z(c.hidden)
+        self.xa, self.xb = z(c.hidden), z(c.hidden)
         self.q, self.k, self.v = z(c.q_width), z(c.kv_width), z(c.kv_width)
         self.attn = z(c.q_width)
         self.h = z(c.intermediate)
@@ -178,7 +179,6 @@ class DecodeSession:
         d = aexq.describe
         self.d = {
             "xa": d(self.xa, 1, c.hidden, P4), "xb": d(self.xb, 1, c.hidden, P4),
-            "xn": d(self.xn, 1, c.hidden, P4),
             "q": d(self.q, 1, c.q_width, P4), "k": d(self.k, 1, c.kv_width, P4),
             "v": d(self.v, 1, c.kv_width, P4), "attn": d(self.attn, 1, c.q_width, P4),
             "h": d(self.h, 1, c.intermediate, P4),
@@ -207,8 +207,8 @@ class DecodeSession:
         c, ctx, d = self.cfg, self.ctx, self.d
         if self.fused is not None:
             self.fused.run(self.token, self.pos, self.xa)
-            ctx.rmsnorm(d["xa"], d["xn"], self.g_final, c.eps)
-            ctx.lmhead_argmax(self.lm, d["xn"], None, self.next_token)
+            ctx.lmhead_argmax(self.lm, d["xa"], None, self.next_token, rmsnorm=True,
+                              rms_gamma=self.g_final, rms_eps=c.eps)
             if advance:
                 ctx.decode_advance(self.pos, self.token, self.next_token, self.history)
             return
@@ -225,8 +225,8 @@ class DecodeSession:
             ctx.linear(w["gate_proj"], d["xb"], d["h"], rmsnorm=True, rms_gamma=L["g_mlp"],
                        rms_eps=c.eps, up=w["up_proj"])
             ctx.linear(w["down_proj"], d["h"], d["xa"], residual=d["xb"])
-        ctx.rmsnorm(d["xa"], d["xn"], self.g_final, c.eps)
-        ctx.lmhead_argmax(self.lm, d["xn"], None, self.next_token)
+        ctx.lmhead_argmax(self.lm, d["xa"], None, self.next_token, rmsnorm=True,
+                          rms_gamma=self.g_final, rms_eps=c.eps)
         if advance:
             ctx.decode_advance(self.pos, self.token, self.next_token, self.history)
 

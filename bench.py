@@ -196,7 +196,10 @@ def extras(torch, aexq, synth, ctx):
         b = n * k + n * 2 + m * k * 2 + m * n * 4
         out[f"config5_lmhead_m{m}"] = {"bytes": b, "ms_per_call": avg,
                                        "GBps": b / (avg * 1e-3) / 1e9,
-                                       "note": "matvec+argmax partials and the finalize launch"}
+                                       "note": ("one launch: matvec, logits and argmax, the "
+                                                "partials merged by the last workgroup" if m == 1
+                                                else "matvec with argmax partials, then the "
+                                                "finalize launch")}
     for h in heads:
         h.release()
     return out
@@ -340,74 +343,89 @@ def config4_single(torch, aexq, synth, ctx, copies: int = 24):
 
 def config3(torch, aexq, ctx, steps: int = 30):
     """Benchmark config 3: one full synthetic Qwen3.5-0.8B-shaped decode step
-    (24 layers, 2048 cached positions, Q8 LM head with argmax), eager and as a
-    replayed HIP graph; tokens/s against the step's algorithmic bytes."""
+    (24 layers, 2048 cached positions, Q8 LM head with argmax); tokens/s
+    against the step's algorithmic bytes.  Two forms of the step: the fused
+    one (every decoder layer in one persistent launch, aexq_decoder_run) and
+    the per-operator one (five launches per layer); each eager, as a replayed
+    HIP graph, and as the Generate loop (one graph per token that feeds the
+    argmax back and advances the device position)."""
     from aiimage_amd import decoder
     cfg = decoder.ModelConfig()
     t0 = time.time()
-    sess = decoder.DecodeSession(ctx, cfg)
-    log(f"config3 model built in {time.time() - t0:.1f} s")
-    sess.token.fill_(1)
-    sess.set_position(cfg.capacity - 1)     # attends over all 2048 positions
-    for _ in range(2):
-        sess.step()
-    torch.cuda.synchronize()
+    sess = decoder.DecodeSession(ctx, cfg, fused=True)
+    log(f"config3 model built in {time.time() - t0:.1f} s ({sess.fused.info()})")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        sess.step()
-    e1.record()
-    torch.cuda.synchronize()
-    eager_ms = e0.elapsed_time(e1) / steps
-    g = sess.capture()
-    for _ in range(3):
-        g.replay()
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(steps):
-        g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    graph_ms = e0.elapsed_time(e1) / steps
-    # the Generate loop: one graph that ends by feeding the argmax back and
-    # advancing the device position, replayed once per token over the last
-    # `steps` positions of the cache
-    ga = sess.capture(advance=True)
-    start = cfg.capacity - steps
-    sess.generate(1, start - 3, 3, graph=ga)          # warm replays
-    sess.token.fill_(1)
-    sess.set_position(start)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(steps):
-        ga.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    gen_ms = e0.elapsed_time(e1) / steps
-    assert int(sess.pos.item()) == cfg.capacity
+
+    def timed(fn):
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    def measure():
+        sess.token.fill_(1)
+        sess.set_position(cfg.capacity - 1)     # attends over all 2048 positions
+        for _ in range(2):
+            sess.step()
+        torch.cuda.synchronize()
+        eager_ms = timed(sess.step)
+        g = sess.capture()
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        graph_ms = timed(g.replay)
+        ga = sess.capture(advance=True)
+        start = cfg.capacity - steps
+        sess.generate(1, start - 3, 3, graph=ga)          # warm replays
+        sess.token.fill_(1)
+        sess.set_position(start)
+        torch.cuda.synchronize()
+        gen_ms = timed(ga.replay)
+        assert int(sess.pos.item()) == cfg.capacity
+        del g, ga
+        return eager_ms, graph_ms, gen_ms, start
+
+    eager_ms, graph_ms, gen_ms, start = measure()
+    err = sess.fused.error()
+    assert err == 0, "the fused step gave up a bounded wait"
+    keep, sess.fused = sess.fused, None
+    p_eager, p_graph, p_gen, _ = measure()
+    sess.fused = keep
     b = cfg.bytes_per_token(cfg.capacity)
     roof = HBM_PEAK_GBS * 1e9 / b["total"]
     # BASELINE.json's "8 kv heads" reading: twice the cached K/V bytes
     roof8 = HBM_PEAK_GBS * 1e9 / (b["total"] + b["kv_read"])
     mean_len = start + (steps + 1) / 2.0
     b_gen = cfg.bytes_per_token(int(round(mean_len)))["total"]
+    tps = lambda ms: round(1000.0 / ms, 1)
     out = {"config3_decode": {
-        "tokens_per_s_graph": round(1000.0 / graph_ms, 1), "ms_per_token_graph": round(graph_ms, 4),
-        "tokens_per_s_eager": round(1000.0 / eager_ms, 1), "ms_per_token_eager": round(eager_ms, 4),
-        "tokens_per_s_generate": round(1000.0 / gen_ms, 1),
-        "ms_per_token_generate": round(gen_ms, 4),
+        "step": "fused decoder layers (one launch) + LM head with the final RMSNorm and argmax",
+        "tokens_per_s_graph": tps(graph_ms), "ms_per_token_graph": round(graph_ms, 4),
+        "tokens_per_s_eager": tps(eager_ms), "ms_per_token_eager": round(eager_ms, 4),
+        "tokens_per_s_generate": tps(gen_ms), "ms_per_token_generate": round(gen_ms, 4),
         "generate_positions": [start, cfg.capacity - 1],
         "generate_frac_of_roofline": round(b_gen / (gen_ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
         "bytes_per_token": b, "roofline_tokens_per_s": round(roof, 1),
         "roofline_tokens_per_s_8kv_heads": round(roof8, 1),
         "frac_of_roofline": round(1000.0 / graph_ms / roof, 4),
+        "frac_of_roofline_8kv_heads": round(1000.0 / graph_ms / roof8, 4),
         "GBps_graph": round(b["total"] / (graph_ms * 1e-3) / 1e9, 1),
         "kv_heads": cfg.heads_kv, "positions": cfg.capacity, "layers": cfg.layers,
-        # embedding; per layer q/k/v, attention, o_proj, gate/up, down; final
-        # norm, LM head and argmax finalize (+ the advance in the Generate loop)
-        "launches_per_token": 1 + cfg.layers * 5 + 3}}
+        "fused_grid": sess.fused.info(),
+        # the fused layers and the LM head (RMSNorm-in, in-kernel argmax merge);
+        # the Generate loop adds the advance
+        "launches_per_token": 2,
+        "per_operator": {
+            "tokens_per_s_graph": tps(p_graph), "ms_per_token_graph": round(p_graph, 4),
+            "tokens_per_s_eager": tps(p_eager), "ms_per_token_eager": round(p_eager, 4),
+            "tokens_per_s_generate": tps(p_gen), "ms_per_token_generate": round(p_gen, 4),
+            # embedding; per layer q/k/v, attention, o_proj, gate/up, down;
+            # the LM head
+            "launches_per_token": 1 + cfg.layers * 5 + 1}}}
     log(f"config3: {out['config3_decode']}")
-    del g, ga, sess
+    del sess
     torch.cuda.empty_cache()
     return out
 

@@ -229,6 +229,14 @@ aexq_status aexq_linear_group(aexq_ctx* ctx, int count, const aexq_weight* const
 aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
                                const aexq_tensor* logits, int32_t* argmax, float* top2_gap);
 
+/* aexq_lmhead_argmax with the final RMSNorm of the decoder (the norm layer the
+ * reference's graph runs before the LM head, CC:4531-4557) fused as the
+ * RMSNorm-in epilogue: args->flags may hold AEXQ_EPI_RMSNORM_IN only (with
+ * rms_gamma / rms_eps), plus alpha, beta and C as for aexq_linear; args NULL
+ * is aexq_lmhead_argmax. */
+aexq_status aexq_lmhead_argmax_ex(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
+                                  const aexq_tensor* logits, const aexq_linear_args* args,
+                                  int32_t* argmax, float* top2_gap);
 /* aexq_lmhead_argmax without logits for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  No counterpart in the reference: it exists for those

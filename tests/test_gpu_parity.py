@@ -4,6 +4,7 @@ Bars (from the benchmark definition): dequantized weights bit-exact with the
 reference unpack; outputs within max|y - r| / max|r| <= 1e-3 of the float64
 oracle; greedy argmax equal except where the oracle's top-2 gap < 1e-3.
 """
+import ctypes
 import sys
 
 import numpy as np
@@ -403,6 +404,56 @@ def test_lmhead_argmax_full_vocab(ctx, aexq, orc, m):
     ctx.lmhead_argmax(w, aexq.describe(dev(x16), m, k), None, am2)
     torch.cuda.synchronize()
     assert np.array_equal(am2.cpu().numpy(), gi)
+
+
+@pytest.mark.parametrize("m,n", [(1, 151936), (4, 30011)])
+def test_lmhead_argmax_rmsnorm_in(ctx, aexq, orc, m, n):
+    """aexq_lmhead_argmax_ex: the final RMSNorm fused into the LM head launch.
+    Logits and indices against the oracle of rmsnorm -> fp16 -> Q8 matvec, and
+    the indices equal to those of the unfused rmsnorm + LM head; epilogues other
+    than RMSNorm-in are refused."""
+    _announce(f"lm head rmsnorm-in m={m} n={n}")
+    from aiimage_amd import synth
+    k, eps = synth.HIDDEN, 1e-6
+    words, scales, _ = synth.q8_weights(n, k, 0xAE0C0F31 + m)
+    w = ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
+    x16 = synth.activations(m, k, 0xAE0C0F32 + m)
+    gamma = synth.rms_gamma(k, 0xAE0C0F33)
+    gd, xdev = dev(gamma), dev(x16)
+    xd = aexq.describe(xdev, m, k)
+    layout = aexq.LAYOUT_PACK4_LINEAR
+    logits = aexq.new_activation(m, n, torch.float32, layout)
+    am = torch.full((m,), -1, dtype=torch.int32, device="cuda")
+    gap = torch.zeros(m, dtype=torch.float32, device="cuda")
+    ctx.lmhead_argmax(w, xd, aexq.describe(logits, m, n, layout), am, gap,
+                      rmsnorm=True, rms_gamma=gd, rms_eps=eps)
+    torch.cuda.synchronize()
+    xn = orc.rmsnorm(x16.astype(np.float32), eps, gamma).astype(np.float16).astype(np.float32)
+    ref = orc.gemm_gpu_semantics(xn, orc.dequant_q8(words, scales, n, k,
+                                                    scale_dtype=orc.SCALE_F16))
+    stride = aexq.storage_elements(layout, m, n)
+    assert normwise(logits.cpu().numpy().reshape(m, stride)[:, :n], ref) <= 1e-3
+    ref_idx = orc.argmax_rows(ref.astype(np.float32))
+    srt = np.sort(ref, axis=1)
+    ref_gap = srt[:, -1] - srt[:, -2]
+    gi = am.cpu().numpy()
+    for r in range(m):
+        if ref_gap[r] >= ARGMAX_TIE:
+            assert gi[r] == ref_idx[r], (r, gi[r], ref_idx[r])
+    # the unfused form: aexq_rmsnorm into fp16, then the plain LM head
+    xn_dev = torch.zeros(m * k, dtype=torch.float16, device="cuda")
+    ctx.rmsnorm(xd, aexq.describe(xn_dev, m, k), gd, eps)
+    am2 = torch.full((m,), -1, dtype=torch.int32, device="cuda")
+    ctx.lmhead_argmax(w, aexq.describe(xn_dev, m, k), None, am2)
+    torch.cuda.synchronize()
+    for r in range(m):
+        if ref_gap[r] >= ARGMAX_TIE:
+            assert int(am2[r]) == gi[r], r
+    with pytest.raises(aexq.NotSupportedError):
+        args = aexq.make_args(rms_gamma=gd, rms_eps=eps, rmsnorm=True, residual=xd)
+        aexq.check(ctx._lib.aexq_lmhead_argmax_ex(
+            ctx.handle, w.handle, ctypes.byref(xd), None, ctypes.byref(args),
+            ctypes.c_void_p(am.data_ptr()), None), "aexq_lmhead_argmax_ex")
 
 
 @pytest.mark.parametrize("bits,m,n", [(8, 20, 50000), (8, 40, 30011), (4, 8, 40000), (4, 24, 20000)])
