@@ -921,6 +921,11 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   }
   if (argmax && (swiglu || (a.flags & AEXQ_EPI_RESIDUAL_ADD)))
     return fail(AEXQ_ERR_UNSUPPORTED, op, "LM head takes no SwiGLU/residual epilogue");
+  // one argmax per activation row: the partials carry no batch index
+  if (argmax && w0->batch != 1)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "LM head over a batched weight (batch=%d)", w0->batch);
+  if (argmax && a.c)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "LM head with a C (bias) term | rejectedFallback=bias");
 
   TensorView xv;
   aexq_status st = view_tensor(x, op, "x", &xv);
@@ -1244,15 +1249,25 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     // persistent grid: every wave resident, each owning a contiguous tile range
     // Workgroups queued beyond the resident count stream best: Q4 16 of 4
     // waves per CU (config 2, against 6, 8, 12, 20, 24 and 32), Q8 12 (config
-    // 1, against the resident count, 8 and 16); argmax launches too, now that
-    // their partials merge in the last workgroup instead of a finalize launch
+    // 1, against the resident count, 8 and 16).  Argmax launches stay at the
+    // resident count: every workgroup ends in a partial store and an arrival
+    // count, which queued workgroups would pay many times over.
     int per_cu = qmv_blocks_per_cu(plan->entry);
-    const int queued = argmax ? per_cu : (fmt == kQ4 ? 16 : 12);
+    const bool fused_argmax = plan->entry->cfg.argmax;
+    const int queued = fused_argmax ? per_cu : (fmt == kQ4 ? 16 : 12);
     if (per_cu < queued) per_cu = queued;
     const char* env = getenv("AEXQ_QMV_BLOCKS_PER_CU");
     if (env && atoi(env) > 0) per_cu = atoi(env);
     const long long need = ((long long)tiles_total + kWaves - 1) / kWaves;
-    const long long cap = (long long)per_cu * ctx->cus;
+    long long cap = (long long)per_cu * ctx->cus;
+    if (fused_argmax) {
+      // every workgroup's logits fit its LDS buffer: at most kArgLogitsMax
+      // (rows x M) per workgroup
+      const long long per_tile = (long long)plan->entry->rw * plan->entry->cfg.mmax;
+      const long long tiles_max = kArgLogitsMax / per_tile;
+      const long long g = (tiles_total + tiles_max - 1) / tiles_max;
+      if (g > cap) cap = g;
+    }
     plan->grid = (int)(need < cap ? need : cap);
     if (plan->grid < 1) plan->grid = 1;
   } else {

@@ -278,6 +278,12 @@ __device__ __forceinline__ long long out_index(const QmvParams& p, const QmvMat&
   return (((long long)(head >> 2) * p.y_rows + p.m_base + row) * mt.y_hd + d) * 4 + (head & 3);
 }
 
+// The LM head's epilogue: gemm_epilogue without a C term (the argmax
+// launches take none), the same arithmetic.
+__device__ __forceinline__ float argmax_epilogue(const QmvParams& p, float v) {
+  return (p.flags & kFlagAlphaIn) ? p.alpha * (0.0f + v) : 0.0f + p.alpha * v;
+}
+
 // Bias, alpha and beta as the reference Gemm resolves them (MM:688-705, 812-820):
 // Pack4-linear output is alpha*(beta*C + sum), tiled output beta*C + alpha*sum.
 __device__ __forceinline__ float gemm_epilogue(const QmvParams& p, int m, int r, float v) {

@@ -9,6 +9,9 @@ namespace aexq {
 constexpr int kMaxGroup = 8;  // matrices per grouped launch
 constexpr int kWaves = 4;     // waves per workgroup of the matvec kernels
 constexpr int kThreads = 64 * kWaves;
+// logits (rows x M) one workgroup of the streaming LM head holds in LDS until
+// its tile loop ends; the host sizes the grid so that no workgroup has more
+constexpr int kArgLogitsMax = 2048;
 
 enum Fmt : int { kQ8 = 0, kQ4 = 1 };
 

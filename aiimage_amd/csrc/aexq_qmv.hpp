@@ -49,7 +49,11 @@ struct Qmv {
 
   typedef uint32_t XRegs[MMAX][CPL][XW];
 
+  // The LM head (ARGMAX) is one matrix of one batch entry (host-checked): its
+  // cursor is the row tile alone, which keeps the tile loop's bookkeeping in
+  // plain scalar arithmetic.
   static __device__ __forceinline__ Cursor locate(const QmvParams& p, int t) {
+    if constexpr (ARGMAX) return Cursor{0, 0, t};
     int j = 0;
     for (int i = 1; i < p.nmat; ++i)
       if (t >= p.mat[i].tile_base) j = i;
@@ -62,6 +66,7 @@ struct Qmv {
   }
 
   static __device__ __forceinline__ Cursor advance(const QmvParams& p, Cursor c) {
+    if constexpr (ARGMAX) return Cursor{0, 0, c.rt + 1};
     if (++c.rt == p.mat[c.j].tiles) {
       c.rt = 0;
       if (++c.b == p.batch) {
@@ -147,7 +152,7 @@ struct Qmv {
     const int rows = live && mt.n > r0 ? mt.n - r0 : 0;
     const int sper = FMT == kQ8 ? 1 : p.groups_per_row;
     const int sbytes = live ? (mt.n * sper * sb + 3) & ~3 : 0;
-    if constexpr (MMAX == 1) {
+    if constexpr (MMAX == 1 && !ARGMAX) {
       // fp16 residual rows of the tile, loaded with it (an empty resource
       // without one); fp32 outputs read theirs in the epilogue
       const bool res = mt.res && (p.flags & kFlagResidual) && !(p.flags & kFlagYf32);
@@ -407,8 +412,8 @@ struct Qmv {
   static __device__ __forceinline__ void compute(const QmvParams& p, const Cursor& cu,
                                                  const Offsets& o, const Buf& buf,
                                                  const XRegs& xr, int sub, int slot, float (&bv)[MMAX],
-                                                 int (&bi)[MMAX],
-                                                 float (&bs)[MMAX]) {
+                                                 int (&bi)[MMAX], float (&bs)[MMAX],
+                                                 float* lg = nullptr, int lg_r0 = 0) {
     const QmvMat& mt = p.mat[cu.j];
     const bool scl16 = (p.flags & kFlagScaleF16) != 0;
     const int toff = scale_tile_offset(p, cu);
@@ -501,6 +506,17 @@ struct Qmv {
       for (int m = 0; m < MMAX; ++m) {
         float v = 0.0f;
         const bool live = r < mt.n && m < p.m;
+        if constexpr (ARGMAX) {
+          // no C and no residual (host-checked); the logits wait in LDS until
+          // the tile loop ends, so the loop issues loads only
+          if (live) v = argmax_epilogue(p, acc[0][u][m]);
+          const int li = (r - lg_r0) * MMAX + m;
+          if (sub == ((u * MMAX + m) & (LPR - 1)) && r < mt.n_store && m < p.m &&
+              li < kArgLogitsMax)
+            lg[li] = v;
+          if (sub == 0 && live) argmax_merge(bv[m], bi[m], bs[m], v, r, -INFINITY);
+          continue;
+        }
         if (live) {
           v = gemm_epilogue(p, m, r, acc[0][u][m]);
           if constexpr (PAIR) v = silu(v) * gemm_epilogue(p, m, r, acc[1][u][m]);
@@ -520,9 +536,6 @@ struct Qmv {
             ((float*)yb)[yi] = v;
           else
             ((f16*)yb)[yi] = (f16)v;
-        }
-        if constexpr (ARGMAX) {
-          if (sub == 0 && live) argmax_merge(bv[m], bi[m], bs[m], v, r, -INFINITY);
         }
       }
     }
@@ -561,6 +574,12 @@ void qmv_kernel(const QmvParams p) {
 
   // a wave without tiles (t0 == t1) still takes part in the staging barrier
   const bool has_tiles = t0 < t1;
+  // the LM head's logits of this workgroup's rows (its waves' tile ranges are
+  // contiguous), stored after the tile loop
+  __shared__ float s_lg[ARGMAX ? kArgLogitsMax : 1];
+  const int lg_t0 = (int)((long long)blockIdx.x * kWaves * p.total_tiles / nw);
+  const int lg_r0 = lg_t0 * Q::RW;
+  float* const lg = ARGMAX ? s_lg : nullptr;
   const typename Q::Offsets o = Q::offsets(p, sub, slot);
   typename Q::Cursor cu = Q::locate(p, has_tiles ? t0 : 0);
   typename Q::Buf A, B;
@@ -584,42 +603,43 @@ void qmv_kernel(const QmvParams p) {
   }
 
   if (has_tiles) {
-    int t = t0;
-    while (true) {
-      // Tile t is in A and its activation rows in xr.  Tile t+1's loads are
-      // issued into B (after the last tile: the same loads against empty
-      // resources), then A is consumed while B is in flight.  Activation rows
-      // change only between batch entries of a batched x (a cold path).
-      bool more = t + 1 < t1;
-      typename Q::Cursor nx = more ? Q::advance(p, cu) : cu;
-      Q::load(p, nx, o, B, more, slot);
-      Q::compute(p, cu, o, A, xr, sub, slot, bv, bi, bs);
-      if (!more) break;
-      ++t;
-      cu = nx;
-      {
+    // Tiles alternate between two register sets: while one is consumed, the
+    // next tile's loads are in flight in the other.  The loop takes tiles in
+    // pairs and leaves only at its head, and an odd last tile is consumed
+    // after it: with no exit between the halves, the wait counts the
+    // compiler places at the loop head see just the loads of the tile in A
+    // (an exit path joining the back edge would add B's loads, pending, and
+    // turn the head's register reuse into a wait for the whole prefetch).
+    // Activation rows change only between batch entries of a batched x (a
+    // cold path).
+    auto next_x = [&]() {
+      if constexpr (!ARGMAX) {
         const f16* xp = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
         if (__builtin_expect(xp != xcur, 0)) {
           Q::load_x(p, xp, sub, xr);
           xcur = xp;
         }
       }
-      // tile t is in B; tile t+1 goes into A
-      more = t + 1 < t1;
+    };
+    int t = t0;
+    while (t + 1 < t1) {
+      // tile t is in A; tile t+1's loads go into B
+      typename Q::Cursor nx = Q::advance(p, cu);
+      Q::load(p, nx, o, B, true, slot);
+      Q::compute(p, cu, o, A, xr, sub, slot, bv, bi, bs, lg, lg_r0);
+      cu = nx;
+      next_x();
+      // tile t+1 is in B; tile t+2's loads (against empty resources past the
+      // last tile) go into A
+      const bool more = t + 2 < t1;
       nx = more ? Q::advance(p, cu) : cu;
       Q::load(p, nx, o, A, more, slot);
-      Q::compute(p, cu, o, B, xr, sub, slot, bv, bi, bs);
-      if (!more) break;
-      ++t;
+      Q::compute(p, cu, o, B, xr, sub, slot, bv, bi, bs, lg, lg_r0);
       cu = nx;
-      {
-        const f16* xp = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
-        if (__builtin_expect(xp != xcur, 0)) {
-          Q::load_x(p, xp, sub, xr);
-          xcur = xp;
-        }
-      }
+      next_x();
+      t += 2;
     }
+    if (t < t1) Q::compute(p, cu, o, A, xr, sub, slot, bv, bi, bs, lg, lg_r0);
   }
 
   if constexpr (ARGMAX) {
@@ -639,6 +659,25 @@ void qmv_kernel(const QmvParams p) {
       }
     }
     __syncthreads();
+    {
+      const QmvMat& mt = p.mat[0];
+      const int lg_t1 = (int)((long long)(blockIdx.x + 1) * kWaves * p.total_tiles / nw);
+      const int rows_x_m = (lg_t1 - lg_t0) * Q::RW * MMAX;
+      const int cnt = rows_x_m < kArgLogitsMax ? rows_x_m : kArgLogitsMax;
+      if (mt.y) {
+        const bool yf32 = (p.flags & kFlagYf32) != 0;
+        for (int i = threadIdx.x; i < cnt; i += kThreads) {
+          const int r = lg_r0 + i / MMAX, m = i % MMAX;
+          if (r < mt.n_store && m < p.m) {
+            const long long yi = out_index(p, mt, m, r);
+            if (yf32)
+              ((float*)mt.y)[yi] = s_lg[i];
+            else
+              ((f16*)mt.y)[yi] = (f16)s_lg[i];
+          }
+        }
+      }
+    }
     if (threadIdx.x < MMAX && (int)threadIdx.x < p.m) {
       const int m = threadIdx.x;
       float v = lv[m][0], s = ls[m][0];
