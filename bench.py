@@ -150,6 +150,57 @@ def time_launches(torch, fn, reps: int):
     return sum(ts) / len(ts), ts[len(ts) // 2]
 
 
+def per_call_cold(torch, aexq, synth, ctx, calls: int = 20):
+    """BASELINE's per-call figure: before each timed call a 512 MiB scratch
+    buffer is written (past the 256 MB Infinity Cache and every L2), then the
+    call alone is bracketed by events.  Config 1 (one Q8 matvec) and config 2
+    (one layer: its four launches, and each launch alone); medians."""
+    scratch = torch.empty(128 << 20, dtype=torch.float32, device="cuda")   # 512 MiB
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(calls)]
+
+    def cold(fn):
+        for i, (a, b) in enumerate(evs):
+            scratch.fill_(float(i))
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        ts = sorted(a.elapsed_time(b) for a, b in evs)
+        return ts[len(ts) // 2]
+
+    out = {}
+    n, k = 3584, 1024
+    words, scales, _ = synth.q8_weights(n, k, synth.SEED_BASE + 1)
+    w = ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
+    x = torch.as_tensor(synth.activations(1, k, 7)).cuda().reshape(-1)
+    y = torch.zeros(n, dtype=torch.float16, device="cuda")
+    xd, yd = aexq.describe(x, 1, k), aexq.describe(y, 1, n, aexq.LAYOUT_PACK4_LINEAR)
+    for _ in range(3):
+        ctx.linear(w, xd, yd)
+    ms = cold(lambda: ctx.linear(w, xd, yd))
+    b1 = n * k + n * 2 + k * 2 + n * 2
+    out["config1_q8_m1_per_call"] = {"us": round(ms * 1e3, 2), "bytes": b1,
+                                     "GBps": round(b1 / (ms * 1e-3) / 1e9, 1)}
+    w.release()
+    layer = Layer(ctx, aexq, synth, torch, 1, synth.SEED_BASE + 2)
+    for _ in range(3):
+        layer.step()
+    ms = cold(layer.step)
+    lb = sum(layer.launch_bytes(i) for i in range(4))
+    per = {}
+    for i, name in enumerate(("qkv_rms", "gate_up_swiglu_rms", "o_proj", "down_proj")):
+        t = cold(lambda i=i: layer.launch(i))
+        per[name] = {"us": round(t * 1e3, 2), "GBps": round(layer.launch_bytes(i) / (t * 1e-3) / 1e9, 1)}
+    out["config2_layer_per_call"] = {"us": round(ms * 1e3, 2), "bytes": lb,
+                                     "GBps": round(lb / (ms * 1e-3) / 1e9, 1), "launches": per,
+                                     "note": "four dependent launches; each pays launch latency "
+                                             "and a cold HBM round trip"}
+    del scratch, layer
+    torch.cuda.empty_cache()
+    return out
+
+
 def extras(torch, aexq, synth, ctx):
     """Per-config kernel measurements (sustained cold via rotating copies)."""
     out = {}
@@ -207,10 +258,9 @@ def extras(torch, aexq, synth, ctx):
 
 def config4(torch, aexq, synth, ctx, copies: int = 120):
     """Benchmark config 4: the layer's linears at M in {16, 64, 512} rows, Q4 and Q8,
-    on the MFMA path.  Every copy reads the same activation rows (x stays in L2)
-    and writes the same outputs (identical replicas), so the stream is the
-    weights plus each copy's algorithmic activation/output bytes; 120 copies
-    (1.1 GB of Q4 weights) per step keep the weights cold."""
+    on the MFMA path.  Each of the 120 copies (1.1 GB of Q4 weights) has its own
+    activation rows and outputs, so every byte counted (weights, scales, x in,
+    y out) streams from or to HBM once per step."""
     out = {}
     P4 = aexq.LAYOUT_PACK4_LINEAR
     for bits in (4, 8):
@@ -227,14 +277,17 @@ def config4(torch, aexq, synth, ctx, copies: int = 120):
             base.release()
         wbytes = 9_142_272 if bits == 4 else 16_277_504
         for m in (16, 64, 512):
-            xs = {k: torch.as_tensor(synth.activations(m, k, 800 + k)).cuda() for k in (1024, 2048, 3584)}
+            # one copy of each activation per weight copy (the same values)
+            xs = {k: torch.as_tensor(synth.activations(m, k, 800 + k)).cuda().reshape(1, -1)
+                  .repeat(copies, 1).reshape(-1) for k in (1024, 2048, 3584)}
             gamma = torch.as_tensor(synth.rms_gamma(1024, 801)).cuda()
-            ys = {name: torch.zeros(m * n, dtype=torch.float16, device="cuda")
+            ystride = {name: m * aexq.storage_elements(P4, m, n) for name, n, _ in synth.LAYER_LINEARS}
+            ys = {name: torch.zeros(copies * ystride[name], dtype=torch.float16, device="cuda")
                   for name, n, _ in synth.LAYER_LINEARS}
             d = aexq.describe
-            yd = {name: d(ys[name], m, n, P4, batch=copies, batch_stride=0)
+            yd = {name: d(ys[name], m, n, P4, batch=copies, batch_stride=ystride[name])
                   for name, n, _ in synth.LAYER_LINEARS}
-            xd = {k: d(v, m, k) for k, v in xs.items()}
+            xd = {k: d(v, m, k, batch=copies, batch_stride=m * k) for k, v in xs.items()}
 
             def step():
                 ctx.linear_group([ws["q_proj"], ws["k_proj"], ws["v_proj"]], xd[1024],
@@ -430,6 +483,31 @@ def config3(torch, aexq, ctx, steps: int = 30):
     return out
 
 
+def host_cpu() -> dict:
+    """The host's CPU: model, logical CPUs, the CPUs this process may run on,
+    and the threads the all-cores runs use (the job's CPU share: the smaller of
+    the affinity set and OMP_NUM_THREADS where that is set)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = nproc
+    share = avail
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        share = min(share, int(env))
+    return {"cpu_model": model, "nproc": nproc, "affinity_cpus": avail, "threads_used": share}
+
+
 def cpu_baseline(seconds: float):
     """RunGemmCpu (GS:13328-13381) restated in C, timed on this host: the seven
     linears of one layer on dequantized fp32 weights (dequant untimed, as at
@@ -441,16 +519,18 @@ def cpu_baseline(seconds: float):
 
     import oracle
     from aiimage_amd import synth
-    threads = max(1, min(16, os.cpu_count() or 1))
+    host = host_cpu()
+    threads = host["threads_used"]
 
-    def timed(fn, budget):
-        n, t0 = 0, time.perf_counter()
-        while True:
+    def timed(fn, budget, min_runs=10):
+        """Median seconds per run over at least min_runs runs and `budget` s."""
+        runs, t0 = [], time.perf_counter()
+        while len(runs) < min_runs or time.perf_counter() - t0 < budget:
+            a = time.perf_counter()
             fn()
-            n += 1
-            el = time.perf_counter() - t0
-            if el >= budget:
-                return el / n, n, el
+            runs.append(time.perf_counter() - a)
+        runs.sort()
+        return runs[len(runs) // 2], len(runs), time.perf_counter() - t0
 
     lin = []
     for i, (name, n, k) in enumerate(synth.LAYER_LINEARS):
@@ -465,9 +545,10 @@ def cpu_baseline(seconds: float):
 
     per_layer, layers, el = timed(lambda: layer(1), seconds)
     out = {"value": LAYER_BYTES / per_layer / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-           "sample": f"{layers} passes of one layer's 7 Q4 linears (M=1) through the C restatement "
-                     f"of RunGemmCpu on dequantized fp32 weights, {el:.1f} s, "
-                     f"{per_layer * 1e3:.2f} ms per layer; rate in algorithmic quantized bytes"}
+           "sample": f"median of {layers} passes of one layer's 7 Q4 linears (M=1) through the C "
+                     f"restatement of RunGemmCpu on dequantized fp32 weights ({el:.1f} s), "
+                     f"{per_layer * 1e3:.2f} ms per layer; rate in algorithmic quantized bytes",
+           "host": host}
     budget = max(1.0, seconds / 5)
     per_layer_mt, _, _ = timed(lambda: layer(threads), budget)
     cfg = {"config2_all_cores": {"GBps": LAYER_BYTES / per_layer_mt / 1e9, "cores": threads}}
@@ -585,6 +666,7 @@ def main():
         torch.cuda.empty_cache()
         log("extras: config 1 and config 5")
         result["extra"] = extras(torch, aexq, synth, ctx)
+        result["extra"].update(per_call_cold(torch, aexq, synth, ctx))
         result["extra"].update(config3(torch, aexq, ctx))
         result["extra"].update(config4(torch, aexq, synth, ctx))
         result["extra"].update(config4_single(torch, aexq, synth, ctx))
