@@ -232,8 +232,8 @@ aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w, const aexq_t
 /* aexq_lmhead_argmax with the final RMSNorm of the decoder (the norm layer the
  * reference's graph runs before the LM head, CC:4531-4557) fused as the
  * RMSNorm-in epilogue: args->flags may hold AEXQ_EPI_RMSNORM_IN only (with
- * rms_gamma / rms_eps), plus alpha, beta and C as for aexq_linear; args NULL
- * is aexq_lmhead_argmax. */
+ * rms_gamma / rms_eps) and alpha applies as for aexq_linear; the LM head takes
+ * no C term (args->c must be NULL).  args NULL is aexq_lmhead_argmax. */
 aexq_status aexq_lmhead_argmax_ex(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
                                   const aexq_tensor* logits, const aexq_linear_args* args,
                                   int32_t* argmax, float* top2_gap);
@@ -241,8 +241,9 @@ aexq_status aexq_lmhead_argmax_ex(aexq_ctx* ctx, const aexq_weight* w, const aex
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  No counterpart in the reference: it exists for those
  * callers only.  It allocates nothing: the argmax partials go to a fixed
- * device array of the library (3 x 32768 entries, 384 KiB per GPU, held until
- * the process ends) instead of the context's growing scratch.  Only the
+ * device array of the library (3 x 32768 partial entries and the merge's
+ * arrival counters, about 400 KiB per GPU, held until the process ends)
+ * instead of the context's growing scratch.  Only the
  * fused-argmax launches qualify (K a multiple of 16 at M = 1, of 128 above);
  * a launch needing more than 32768 (workgroup, row) partials, or the separate
  * logits pass, returns AEXQ_ERR_UNSUPPORTED.  Every call on one GPU shares the
