@@ -446,7 +446,8 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
   __shared__ __align__(16) f16 s_h[kStepMaxInter];     // SwiGLU output, pair order (P5)
   // attention scratch of the compute waves
   __shared__ __align__(16) f16 s_v[kAP * kHd];         // V rows (wave w: rows 8w .. 8w + 7)
-  __shared__ float s_e[kAW][GQ][8];                    // exp(score - wave max)
+  __shared__ __align__(16) float s_e[kAW][GQ][8];      // the wave's scores per head
+  __shared__ __align__(16) float s_x[kAW][GQ][8];      // exp(score - wave max)
   __shared__ float s_wm[kAW][GQ], s_wl[kAW][GQ];       // wave max, wave sum
   __shared__ __align__(16) float s_wacc[kAW][GQ][kHd]; // wave P.V sums
   __shared__ StepLayer s_layers[kStepMaxLayers];        // the layer table
@@ -613,7 +614,8 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
             *(u32x4*)&s_v[pl * kHd + j * 16] = vreg[0];
             *(u32x4*)&s_v[pl * kHd + j * 16 + 8] = vreg[1];
             const bool live = pl < sl_len;
-            float wl[GQ];
+            // scores of all heads first (independent chains the compiler interleaves)
+            float sc[GQ];
 #pragma unroll
             for (int h = 0; h < GQ; ++h) {
               const u32x4 q0 = *(const u32x4*)&s_q[h * kHd + j * 16];
@@ -626,30 +628,54 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
               a += dppf<0xB1>(a);   // quad_perm [1,0,3,2]
               a += dppf<0x4E>(a);   // quad_perm [2,3,0,1]
               a += dppf<0x141>(a);  // row_half_mirror: the other quad of the 8 lanes
-              const float sc = live ? a * p.scale : -INFINITY;
-              // the wave's maximum over its 8 positions
-              float m = fmaxf(sc, dppf<0x128>(sc));  // row_ror:8
-              m = fmaxf(m, __shfl_xor(m, 16, 64));
-              m = fmaxf(m, __shfl_xor(m, 32, 64));
-              const float ex = live ? __expf(sc - m) : 0.0f;
-              wl[h] = wave_sum(j == 0 ? ex : 0.0f);
-              if (j == 0) s_e[wave][h][pl & 7] = ex;
-              if (lane == 0) s_wm[wave][h] = m == -INFINITY ? kNegBig : m;
+              sc[h] = live ? a * p.scale : -INFINITY;
+            }
+            // softmax statistics through LDS (a wave's LDS accesses complete in
+            // order): the 8 scores per head give every lane the wave maximum,
+            // each position's lanes form its exp once, and the 8 exps per head
+            // come back for the sums and P.V
+            if (j == 0) {
+#pragma unroll
+              for (int h = 0; h < GQ; ++h) s_e[wave][h][pl & 7] = sc[h];
+            }
+            __asm__ volatile("" ::: "memory");
+            float mh[GQ];
+#pragma unroll
+            for (int h = 0; h < GQ; ++h) {
+              const f32x4 e0 = *(const f32x4*)&s_e[wave][h][0];
+              const f32x4 e1 = *(const f32x4*)&s_e[wave][h][4];
+              mh[h] = fmaxf(fmaxf(fmaxf(e0[0], e0[1]), fmaxf(e0[2], e0[3])),
+                            fmaxf(fmaxf(e1[0], e1[1]), fmaxf(e1[2], e1[3])));
+            }
+            // this lane's dims 2l, 2l + 1 of the wave's 8 V rows, for every head
+            f16x2 vv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              vv[i] = as_h2(*(const uint32_t*)&s_v[(wave * 8 + i) * kHd + 2 * lane]);
+            __asm__ volatile("" ::: "memory");
+            if (j == 0) {
+#pragma unroll
+              for (int h = 0; h < GQ; ++h) s_x[wave][h][pl & 7] = live ? __expf(sc[h] - mh[h]) : 0.0f;
             }
             __asm__ volatile("" ::: "memory");
             // P.V over the wave's 8 positions: lane l owns dims 2l, 2l + 1 of every head
 #pragma unroll
             for (int h = 0; h < GQ; ++h) {
-              float a0 = 0.0f, a1 = 0.0f;
+              const f32x4 x0 = *(const f32x4*)&s_x[wave][h][0];
+              const f32x4 x1 = *(const f32x4*)&s_x[wave][h][4];
+              const float e8[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+              float l = 0.0f, a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
               for (int i = 0; i < 8; ++i) {
-                const float e = s_e[wave][h][i];
-                const f16x2 vv = as_h2(*(const uint32_t*)&s_v[(wave * 8 + i) * kHd + 2 * lane]);
-                a0 = fmaf(e, (float)vv[0], a0);
-                a1 = fmaf(e, (float)vv[1], a1);
+                l += e8[i];
+                a0 = fmaf(e8[i], (float)vv[i][0], a0);
+                a1 = fmaf(e8[i], (float)vv[i][1], a1);
               }
               *(float2*)&s_wacc[wave][h][2 * lane] = make_float2(a0, a1);
-              if (lane == 0) s_wl[wave][h] = wl[h];
+              if (lane == 0) {
+                s_wm[wave][h] = mh[h] == -INFINITY ? kNegBig : mh[h];
+                s_wl[wave][h] = l;
+              }
             }
           }
           cbar(&s_cbar, cbar_target, lane, err, broken);
@@ -884,9 +910,23 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
           a[e] = in ? as_f32(v[0][e] & ~0xffu) * f : 0.0f;
           a[4 + e] = in ? as_f32(v[1][e] & ~0xffu) * f : 0.0f;
         }
-        for (int o = lps; o < 64; o <<= 1)
+        // the sum over splits (lanes lps apart): rotations within each row of
+        // 16 lanes by DPP, then the four rows
 #pragma unroll
-          for (int e = 0; e < 8; ++e) a[e] += __shfl_xor(a[e], o, 64);
+        for (int e = 0; e < 8; ++e) {
+          float x = a[e];
+          if (lps == 1) x += dppf<0x121>(x);  // row_ror:1
+          if (lps <= 2) x += dppf<0x122>(x);  // row_ror:2
+          if (lps <= 4) x += dppf<0x124>(x);  // row_ror:4
+          if (lps <= 8) x += dppf<0x128>(x);  // row_ror:8
+          a[e] = x;
+        }
+        if (lps <= 16) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[e] += __shfl_xor(a[e], 16, 64);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] += __shfl_xor(a[e], 32, 64);
         if (lane < lps) {
           const float inv_l = 1.0f / fmaxf(lsum, 1e-20f);
 #pragma unroll
