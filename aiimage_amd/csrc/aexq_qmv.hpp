@@ -31,7 +31,7 @@ struct Qmv {
   static constexpr int NW = PAIR ? 2 : 1;                // gate (+ up) weights
   static constexpr int NS = FMT == kQ8 ? 1 : (GM == kG16 ? 2 * CPL : CPL);  // scales per row
   // vector memory reads of one tile: residual (M = 1), codes, scales
-  static constexpr int kLoadsPerTile = (MMAX == 1 ? U : 0) + NW * U * (CPL + NS);
+  static constexpr int kLoadsPerTile = (MMAX == 1 && !ARGMAX ? U : 0) + NW * U * (CPL + NS);
 #ifndef QMV_VALU_PER_LOAD
 #define QMV_VALU_PER_LOAD 8
 #endif
