@@ -51,6 +51,7 @@ class ModelConfig:
     capacity: int = 2048     # KV cache positions
     group: int = 32          # Q4 scale group
     seed: int = synth.SEED_BASE + 3
+    scales_f32: bool = False  # layer scales fp32 (the reference archives' dtype) instead of fp16
 
     @property
     def q_width(self):
@@ -70,7 +71,8 @@ class ModelConfig:
         """Algorithmic HBM bytes of one decode step attending over `length`
         positions: every weight code and scale once, each cached K and V row
         once, and the activations each launch reads and writes."""
-        weights = sum(n * k // 2 + n * (k // self.group) * 2 for _, n, k in self.linears())
+        sb = 4 if self.scales_f32 else 2
+        weights = sum(n * k // 2 + n * (k // self.group) * sb for _, n, k in self.linears())
         kv_read = 2 * self.heads_kv * length * self.head_dim * 2
         h, qw, kw, i = self.hidden, self.q_width, self.kv_width, self.intermediate
         act = 2 * (h + qw + 2 * kw          # q/k/v: x in, q/k/v out
@@ -90,7 +92,8 @@ def host_weights(cfg: ModelConfig, layer: int):
     out = {}
     for i, (name, n, k) in enumerate(cfg.linears()):
         out[name] = synth.q4_weights(n, k, cfg.seed + 97 * layer + i, group=cfg.group,
-                                     code=synth.NIBBLE_OFFSET8)
+                                     code=synth.NIBBLE_OFFSET8,
+                                     scale_dtype=np.float32 if cfg.scales_f32 else np.float16)
     g_attn = synth.rms_gamma(cfg.hidden, cfg.seed + 97 * layer + 50)
     g_mlp = synth.rms_gamma(cfg.hidden, cfg.seed + 97 * layer + 51)
     return out, g_attn, g_mlp

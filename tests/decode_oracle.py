@@ -30,7 +30,7 @@ class OracleDecoder:
             for name, n, k in cfg.linears():
                 words, scales, _ = ws[name]
                 W[name] = orc.dequant_q4(words, scales, n, k, cfg.group, synth.NIBBLE_OFFSET8,
-                                         orc.SCALE_F16)
+                                         orc.SCALE_F32 if cfg.scales_f32 else orc.SCALE_F16)
             self.layers.append((W, g_attn, g_mlp))
         self.caches = []
         for l in range(cfg.layers):

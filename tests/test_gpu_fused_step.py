@@ -195,6 +195,33 @@ def test_fused_config3_full_size(ctx, aexq, orc):
         assert t_f == int(np.argmax(logits)) == t_p
 
 
+@pytest.mark.parametrize("workgroups", [0, 256])
+def test_fused_fp32_scales_and_grid(ctx, aexq, orc, workgroups):
+    """Layer scales in fp32 (the reference archives' dtype) and the 256-workgroup
+    grid (half the positions per attention split, a merge slice of 8 dims):
+    against the oracle and the per-operator step, the V row bit for bit."""
+    from aiimage_amd import decoder
+    from decode_oracle import OracleDecoder, top2_gap
+    cfg = decoder.ModelConfig(layers=2, capacity=128, scales_f32=True)
+    sess = decoder.DecodeSession(ctx, cfg, fused=True, workgroups=workgroups)
+    info = sess.fused.info()
+    _announce(f"fused step fp32 scales, grid {workgroups}: {info}")
+    if workgroups:
+        assert info["workgroups"] == workgroups
+    tok, pos = 777, 100
+    x_p, t_p = _step(sess, tok, pos, fused=False)
+    v_p = _v_row(sess, 0, pos)
+    sess.layers[0]["v_cache"].view(cfg.heads_kv, cfg.capacity, cfg.head_dim)[:, pos] = 0
+    x_f, t_f = _step(sess, tok, pos)
+    assert sess.fused.error() == 0
+    assert torch.equal(_v_row(sess, 0, pos), v_p)
+    x_ref, logits = OracleDecoder(orc, cfg).step(tok, pos)
+    assert normwise(x_f.cpu().numpy(), x_ref) <= 5e-3
+    assert normwise(x_f.cpu().numpy(), x_p.cpu().numpy()) <= 5e-3
+    if top2_gap(logits) >= ARGMAX_TIE:
+        assert t_f == int(np.argmax(logits)) == t_p
+
+
 def test_fused_rejects_shapes_it_does_not_take(ctx, aexq):
     _announce("fused step rejections")
     from aiimage_amd import decoder
