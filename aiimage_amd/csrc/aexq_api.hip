@@ -1046,7 +1046,19 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     int bm = (M <= 64 || (fmt == kQ4 && !split)) ? 64 : 128;
     const char* benv = getenv("AEXQ_QGEMM_BM");  // tuning override: 64 or 128
     if (benv && (atoi(benv) == 64 || atoi(benv) == 128) && !split) bm = atoi(benv);
-    QgemmConfig gc{fmt, bm, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16, split, g16};
+    QgemmConfig gc{fmt, bm, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16, split, g16, false};
+    // the LDS-direct pipeline: Q8, and Q4 whose fp16 scales split exactly in
+    // groups of 16 or 32 (AEXQ_QGEMM_DL=0: the register-staged kernel)
+    const char* dlenv = getenv("AEXQ_QGEMM_DL");
+    const bool dl = !(dlenv && atoi(dlenv) == 0) &&
+                    (fmt == kQ8 || (small && (w0->block == 16 || w0->block == 32) &&
+                                    getenv("AEXQ_QGEMM_NOSPLIT") == nullptr));
+    if (dl) {
+      gc.bm = M <= 64 ? 64 : 128;
+      if (benv && (atoi(benv) == 64 || atoi(benv) == 128)) gc.bm = atoi(benv);
+      gc.split = fmt == kQ4;
+      gc.direct = true;
+    }
     plan->gentry = qgemm_find(gc);
     if (plan->gentry) {
       plan->kind = kPlanGemm;
@@ -1383,11 +1395,11 @@ extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, cons
       snprintf(diag, diag_len, "%s", g_last_error.c_str());
     else if (plan.kind == kPlanGemm)
       snprintf(diag, diag_len,
-               "kernel=qgemm bits=%d bm=%d swiglu=%d split=%d rms_prepass=%d tiles=%d grid=%d "
-               "splitk=%d",
+               "kernel=qgemm bits=%d bm=%d swiglu=%d split=%d direct=%d rms_prepass=%d tiles=%d "
+               "grid=%d splitk=%d",
                w->bits, plan.gentry->cfg.bm, (int)plan.gentry->cfg.pair,
-               (int)plan.gentry->cfg.split, (int)plan.rms_prepass, plan.p.total_tiles, plan.grid,
-               plan.sk_chunks);
+               (int)plan.gentry->cfg.split, (int)plan.gentry->cfg.direct, (int)plan.rms_prepass,
+               plan.p.total_tiles, plan.grid, plan.sk_chunks);
     else if (plan.kind == kPlanMfma)
       snprintf(diag, diag_len, "kernel=qmm bits=%d mt=%d nt=%d swiglu=%d wide=%d rms_prepass=%d "
                "tiles=%d grid=%d mblock=%d splitk=%d",

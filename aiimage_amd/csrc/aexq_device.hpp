@@ -284,21 +284,53 @@ __device__ __forceinline__ float argmax_epilogue(const QmvParams& p, float v) {
   return (p.flags & kFlagAlphaIn) ? p.alpha * (0.0f + v) : 0.0f + p.alpha * v;
 }
 
+// The operands of gemm_epilogue, for loops that finish many outputs: taken
+// out of the kernel arguments once (epi_args) and held in scalar registers.
+struct EpiArgs {
+  const __attribute__((address_space(1))) float* c;  // global (not flat) loads
+  float alpha, beta;
+  int bcast, c_rstride, flags;
+};
+
 // Bias, alpha and beta as the reference Gemm resolves them (MM:688-705, 812-820):
 // Pack4-linear output is alpha*(beta*C + sum), tiled output beta*C + alpha*sum.
-__device__ __forceinline__ float gemm_epilogue(const QmvParams& p, int m, int r, float v) {
+__device__ __forceinline__ float gemm_epilogue(const EpiArgs& e, int m, int r, float v) {
   float bias = 0.0f;
-  if (p.c) {
-    switch (p.bcast) {
-      case 0: bias = p.c[0]; break;
-      case 1: bias = p.c[m]; break;
-      case 3: bias = p.c[(long long)m * p.c_rstride + r]; break;
-      case 4: bias = p.c[r]; break;
+  if (e.c) {
+    switch (e.bcast) {
+      case 0: bias = e.c[0]; break;
+      case 1: bias = e.c[m]; break;
+      case 3: bias = e.c[(long long)m * e.c_rstride + r]; break;
+      case 4: bias = e.c[r]; break;
       default: bias = 0.0f; break;
     }
-    bias *= p.beta;
+    bias *= e.beta;
   }
-  return (p.flags & kFlagAlphaIn) ? p.alpha * (bias + v) : bias + p.alpha * v;
+  return (e.flags & kFlagAlphaIn) ? e.alpha * (bias + v) : bias + e.alpha * v;
+}
+__device__ __forceinline__ float gemm_epilogue(const QmvParams& p, int m, int r, float v) {
+  return gemm_epilogue(EpiArgs{(const __attribute__((address_space(1))) float*)p.c, p.alpha,
+                               p.beta, p.bcast, p.c_rstride, p.flags},
+                       m, r, v);
+}
+
+// A wave-uniform value computed once: the readfirstlane makes it an
+// instruction result, so the compiler keeps it in a scalar register instead
+// of loading it from the kernel arguments again inside a loop.
+__device__ __forceinline__ int sreg(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float sreg(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+template <typename T>
+__device__ __forceinline__ T* sreg(T* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ EpiArgs epi_args(const QmvParams& p) {
+  return EpiArgs{(const __attribute__((address_space(1))) float*)sreg(p.c), sreg(p.alpha),
+                 sreg(p.beta), sreg(p.bcast), sreg(p.c_rstride), sreg(p.flags)};
 }
 
 }  // namespace aexq

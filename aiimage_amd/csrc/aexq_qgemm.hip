@@ -3,14 +3,26 @@
 // fp16 or fp32 scales, single weights or SwiGLU pairs; 64-row activation
 // tiles (Q4, Q8) and 128-row tiles (Q8; Q4 with split fp16 scales).
 #include "aexq_qgemm.hpp"
+#include "aexq_qgemm_dl.hpp"
 
 namespace aexq {
 
 #define QGEG(FMT, BM, PAIR, SF16, SPLIT, G16)                                 \
   QgemmEntry {                                                                \
-    QgemmConfig{FMT, BM, PAIR, SF16, SPLIT, G16},                             \
+    QgemmConfig{FMT, BM, PAIR, SF16, SPLIT, G16, false},                      \
         &qgemm_kernel<FMT, BM, PAIR, SF16, SPLIT, G16>                        \
   }
+// LDS-direct forms: 128-row tiles two workgroups per CU, 64-row tiles three
+#define QGDL(FMT, BM, PAIR, SF16, G)                                          \
+  QgemmEntry {                                                                \
+    QgemmConfig{FMT, BM, PAIR, SF16, FMT == kQ4, G == 16, true},              \
+        &qgemm_dl_kernel<FMT, BM, PAIR, SF16, G, BM == 128 ? 2 : 3>           \
+  }
+#define QGDL_BM(BM)                                                            \
+  QGDL(kQ8, BM, false, true, 0), QGDL(kQ8, BM, false, false, 0),              \
+      QGDL(kQ8, BM, true, true, 0), QGDL(kQ8, BM, true, false, 0),            \
+      QGDL(kQ4, BM, false, true, 32), QGDL(kQ4, BM, true, true, 32),          \
+      QGDL(kQ4, BM, false, true, 16), QGDL(kQ4, BM, true, true, 16)
 #define QGE(FMT, BM, PAIR, SF16, SPLIT) QGEG(FMT, BM, PAIR, SF16, SPLIT, false)
 
 #define QG_BM(FMT, BM) \
@@ -23,7 +35,7 @@ static const QgemmEntry kTableG[] = {
     QG_BM(kQ4, 64), QG_BM(kQ8, 64), QG_BM(kQ8, 128), QGE(kQ4, 128, false, true, true),
     QGE(kQ4, 128, true, true, true), QGEG(kQ4, 64, false, true, false, true),
     QGEG(kQ4, 64, false, false, false, true), QGEG(kQ4, 64, true, true, false, true),
-    QGEG(kQ4, 64, true, false, false, true)};
+    QGEG(kQ4, 64, true, false, false, true), QGDL_BM(64), QGDL_BM(128)};
 
 static constexpr int kCountG = (int)(sizeof(kTableG) / sizeof(kTableG[0]));
 
@@ -31,7 +43,7 @@ const QgemmEntry* qgemm_find(const QgemmConfig& c) {
   for (int i = 0; i < kCountG; ++i) {
     const QgemmConfig& q = kTableG[i].cfg;
     if (q.fmt == c.fmt && q.bm == c.bm && q.pair == c.pair && q.sf16 == c.sf16 &&
-        q.split == c.split && q.g16 == c.g16)
+        q.split == c.split && q.g16 == c.g16 && q.direct == c.direct)
       return &kTableG[i];
   }
   return nullptr;

@@ -1,0 +1,622 @@
+// Tiled quantized GEMM for M > 32 activation rows with LDS-direct loads
+// (gfx950 `buffer_load_dwordx4 ... lds`): Y[M][N] = X[M][K] W[N][K]^T for Q8
+// with one scale per row and Q4 with fp16 scales of magnitude <= 4096 in
+// groups of 16 or 32 codes, K a multiple of 64.
+//
+// A workgroup owns one output tile: BM activation rows by 128 weight rows (a
+// SwiGLU pair: 64 gate rows and the same 64 up rows), 256 threads.  Each
+// 64-wide K step's activation tile, code tile and (Q4) scales travel from
+// global memory straight into LDS: every 16-byte load instruction of a wave
+// writes 1 KB of LDS, lane i at byte 16 i, so the lanes' global addresses are
+// chosen to give the layout the MFMA fragment reads want, and no register
+// holds a step in transit.  Three LDS stages rotate with one barrier per
+// step, so a step's loads have two steps of MFMAs to land.
+//
+// The K order inside a step is permuted: the MFMA's lane group g (l / 16)
+// carries codes 16 g .. 16 g + 15 of the step, the first eight in the step's
+// first MFMA K extent and the rest in the second.  A lane's codes then sit
+// together (Q8: one 16-byte read for both halves; Q4: one 8-byte read), and
+// the activation fragments are read in the same order.  The products are
+// those of K order, summed in another order inside fp32 accumulators.
+//
+// Codes become exact fp16 integers in registers.  Q8 accumulates the row in
+// the MFMA and applies its row scale once at the end.  Q4 splits each fp16
+// scale s into s_hi (its top 7 significand bits) and s_lo = s - s_hi; q * s_hi
+// and q * s_lo are exact fp16 values (|q| <= 8), so two MFMAs accumulate
+// x * (q * s) exactly; a lane's 16 codes lie in one scale group for groups of
+// 16 and 32 alike.
+//
+// Activation rows are 128 bytes per step in LDS with their 16-byte chunks
+// XOR-swizzled by the row (chunk c of row r at slot c ^ ((r & 7) ^ ((r >> 3) & 1))),
+// so the 16 rows of a fragment read spread over every bank.  The code tile is
+// stored per 16-row block in read order (Q8: [16-byte quarter][row]; Q4:
+// [half][row]), so a fragment read is one contiguous run.
+//
+// Waves: BM = 128 as 2 x 2 (64 activation rows by 64 weight rows each),
+// BM = 64 as 1 x 4 (64 by 32): four 16-row A blocks per wave either way.
+// Inside a step the barrier sits between the two K halves: the first half's
+// MFMAs cover the second half's fragment reads and the barrier wait, the
+// second half's MFMAs cover the next step's first fragment reads.
+//
+// Workgroup b runs on XCD b % 8: the numbering puts the BM-row tiles of one
+// weight tile on one XCD, whose L2 then fetches that weight tile once.
+//
+// MFMA 16x16x32 f16 lane layout (lane l): A[l % 16][8 (l / 16) + j],
+// B[8 (l / 16) + j][l % 16], D[4 (l / 16) + r][l % 16], j < 8, r < 4.
+#pragma once
+
+#include "aexq_qmm.hpp"
+
+namespace aexq {
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(1))) char gchar;  // global memory
+typedef __attribute__((address_space(1))) f32x4 gf32x4;
+typedef __attribute__((address_space(1))) u32x4 gu32x4;
+
+// LDS byte address of a generic pointer into LDS (the low half of the
+// generic address), wave-uniform.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+
+// One LDS-direct load: lane i's BYTES (16 or 4) at byte voff of resource r go
+// to LDS byte lds + BYTES * i; offsets past the resource's end write zeros.
+// Written as assembly so that the compiler does not see LDS stores in flight:
+// it would otherwise wait for every outstanding load before each LDS read.
+// The kernel orders them itself -- s_waitcnt vmcnt for its own loads, then a
+// barrier for the other waves' -- and the memory clobber keeps the compiler
+// from moving LDS accesses across a load.
+template <int BYTES>
+__device__ __forceinline__ void dma(__amdgpu_buffer_rsrc_t r, uint32_t lds, int voff) {
+  static_assert(BYTES == 16 || BYTES == 4, "dword or dwordx4");
+  if constexpr (BYTES == 16)
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(r)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(r)
+                 : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14));
+}
+// s_waitcnt lgkmcnt(0).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+// Workgroup barrier without the fence __syncthreads() adds (whose vmcnt(0)
+// would also wait for the LDS-direct loads of the steps ahead); the empty asm
+// statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void bar() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Eight offset-8 nibbles (n0 in bits 0-3) -> four fp16 pairs of the exact
+// codes n - 8 in element order: pair j = (n_2j, n_2j+1).  Byte j goes to both
+// halves (v_perm), the mask keeps n_2j low in half 0 and n_2j+1 at bits 4-7
+// of half 1; with the exponent pattern 0x6400 the halves are 1024 + n_2j and
+// 1024 + 16 n_2j+1, and one fma with (1, 1/16), (-1032, -72) gives both codes.
+__device__ __forceinline__ void q4_pairs_seq(uint32_t w, uint32_t q[4]) {
+  uint32_t E = 0x64006400u, m = 0x00F0000Fu;
+  __asm__("" : "+v"(E));
+  __asm__("" : "+s"(m));
+  const f16x2 mul = {(f16)1.0f, (f16)0.0625f};
+  const f16x2 add = {(f16)-1032.0f, (f16)-72.0f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t t = __builtin_amdgcn_perm(w, w, 0x0C000C00u | (j << 16) | j);
+    q[j] = as_u(__builtin_elementwise_fma(as_h2((t & m) | E), mul, add));
+  }
+}
+
+template <int FMT, int BM, bool PAIR, bool SF16, int G>
+struct QGemmDL {
+  static_assert(FMT == kQ8 ? G == 0 : (SF16 && (G == 16 || G == 32)),
+                "Q8 (row scales) or Q4 with fp16 scales in groups of 16 or 32");
+  static_assert(BM == 64 || BM == 128, "64- or 128-row activation tiles");
+  static constexpr int BN = 128;                  // weight rows of a tile
+  static constexpr int BK = 64;                   // K per step
+  static constexpr int NOUT = PAIR ? BN / 2 : BN;  // output columns of a tile
+  static constexpr int WGN = BM == 128 ? 2 : 4;   // waves across the weight rows
+  static constexpr int WR = BN / WGN;             // weight rows per wave
+  static constexpr int TN = WR / 16;              // 16-row B blocks per wave
+  static constexpr int TM = 4;                    // 16-row A blocks per wave (64 rows)
+  static constexpr int CP = FMT == kQ8 ? 64 : 32;  // code bytes per row and step
+  static constexpr int A_BYTES = BM * 128;
+  static constexpr int B_BYTES = BN * CP;
+  static constexpr int S_BYTES = FMT == kQ8 ? 0 : 1024;
+  static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+  static constexpr int A_INST = A_BYTES / 1024 / 4;  // direct loads per wave and step
+  static constexpr int B_INST = B_BYTES / 1024 / 4;
+  static constexpr int S_INST = FMT == kQ8 ? 0 : 1;
+  static constexpr int NL = A_INST + B_INST + S_INST;
+  static constexpr int SPR = FMT == kQ8 ? 0 : BK / G;  // scales per row and step
+
+  // Tile row (0..127 of the code tile) of B block tn of wave column wn.
+  static __device__ __forceinline__ int brow(int wn, int tn) {
+    if constexpr (PAIR)
+      return (tn >= TN / 2 ? 64 : 0) + wn * (WR / 2) + 16 * (tn % (TN / 2));
+    return wn * WR + 16 * tn;
+  }
+
+  struct Src {
+    __amdgpu_buffer_rsrc_t xr, wr, sr;
+    int oa[A_INST];  // per-lane byte offsets of step 0
+    int ob[B_INST];
+    int os;
+  };
+
+  static __device__ __forceinline__ Src source(const QmvParams& p, const QmvMat& mt, int b,
+                                               int n0, int m0, int lane, int wave) {
+    Src s;
+    const int rb = FMT == kQ8 ? p.k : p.k / 2;  // code bytes per weight row
+    const int rows = mt.n > n0 ? min(mt.n - n0, NOUT) : 0;
+    // B rows of this wave's code loads: Q8 blocks 2w, 2w + 1 (rows 32 w ..), Q4
+    // rows 32 w ..: the up weight for w >= 2 of a pair
+    const bool up = PAIR && wave >= 2;
+    const char* wb = (const char*)(up ? mt.w2 : mt.w) + (long long)b * mt.w_bstride * 4 +
+                     (long long)n0 * rb;
+    s.wr = __builtin_amdgcn_make_buffer_rsrc((void*)wb, (short)0, rows * rb, kBufferRsrcWord3);
+    const int rs2 = (int)(p.x_rstride * 2);
+    const char* xb = (const char*)mt.x + (long long)b * mt.x_bstride * 2 + (long long)m0 * rs2;
+    const int mrows = p.m - m0 < BM ? p.m - m0 : BM;
+    s.xr = __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, mrows * rs2, kBufferRsrcWord3);
+#pragma unroll
+    for (int t = 0; t < A_INST; ++t) {
+      const int row = 8 * (wave * A_INST + t) + (lane >> 3);
+      const int c = (lane & 7) ^ ((row & 7) ^ ((row >> 3) & 1));
+      s.oa[t] = row * rs2 + c * 16;
+    }
+    if constexpr (FMT == kQ8) {
+#pragma unroll
+      for (int t = 0; t < B_INST; ++t) {
+        const int r = 16 * (wave * B_INST + t) + (lane & 15);
+        s.ob[t] = (PAIR ? (r & 63) : r) * rb + 16 * (lane >> 4);
+      }
+      // row scales: wave 0 rows 0-63 (the gate rows of a pair), wave 1 rows
+      // 64-127 (the up rows); fp16: lane i fetches rows 2i, 2i + 1 (lanes 32..
+      // fall past the rows), fp32: row i
+      constexpr int sb = SF16 ? 2 : 4;
+      const bool sup = PAIR && wave == 1;
+      const int base_row = PAIR ? 0 : 64 * (wave & 1);
+      const char* sp = (const char*)(sup ? mt.s2 : mt.s) + (long long)b * mt.s_bstride * sb +
+                       (long long)(n0 + base_row) * sb;
+      const int srows = __builtin_amdgcn_readfirstlane(min(max(rows - base_row, 0), 64));
+      s.sr = __builtin_amdgcn_make_buffer_rsrc((void*)sreg(sp), (short)0, srows * sb,
+                                               kBufferRsrcWord3);
+      s.os = 4 * lane;
+    } else {
+      const int r = 32 * wave + 16 * (lane >> 5) + (lane & 15);
+      s.ob[0] = (PAIR ? (r & 63) : r) * rb + 16 * ((lane >> 4) & 1);
+      // scales: G32 waves 0, 1 (64 rows x 2 scales each), G16 all four waves
+      // (32 rows x 4 scales); the other waves' loads fall past the resource
+      const bool sup = PAIR && (G == 32 ? wave == 1 : wave >= 2);
+      const char* sp = (const char*)(sup ? mt.s2 : mt.s) +
+                       ((long long)b * mt.s_bstride + (long long)n0 * p.groups_per_row) * 2;
+      s.sr = __builtin_amdgcn_make_buffer_rsrc((void*)sp, (short)0,
+                                               rows * p.groups_per_row * 2, kBufferRsrcWord3);
+      int srow, sdw;
+      if constexpr (G == 32) {
+        srow = 64 * wave + lane;
+        sdw = 0;
+      } else {
+        srow = 32 * wave + (lane >> 1);
+        sdw = lane & 1;
+      }
+      const int wrow = PAIR ? (srow & 63) : srow;
+      s.os = (G == 32 && wave >= 2) ? (1 << 30)
+                                    : (wrow * p.groups_per_row + 2 * sdw) * 2;
+    }
+    return s;
+  }
+
+  // The direct loads of step st into the LDS stage at byte `base`.
+  static __device__ __forceinline__ void issue(const Src& s, uint32_t base, int wave, int st) {
+#pragma unroll
+    for (int t = 0; t < A_INST; ++t)
+      dma<16>(s.xr, base + (wave * A_INST + t) * 1024, s.oa[t] + st * 128);
+#pragma unroll
+    for (int t = 0; t < B_INST; ++t)
+      dma<16>(s.wr, base + A_BYTES + (wave * B_INST + t) * 1024, s.ob[t] + st * CP);
+    if constexpr (FMT == kQ4) dma<4>(s.sr, base + A_BYTES + B_BYTES + wave * 256, s.os + st * SPR * 2);
+  }
+
+  // Fragments of one step a wave reads from LDS: the activation blocks of one
+  // K half and the raw codes (and Q4 scales) of both halves.
+  struct Frag {
+    f16x8 a[TM];
+    typename std::conditional<FMT == kQ8, u32x4, u32x2>::type c[TN];
+    uint32_t s[FMT == kQ8 ? 1 : TN];
+  };
+
+  struct Lane {
+    int a_off[2];  // activation fragment offset of K half 0 / 1 (row l16 of block 0)
+    int b_off;     // code fragment offset inside a 16-row block
+    int s_off;     // scale offset (row l16, the lane group's scale group) inside block row 0
+  };
+
+  static __device__ __forceinline__ Lane lane_offsets(int lane) {
+    Lane L;
+    const int l16 = lane & 15, lk = lane >> 4;
+    const int f = (l16 & 7) ^ (l16 >> 3);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) L.a_off[kk] = l16 * 128 + (((2 * lk + kk) ^ f) << 4);
+    L.b_off = FMT == kQ8 ? 16 * lane : (lk >> 1) * 256 + l16 * 16 + 8 * (lk & 1);
+    L.s_off = FMT == kQ8 ? 0 : l16 * (2 * SPR) + 2 * (G == 32 ? (lk >> 1) : lk);
+    return L;
+  }
+
+  static __device__ __forceinline__ void read_a(const char* base, const Lane& L, int wm, int kk,
+                                                f16x8 (&a)[TM]) {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+      a[tm] = *(const f16x8*)(base + (wm * 64 + 16 * tm) * 128 + L.a_off[kk]);
+  }
+
+  static __device__ __forceinline__ void read_b(const char* base, const Lane& L, int wn, Frag& f) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int blk = brow(wn, tn) >> 4;
+      if constexpr (FMT == kQ8) {
+        f.c[tn] = *(const u32x4*)(base + A_BYTES + blk * 1024 + L.b_off);
+      } else {
+        f.c[tn] = *(const u32x2*)(base + A_BYTES + blk * 512 + L.b_off);
+        f.s[tn] = *(const uint16_t*)(base + A_BYTES + B_BYTES + blk * 16 * (2 * SPR) + L.s_off);
+      }
+    }
+  }
+
+  // The MFMAs of K half kk from the activation blocks a and the step's codes.
+  static __device__ __forceinline__ void mfma_half(int kk, const f16x8 (&a)[TM], const Frag& f,
+                                                   f32x4 (&acc)[TM][TN]) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      if constexpr (FMT == kQ8) {
+        uint32_t e0, e1, e2, e3;
+        q8_pairs(f.c[tn][2 * kk], e0, e1);
+        q8_pairs(f.c[tn][2 * kk + 1], e2, e3);
+        const f16x8 bq = pack8(e0, e1, e2, e3);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bq, acc[tm][tn], 0, 0, 0);
+      } else {
+        uint32_t e[4];
+        q4_pairs_seq(f.c[tn][kk], e);
+        // (s_hi, s_lo): s_hi keeps the top 7 significand bits, s_lo = s - s_hi exactly
+        const f16 sv = __builtin_bit_cast(f16, (uint16_t)f.s[tn]);
+        const f16 hi = __builtin_bit_cast(f16, (uint16_t)(f.s[tn] & 0xFFF0u));
+        const f16 lo = sv - hi;
+        const f16x2 shi = {hi, hi}, slo = {lo, lo};
+        const f16x8 bhi = pack8(as_u(as_h2(e[0]) * shi), as_u(as_h2(e[1]) * shi),
+                                as_u(as_h2(e[2]) * shi), as_u(as_h2(e[3]) * shi));
+        const f16x8 blo = pack8(as_u(as_h2(e[0]) * slo), as_u(as_h2(e[1]) * slo),
+                                as_u(as_h2(e[2]) * slo), as_u(as_h2(e[3]) * slo));
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bhi, acc[tm][tn], 0, 0, 0);
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], blo, acc[tm][tn], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // Output column (tile-relative) of output block `to` of wave column wn.
+  static __device__ __forceinline__ int ocol(int wn, int to) {
+    return PAIR ? wn * (WR / 2) + 16 * to : wn * WR + 16 * to;
+  }
+
+  // The finished tile, through LDS.  The waves of activation rows 64 h ..
+  // 64 h + 63 write their raw accumulators into an fp32 tile C[64][CW] (the
+  // pipeline's stages are free by then); then each thread finishes 8
+  // consecutive outputs of a row per pass -- row scale (Q8), bias, alpha/beta,
+  // SwiGLU, residual -- and stores them with one 16-byte (fp16) or two
+  // (fp32) stores where the layout allows, element by element otherwise.
+  // One short loop for every output keeps the code (and the instruction
+  // cache) small, and the stores cover whole rows of the tile.
+  static constexpr int CW = BN + 4;            // floats per LDS row of C
+  static constexpr int TPR = NOUT / 8;         // threads per output row
+  static constexpr int RPP = kThreads / TPR;   // rows per pass
+  static constexpr int C_BYTES = 64 * CW * 4;
+
+  static __device__ __forceinline__ void finish(const QmvParams& p, const QmvMat& mt, int b,
+                                                int n0, int m0, int tid, int lane, int wm,
+                                                int wn, const f32x4 (&acc)[TM][TN], float* C,
+                                                const char* qs) {
+    const int l16 = lane & 15, lk = lane >> 4;
+    // everything the loops below use, in registers (see sreg)
+    const EpiArgs E = epi_args(p);
+    const bool yf32 = (E.flags & kFlagYf32) != 0;
+    const bool resid = mt.res && (E.flags & kFlagResidual);
+    const int esz = yf32 ? 4 : 2;
+    // (global pointers: the stores and residual loads are global, not flat)
+    gchar* const yb = (gchar*)sreg((char*)mt.y + (long long)b * mt.y_bstride * esz);
+    const gchar* const rb =
+        resid ? (const gchar*)sreg((const char*)mt.res + (long long)b * mt.r_bstride * esz)
+              : nullptr;
+    const int mn = sreg(mt.n), nst = sreg(mt.n_store), pm = sreg(p.m), mbase = sreg(p.m_base);
+    const long long yrs = ((long long)sreg((int)(mt.y_rstride >> 32)) << 32) |
+                          (uint32_t)sreg((int)mt.y_rstride);
+    const long long rrs = ((long long)sreg((int)(p.r_rstride >> 32)) << 32) |
+                          (uint32_t)sreg((int)p.r_rstride);
+    const int cg = tid % TPR, r0 = tid / TPR;
+    const int nb = n0 + 8 * cg;  // first of the thread's 8 output columns
+    // 8-wide rows: row-major output, every column stored, aligned rows
+    const bool vec = mt.y_hd == 0 && nb + 8 <= nst && (yrs & 7) == 0 &&
+                     ((uintptr_t)yb & 15) == 0 &&
+                     (!resid || ((rrs & 7) == 0 && ((uintptr_t)rb & 15) == 0));
+    // every column stored and real, no bias: the branch-free form below
+    const bool fast = vec && nb + 8 <= mn && !E.c;
+    const bool alpha_in = (E.flags & kFlagAlphaIn) != 0;
+    const float a_in = alpha_in ? E.alpha : 1.0f, a_out = alpha_in ? 1.0f : E.alpha;
+    float rs0[8], rs1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      rs0[j] = 1.0f;
+      rs1[j] = 1.0f;
+      if constexpr (FMT == kQ8) {
+        // row scales as the prologue placed them: tile row r at (r / 64) * 512
+        // + (r % 64) * (2 or 4) bytes; the up half of a pair from row 64
+        const int r = 8 * cg + j;
+        rs0[j] = scale_of(SF16 ? *(const uint16_t*)(qs + (r >> 6) * 512 + (r & 63) * 2)
+                               : *(const uint32_t*)(qs + (r >> 6) * 512 + (r & 63) * 4),
+                          SF16);
+        if constexpr (PAIR)
+          rs1[j] = scale_of(SF16 ? *(const uint16_t*)(qs + 512 + r * 2)
+                                 : *(const uint32_t*)(qs + 512 + r * 4),
+                            SF16);
+      }
+    }
+#pragma unroll 1
+    for (int h = 0; h < BM / 64; ++h) {
+      if (h > 0) bar();  // every thread has read the previous half
+      if (wm == h) {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              C[(16 * tm + 4 * lk + r) * CW + brow(wn, tn) + l16] = acc[tm][tn][r];
+      }
+      wait_lgkm0();
+      bar();
+#pragma unroll 1
+      for (int row = r0; row < 64; row += RPP) {
+        const int m = m0 + 64 * h + row;
+        if (m >= pm || !yb) continue;
+        float g[8], u[8];
+        *(f32x4*)&g[0] = *(const f32x4*)&C[row * CW + 8 * cg];
+        *(f32x4*)&g[4] = *(const f32x4*)&C[row * CW + 8 * cg + 4];
+        if constexpr (PAIR) {
+          *(f32x4*)&u[0] = *(const f32x4*)&C[row * CW + 64 + 8 * cg];
+          *(f32x4*)&u[4] = *(const f32x4*)&C[row * CW + 64 + 8 * cg + 4];
+        }
+        float res[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) res[j] = 0.0f;
+        if (resid) {
+          const long long ri = (long long)m * rrs + nb;
+          if (vec) {
+            if (yf32) {
+              *(f32x4*)&res[0] = *(const gf32x4*)(rb + ri * 4);
+              *(f32x4*)&res[4] = *(const gf32x4*)(rb + ri * 4 + 16);
+            } else {
+              const u32x4 h8 = *(const gu32x4*)(rb + ri * 2);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const f16x2 hv = as_h2(h8[q]);
+                res[2 * q] = (float)hv[0];
+                res[2 * q + 1] = (float)hv[1];
+              }
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              if (nb + j < mn)
+                res[j] = yf32 ? ((const __attribute__((address_space(1))) float*)rb)[ri + j]
+                              : (float)((const __attribute__((address_space(1))) f16*)rb)[ri + j];
+          }
+        }
+        float v[8];
+        if (fast) {
+          // no bias: alpha * (0 + x) or 0 + alpha * x as a_in * (0 + a_out * x),
+          // the same roundings with no branch per output
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            v[j] = a_in * (0.0f + a_out * (g[j] * rs0[j]));
+            if constexpr (PAIR) v[j] = silu(v[j]) * (a_in * (0.0f + a_out * (u[j] * rs1[j])));
+            v[j] += res[j];
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int n = nb + j;
+            v[j] = 0.0f;
+            if (n < mn) {
+              v[j] = gemm_epilogue(E, mbase + m, n, g[j] * rs0[j]);
+              if constexpr (PAIR)
+                v[j] = silu(v[j]) * gemm_epilogue(E, mbase + m, n, u[j] * rs1[j]);
+              v[j] += res[j];
+            }
+          }
+        }
+        if (vec) {
+          const long long yi = (long long)m * yrs + nb;
+          if (yf32) {
+            *(gf32x4*)(yb + yi * 4) = f32x4{v[0], v[1], v[2], v[3]};
+            *(gf32x4*)(yb + yi * 4 + 16) = f32x4{v[4], v[5], v[6], v[7]};
+          } else {
+            u32x4 o;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q] = as_u(f16x2{(f16)v[2 * q], (f16)v[2 * q + 1]});
+            *(gu32x4*)(yb + yi * 2) = o;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int n = nb + j;
+            if (n < nst) {
+              const long long yi = out_index(p, mt, m, n);
+              if (yf32)
+                ((__attribute__((address_space(1))) float*)yb)[yi] = v[j];
+              else
+                ((__attribute__((address_space(1))) f16*)yb)[yi] = (f16)v[j];
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // Split K: the raw accumulators of K chunk c (no row scale, no epilogue)
+  // into partial plane c.
+  static __device__ __forceinline__ void spill(const QmvParams& p, const QmvMat& mt, int b,
+                                               int n0, int m0, int lane, int wm, int wn, int c,
+                                               const f32x4 (&acc)[TM][TN]) {
+    const int l16 = lane & 15, lk = lane >> 4;
+    constexpr int NW = PAIR ? 2 : 1;
+    constexpr int TO = PAIR ? TN / 2 : TN;
+    float* base = p.sk_part + (long long)c * p.sk_plane + mt.sk_off +
+                  (long long)b * p.m * NW * mt.n_store;
+#pragma unroll
+    for (int to = 0; to < TO; ++to) {
+      const int n = n0 + ocol(wn, to) + l16;
+      if (n >= mt.n) continue;
+#pragma unroll
+      for (int h = 0; h < NW; ++h)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm * 64 + 16 * tm + 4 * lk + r;
+            if (m < p.m) base[((long long)m * NW + h) * mt.n_store + n] = acc[tm][to + TO * h][r];
+          }
+    }
+  }
+};
+
+// One step of the pipeline on LDS stage `cur` (the next step's stage `nxt`,
+// the stage refilled with step st + 3 is `cur` itself): on entry f holds the
+// step's codes and first-half activation blocks; on return, the next step's.
+template <typename G>
+__device__ __forceinline__ void qgemm_dl_step(const typename G::Src& src, const typename G::Lane& L,
+                                              char* cur, char* nxt, int wave, int wm, int wn,
+                                              int st, int s1, typename G::Frag& f,
+                                              f32x4 (&acc)[G::TM][G::TN]) {
+  f16x8 a1[G::TM];
+  G::read_a(cur, L, wm, 1, a1);
+  __builtin_amdgcn_sched_barrier(0);  // the reads go out ahead of the MFMAs
+  G::mfma_half(0, f.a, f, acc);
+  // this step's fragments are in registers before any wave refills `cur`;
+  // step st + 1's loads (the oldest in flight) have landed
+  wait_lgkm0();
+  if (st + 2 < s1)
+    wait_vm<G::NL>();
+  else
+    wait_vm<0>();
+  bar();
+  if (st + 3 < s1) G::issue(src, lds_addr(cur), wave, st + 3);
+  typename G::Frag g;
+  if (st + 1 < s1) {
+    G::read_a(nxt, L, wm, 0, g.a);
+    G::read_b(nxt, L, wn, g);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  G::mfma_half(1, a1, f, acc);
+  f = g;
+}
+
+template <int FMT, int BM, bool PAIR, bool SF16, int G, int WPE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WPE)))
+void qgemm_dl_kernel(const QmvParams p, int mtiles) {
+  using Q = QGemmDL<FMT, BM, PAIR, SF16, G>;
+  static_assert(Q::C_BYTES <= 3 * Q::STAGE, "the accumulator tile reuses the stages");
+  __shared__ __align__(1024) char lds[3 * Q::STAGE];
+  __shared__ __align__(16) char qs[FMT == kQ8 ? 1024 : 16];  // Q8 row scales of the tile
+  char* const st0 = lds;
+  char* const st1 = lds + Q::STAGE;
+  char* const st2 = lds + 2 * Q::STAGE;
+  // weight tile tn, row tile tm and K chunk kc of this workgroup (the chunks
+  // of a split K sit next to each other on one XCD); readfirstlane keeps the
+  // workgroup-uniform coordinates in scalar registers
+  const int S = p.sk_chunks > 1 ? p.sk_chunks : 1;
+  const int per = mtiles * S;
+  const int bid = blockIdx.x, i = bid >> 3;
+  const int tn = __builtin_amdgcn_readfirstlane((i / per) * 8 + (bid & 7));
+  const int rem = i - (i / per) * per;
+  const int tm = __builtin_amdgcn_readfirstlane(rem / S);
+  const int kc = __builtin_amdgcn_readfirstlane(rem - (rem / S) * S);
+  if (tn >= p.total_tiles) return;
+  int j = 0;
+  for (int q = 1; q < p.nmat; ++q)
+    if (tn >= p.mat[q].tile_base) j = q;
+  j = __builtin_amdgcn_readfirstlane(j);
+  const QmvMat& mt = p.mat[j];
+  const int local = tn - mt.tile_base;
+  const int b = __builtin_amdgcn_readfirstlane(local / mt.tiles);
+  const int n0 = __builtin_amdgcn_readfirstlane((local - b * mt.tiles) * Q::NOUT);
+  const int m0 = tm * BM;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / Q::WGN, wn = wave % Q::WGN;
+  const int steps = p.k / Q::BK;
+  const int cs = S > 1 ? p.sk_cs : steps;
+  const int s0 = kc * cs, s1 = min(s0 + cs, steps);  // this workgroup's K steps
+  if (s0 >= s1) return;
+  const typename Q::Src src = Q::source(p, mt, b, n0, m0, lane, wave);
+  const typename Q::Lane L = Q::lane_offsets(lane);
+
+  f32x4 acc[Q::TM][Q::TN];
+#pragma unroll
+  for (int a = 0; a < Q::TM; ++a)
+#pragma unroll
+    for (int c = 0; c < Q::TN; ++c) acc[a][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // prologue: steps s0 .. s0 + 2 in flight, step s0 landed and its first
+  // fragments read
+  // Q8: the tile's row scales go to LDS with the first step (waves 0 and 1:
+  // rows 0-63 and 64-127, or the gate and up rows of a pair)
+  if constexpr (FMT == kQ8)
+    if (S == 1 && wave < 2) dma<4>(src.sr, lds_addr(qs) + wave * 512, src.os);
+  Q::issue(src, lds_addr(st0), wave, s0);
+  if (s0 + 1 < s1) Q::issue(src, lds_addr(st1), wave, s0 + 1);
+  if (s0 + 2 < s1) Q::issue(src, lds_addr(st2), wave, s0 + 2);
+  if (s0 + 2 < s1)
+    wait_vm<2 * Q::NL>();  // (the row scales, issued first, have landed too)
+  else if (s0 + 1 < s1)
+    wait_vm<Q::NL>();
+  else
+    wait_vm<0>();
+  bar();
+  typename Q::Frag f;
+  Q::read_a(st0, L, wm, 0, f.a);
+  Q::read_b(st0, L, wn, f);
+  // three steps per iteration: the stages rotate with compile-time names
+  int st = s0;
+  for (int it = (s1 - s0) / 3; it > 0; --it) {
+    qgemm_dl_step<Q>(src, L, st0, st1, wave, wm, wn, st, s1, f, acc);
+    qgemm_dl_step<Q>(src, L, st1, st2, wave, wm, wn, st + 1, s1, f, acc);
+    qgemm_dl_step<Q>(src, L, st2, st0, wave, wm, wn, st + 2, s1, f, acc);
+    st += 3;
+  }
+  const int tail = s1 - st;
+  if (tail >= 1) qgemm_dl_step<Q>(src, L, st0, st1, wave, wm, wn, st, s1, f, acc);
+  if (tail >= 2) qgemm_dl_step<Q>(src, L, st1, st2, wave, wm, wn, st + 1, s1, f, acc);
+  if (S == 1) {
+    wait_lgkm0();  // the last fragments are read before the stages become C
+    bar();
+    Q::finish(p, mt, b, n0, m0, threadIdx.x, lane, wm, wn, acc, (float*)lds, qs);
+  } else
+    Q::spill(p, mt, b, n0, m0, lane, wm, wn, kc, acc);
+}
+
+}  // namespace aexq

@@ -1,4 +1,5 @@
-"""GPU parity of the tiled GEMM path (M > 32 activation rows, aexq_qgemm.hpp)
+"""GPU parity of the tiled GEMM path (M > 32 activation rows: aexq_qgemm_dl.hpp, the
+LDS-direct kernel, and aexq_qgemm.hpp, the register-staged one)
 against the CPU oracle, through the C ABI.
 
 Bars as in the other parity tests: normwise max|y - r| / max|r| <= 1e-3 of the
@@ -225,7 +226,10 @@ def test_gemm_group16(ctx, aexq, orc, monkeypatch, scale_f16, n, k, m, swiglu, s
         wu, uf = _weight(ctx, aexq, orc, 4, n, k, 93 + m, group=16, scale_f16=scale_f16, code=0)
         kw = dict(up=wu)
     plan = ctx.plan_check(w, xd, yd, **kw)
-    assert plan.startswith("kernel=qgemm") and "bm=64" in plan, plan
+    # fp16 scales (all small) take the LDS-direct split-scale kernel, fp32 the
+    # per-group fp32 scaling of the 64-row register-staged one
+    assert plan.startswith("kernel=qgemm"), plan
+    assert ("direct=1" in plan) == scale_f16 and (scale_f16 or "bm=64" in plan), plan
     ctx.linear(w, xd, yd, **kw)
     torch.cuda.synchronize()
     g = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
@@ -296,3 +300,58 @@ def test_gemm_q4_scale_above_bound_keeps_group_scaling(ctx, aexq, orc):
     torch.cuda.synchronize()
     ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
     assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
+
+
+@pytest.mark.parametrize("bits,group", [(8, 0), (4, 32), (4, 16)])
+@pytest.mark.parametrize("k", [64, 128, 192, 320])
+@pytest.mark.parametrize("m", [40, 100])
+def test_gemm_direct_step_counts(ctx, aexq, orc, bits, group, k, m):
+    """The LDS-direct kernel runs its K steps three per loop iteration with a
+    tail of one or two: 1, 2, 3 and 5 steps, on 64-row (M = 40) and 128-row
+    (M = 100) tiles, two weight tiles with the second one partial."""
+    _announce(f"qgemm direct q{bits} g={group} k={k} m={m}")
+    from aiimage_amd import synth
+    n = 200
+    w, wf = _weight(ctx, aexq, orc, bits, n, k, 7 * k + m + bits, group=group or k, code=0)
+    x16 = synth.activations(m, k, k + m)
+    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    plan = ctx.plan_check(w, xd, yd)
+    assert "direct=1" in plan and f"bm={64 if m <= 64 else 128}" in plan, plan
+    ctx.linear(w, xd, yd)
+    torch.cuda.synchronize()
+    stride = aexq.storage_elements(aexq.LAYOUT_PACK4_LINEAR, m, n)
+    got = y.cpu().numpy().reshape(m, stride)
+    assert np.all(got[:, n:] == 0)
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    assert normwise(got[:, :n], ref) <= TOL32
+
+
+@pytest.mark.parametrize("bits,group", [(8, 0), (4, 16)])
+@pytest.mark.parametrize("m", [40, 100])
+def test_gemm_direct_pair_matches_register_staged(ctx, aexq, orc, monkeypatch, bits, group, m):
+    """gate/up pairs on the LDS-direct kernel against the oracle, and against
+    the register-staged kernel (AEXQ_QGEMM_DL=0) on the same inputs."""
+    _announce(f"qgemm direct pair q{bits} g={group} m={m}")
+    from aiimage_amd import synth
+    n, k = 320, 256
+    wg, gf = _weight(ctx, aexq, orc, bits, n, k, 301 + m, group=group or k, code=0)
+    wu, uf = _weight(ctx, aexq, orc, bits, n, k, 302 + m, group=group or k, code=0)
+    x16 = synth.activations(m, k, 303)
+    xd = aexq.describe(dev(x16), m, k)
+    outs = []
+    for dl in ("1", "0"):
+        monkeypatch.setenv("AEXQ_QGEMM_DL", dl)
+        y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+        yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+        plan = ctx.plan_check(wg, xd, yd, up=wu)
+        assert plan.startswith("kernel=qgemm") and f"direct={dl}" in plan, plan
+        ctx.linear(wg, xd, yd, up=wu)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy().reshape(m, -1)[:, :n].astype(np.float64))
+    g = orc.gemm_gpu_semantics(x16.astype(np.float32), gf)
+    u = orc.gemm_gpu_semantics(x16.astype(np.float32), uf)
+    ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32)) for r in range(m)])
+    assert normwise(outs[0], ref) <= TOL32
+    assert normwise(outs[0], outs[1]) <= TOL32

@@ -129,6 +129,8 @@ def test_tied_alias_embedding_and_lm_head(ctx, aexq, orc):
     owner.release()
 
 
+# the refused capture below launches nothing, so torch warns that its graph is empty
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
 def test_graph_replays_after_scratch_growth(ctx, aexq, orc):
     _announce("graph replay after the context's scratch grows; growth under capture refused")
     from aiimage_amd import _abi, synth
