@@ -32,8 +32,9 @@
 // stored per 16-row block in read order (Q8: [16-byte quarter][row]; Q4:
 // [half][row]), so a fragment read is one contiguous run.
 //
-// Waves: BM = 128 as 2 x 2 (64 activation rows by 64 weight rows each),
-// BM = 64 as 1 x 4 (64 by 32): four 16-row A blocks per wave either way.
+// Waves: 1 x 4, each every activation row of the tile by 32 weight rows, so
+// a code fragment is expanded to fp16 once per workgroup (a 2 x 2 layout
+// expands every B block in two waves: Q4 at M = 512 measured 7% slower).
 // Inside a step the barrier sits between the two K halves: the first half's
 // MFMAs cover the second half's fragment reads and the barrier wait, the
 // second half's MFMAs cover the next step's first fragment reads.
@@ -125,10 +126,10 @@ struct QGemmDL {
   static constexpr int BN = 128;                  // weight rows of a tile
   static constexpr int BK = 64;                   // K per step
   static constexpr int NOUT = PAIR ? BN / 2 : BN;  // output columns of a tile
-  static constexpr int WGN = BM == 128 ? 2 : 4;   // waves across the weight rows
-  static constexpr int WR = BN / WGN;             // weight rows per wave
-  static constexpr int TN = WR / 16;              // 16-row B blocks per wave
-  static constexpr int TM = 4;                    // 16-row A blocks per wave (64 rows)
+  static constexpr int WGN = 4;                   // waves across the weight rows
+  static constexpr int WR = BN / WGN;             // weight rows per wave (32)
+  static constexpr int TN = WR / 16;              // 16-row B blocks per wave (2)
+  static constexpr int TM = BM / 16;              // 16-row A blocks per wave (every row)
   static constexpr int CP = FMT == kQ8 ? 64 : 32;  // code bytes per row and step
   static constexpr int A_BYTES = BM * 128;
   static constexpr int B_BYTES = BN * CP;
@@ -374,18 +375,16 @@ struct QGemmDL {
                             SF16);
       }
     }
-#pragma unroll 1
+#pragma unroll
     for (int h = 0; h < BM / 64; ++h) {
       if (h > 0) bar();  // every thread has read the previous half
-      if (wm == h) {
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
+      for (int tq = 0; tq < 4; ++tq)
 #pragma unroll
-          for (int tn = 0; tn < TN; ++tn)
+        for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              C[(16 * tm + 4 * lk + r) * CW + brow(wn, tn) + l16] = acc[tm][tn][r];
-      }
+          for (int r = 0; r < 4; ++r)
+            C[(16 * tq + 4 * lk + r) * CW + brow(wn, tn) + l16] = acc[4 * h + tq][tn][r];
       wait_lgkm0();
       bar();
 #pragma unroll 1
