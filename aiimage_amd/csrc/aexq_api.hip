@@ -99,7 +99,6 @@ struct aexq_weight {
   long long code_stride = 0;   // bytes between copies
   long long scale_stride = 0;  // bytes between copies
   bool owns = true;
-  bool scales_small = false;   // fp16 scales, all finite with |s| <= 4096 (split-scale GEMM)
 };
 
 static long long round_up(long long v, long long a) { return (v + a - 1) / a * a; }
@@ -284,13 +283,6 @@ static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const 
     const uint32_t* in = (const uint32_t*)packed;
     for (long long i = 0; i < nw; ++i) recoded[(size_t)i] = in[i] ^ flip;
     src = recoded.data();
-  }
-  if (scale_dtype == AEXQ_DTYPE_F16) {
-    // |s| <= 4096 (bits 0x6C00): q * s_hi stays inside fp16 for every code
-    const uint16_t* sb = (const uint16_t*)scales;
-    bool small = true;
-    for (long long i = 0; i < w->scale_count && small; ++i) small = (sb[i] & 0x7FFFu) <= 0x6C00u;
-    w->scales_small = small;
   }
   hipError_t e = hipMemcpy(w->codes, src, w->code_bytes, hipMemcpyHostToDevice);
   if (e == hipSuccess)
@@ -778,7 +770,7 @@ struct Plan {
 // the split a handful of workgroups would walk all of K on a 256-CU part.
 // AEXQ_SPLITK=n forces n chunks (1: no split).
 static void pick_split(long long units, int steps, long long slots, double step_us,
-                       double plane_bytes, int* chunks, int* cs) {
+                       double wg_us, int max_chunks, double plane_bytes, int* chunks, int* cs) {
   constexpr double kFixupUs = 5.0;         // the fix-up launch and its round trips
   constexpr double kPartBytesPerUs = 5e6;  // partial planes written and read back
   constexpr double kMaxPartBytes = 256.0 * 1024 * 1024;
@@ -801,10 +793,10 @@ static void pick_split(long long units, int steps, long long slots, double step_
     const int w = (steps + c - 1) / c;  // steps per chunk
     const int n = (steps + w - 1) / w;  // chunks that takes
     if (n != c) continue;               // same chunking as a smaller count
-    if (n > 1 && n * plane_bytes > kMaxPartBytes) break;
+    if (n > 1 && (n * plane_bytes > kMaxPartBytes || n > max_chunks)) break;
     const long long work = units * n;
     const long long rounds = (work + slots - 1) / slots;
-    double t = (double)rounds * w * step_us;
+    double t = (double)rounds * (w * step_us + wg_us);
     if (n > 1) t += kFixupUs + n * plane_bytes * 2.0 / kPartBytesPerUs;
     if (c == 1 || t < best) {
       best = t;
@@ -1038,26 +1030,15 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   const bool gemm_ok = M > 32 && K % 64 == 0 && (fmt == kQ8 || w0->block % 32 == 0 || g16) &&
                        (rms_in || x_ok) && getenv("AEXQ_QGEMM_OFF") == nullptr;
   if (gemm_ok && size_ok && !argmax) {
-    // Q4 takes 128-row tiles only with split fp16 scales (its per-group
-    // scaling otherwise needs the registers the larger tile's accumulators take)
-    bool small = fmt == kQ4 && w0->scale_dtype == AEXQ_DTYPE_F16 && (!swiglu || a.up->scales_small);
-    for (int i = 0; i < count; ++i) small = small && ws[i]->scales_small;
-    const bool split = small && !g16 && M > 64 && getenv("AEXQ_QGEMM_NOSPLIT") == nullptr;
-    int bm = (M <= 64 || (fmt == kQ4 && !split)) ? 64 : 128;
-    const char* benv = getenv("AEXQ_QGEMM_BM");  // tuning override: 64 or 128
-    if (benv && (atoi(benv) == 64 || atoi(benv) == 128) && !split) bm = atoi(benv);
-    QgemmConfig gc{fmt, bm, swiglu, w0->scale_dtype == AEXQ_DTYPE_F16, split, g16, false};
-    // the LDS-direct pipeline: Q8, and Q4 whose fp16 scales split exactly in
-    // groups of 16 or 32 (AEXQ_QGEMM_DL=0: the register-staged kernel)
-    const char* dlenv = getenv("AEXQ_QGEMM_DL");
-    const bool dl = !(dlenv && atoi(dlenv) == 0) &&
-                    (fmt == kQ8 || (small && (w0->block == 16 || w0->block == 32) &&
-                                    getenv("AEXQ_QGEMM_NOSPLIT") == nullptr));
-    if (dl) {
-      gc.bm = M <= 64 ? 64 : 128;
-      if (benv && (atoi(benv) == 64 || atoi(benv) == 128)) gc.bm = atoi(benv);
-      gc.split = fmt == kQ4;
-      gc.direct = true;
+    const bool sf16 = w0->scale_dtype == AEXQ_DTYPE_F16;
+    // the LDS-direct kernel: Q8 and Q4 groups of 16 or 32; larger Q4 groups
+    // (multiples of 32) the register-staged one, 64-row tiles
+    QgemmConfig gc{fmt, 64, swiglu, sf16, false, false};
+    if (fmt == kQ8 || w0->block == 16 || w0->block == 32) {
+      int bm = M <= 64 ? 64 : 128;
+      const char* benv = getenv("AEXQ_QGEMM_BM");  // tuning override: 64 or 128
+      if (benv && (atoi(benv) == 64 || atoi(benv) == 128)) bm = atoi(benv);
+      gc = QgemmConfig{fmt, bm, swiglu, sf16, g16, true};
     }
     plan->gentry = qgemm_find(gc);
     if (plan->gentry) {
@@ -1210,10 +1191,21 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     const int mtiles = (M + bm - 1) / bm;
     plan->mblock = bm;
     const long long slots = (long long)qgemm_blocks_per_cu(plan->gentry) * ctx->cus;
-    // per-step times measured on single-layer launches (graph replays)
-    const double step_us = fmt == kQ4 ? (bm == 128 ? 1.35 : (g16 ? 1.1 : 0.9))
-                                      : (bm == 128 ? 1.0 : 0.66);
-    pick_split((long long)tiles_total * mtiles, K / 64, slots, step_us,
+    // per-step and per-workgroup (prologue, epilogue or partial spill) times
+    // measured on single-layer launches (graph replays) and s_memrealtime
+    // stamps of the LDS-direct kernel
+    double step_us, wg_us = 0.0;
+    if (plan->gentry->cfg.direct) {
+      step_us = fmt == kQ8 ? (bm == 128 ? 0.9 : 0.6)
+                           : (g16 ? (bm == 128 ? 2.0 : 1.4) : (bm == 128 ? 1.4 : 1.0));
+      wg_us = 3.0;
+    } else {
+      step_us = 0.9;
+    }
+    // (at most 8 chunks for the LDS-direct kernel: single layers at M = 64
+    // and 512 measured fastest at 4 to 8, slower at 14 to 28)
+    pick_split((long long)tiles_total * mtiles, K / 64, slots, step_us, wg_us,
+               plan->gentry->cfg.direct ? 8 : 1 << 30,
                (double)M * nw * tiles_total * plan->rows_per_tile * 4.0,
                &plan->sk_chunks, &plan->sk_cs);
     plan->grid = (int)(((long long)tiles_total + 7) / 8 * 8 * mtiles * plan->sk_chunks);
@@ -1228,7 +1220,7 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     const bool wide = plan->mentry->cfg.wide;
     if (!plan->mentry->cfg.argmax)
       pick_split(tiles_total, K / (wide ? 256 : 128), wide ? cap : cap * kWaves,
-                 wide ? (fmt == kQ4 ? 2.2 : 1.15) : 1.0,
+                 wide ? (fmt == kQ4 ? 2.2 : 1.15) : 1.0, 0.0, 1 << 30,
                  (double)M * nw * tiles_total * plan->rows_per_tile * 4.0, &plan->sk_chunks,
                  &plan->sk_cs);
     const long long items = (long long)tiles_total * plan->sk_chunks;
@@ -1395,11 +1387,11 @@ extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, cons
       snprintf(diag, diag_len, "%s", g_last_error.c_str());
     else if (plan.kind == kPlanGemm)
       snprintf(diag, diag_len,
-               "kernel=qgemm bits=%d bm=%d swiglu=%d split=%d direct=%d rms_prepass=%d tiles=%d "
-               "grid=%d splitk=%d",
+               "kernel=qgemm bits=%d bm=%d swiglu=%d direct=%d rms_prepass=%d tiles=%d grid=%d "
+               "splitk=%d",
                w->bits, plan.gentry->cfg.bm, (int)plan.gentry->cfg.pair,
-               (int)plan.gentry->cfg.split, (int)plan.gentry->cfg.direct, (int)plan.rms_prepass,
-               plan.p.total_tiles, plan.grid, plan.sk_chunks);
+               (int)plan.gentry->cfg.direct, (int)plan.rms_prepass, plan.p.total_tiles, plan.grid,
+               plan.sk_chunks);
     else if (plan.kind == kPlanMfma)
       snprintf(diag, diag_len, "kernel=qmm bits=%d mt=%d nt=%d swiglu=%d wide=%d rms_prepass=%d "
                "tiles=%d grid=%d mblock=%d splitk=%d",

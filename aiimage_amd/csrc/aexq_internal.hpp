@@ -159,7 +159,6 @@ hipError_t qmm_launch(const QmmEntry* e, const QmvParams& p, int grid, hipStream
 struct QgemmConfig {
   int fmt, bm;
   bool pair, sf16;
-  bool split;  // Q4 fp16 scales folded into B as exact hi + lo parts (|scale| <= 4096)
   bool g16;    // Q4 with one scale per 16 codes
   bool direct; // LDS-direct pipeline (Q8; Q4 split scales in groups of 16 or 32)
 };

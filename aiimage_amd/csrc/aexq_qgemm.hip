@@ -1,41 +1,32 @@
-// Instantiations of the tiled quantized GEMM (aexq_qgemm.hpp) and its table:
-// Q8 with one scale per row and Q4 with one scale per multiple of 32 codes,
-// fp16 or fp32 scales, single weights or SwiGLU pairs; 64-row activation
-// tiles (Q4, Q8) and 128-row tiles (Q8; Q4 with split fp16 scales).
+// Instantiations of the tiled quantized GEMM and its table: the LDS-direct
+// kernel (aexq_qgemm_dl.hpp) for Q8 with one scale per row and Q4 with one
+// scale per 16 or 32 codes, the register-staged one (aexq_qgemm.hpp) for Q4
+// with one scale per larger multiple of 32; fp16 or fp32 scales, single
+// weights or SwiGLU pairs.
 #include "aexq_qgemm.hpp"
 #include "aexq_qgemm_dl.hpp"
 
 namespace aexq {
 
-#define QGEG(FMT, BM, PAIR, SF16, SPLIT, G16)                                 \
+// the register-staged kernel: Q4 with scale groups of 64 or more codes
+#define QGE(PAIR, SF16)                                                       \
   QgemmEntry {                                                                \
-    QgemmConfig{FMT, BM, PAIR, SF16, SPLIT, G16, false},                      \
-        &qgemm_kernel<FMT, BM, PAIR, SF16, SPLIT, G16>                        \
+    QgemmConfig{kQ4, 64, PAIR, SF16, false, false}, &qgemm_kernel<PAIR, SF16> \
   }
-// LDS-direct forms: 128-row tiles two workgroups per CU, 64-row tiles three
+// LDS-direct forms (aexq_qgemm_dl.hpp): Q8; Q4 in groups of 16 or 32; fp16
+// or fp32 scales; 128-row tiles two workgroups per CU, 64-row tiles three
 #define QGDL(FMT, BM, PAIR, SF16, G)                                          \
   QgemmEntry {                                                                \
-    QgemmConfig{FMT, BM, PAIR, SF16, FMT == kQ4, G == 16, true},              \
+    QgemmConfig{FMT, BM, PAIR, SF16, G == 16, true},                          \
         &qgemm_dl_kernel<FMT, BM, PAIR, SF16, G, BM == 128 ? 2 : 3>           \
   }
-#define QGDL_BM(BM)                                                            \
-  QGDL(kQ8, BM, false, true, 0), QGDL(kQ8, BM, false, false, 0),              \
-      QGDL(kQ8, BM, true, true, 0), QGDL(kQ8, BM, true, false, 0),            \
-      QGDL(kQ4, BM, false, true, 32), QGDL(kQ4, BM, true, true, 32),          \
-      QGDL(kQ4, BM, false, true, 16), QGDL(kQ4, BM, true, true, 16)
-#define QGE(FMT, BM, PAIR, SF16, SPLIT) QGEG(FMT, BM, PAIR, SF16, SPLIT, false)
+#define QGDL_PS(FMT, BM, G)                                                    \
+  QGDL(FMT, BM, false, true, G), QGDL(FMT, BM, false, false, G),              \
+      QGDL(FMT, BM, true, true, G), QGDL(FMT, BM, true, false, G)
+#define QGDL_BM(BM) QGDL_PS(kQ8, BM, 0), QGDL_PS(kQ4, BM, 32), QGDL_PS(kQ4, BM, 16)
 
-#define QG_BM(FMT, BM) \
-  QGE(FMT, BM, false, true, false), QGE(FMT, BM, false, false, false), \
-      QGE(FMT, BM, true, true, false), QGE(FMT, BM, true, false, false)
-
-// Q4 with fp16 scales split into B (128-row tiles): single weights and pairs;
-// Q4 with 16-code groups (64-row tiles)
-static const QgemmEntry kTableG[] = {
-    QG_BM(kQ4, 64), QG_BM(kQ8, 64), QG_BM(kQ8, 128), QGE(kQ4, 128, false, true, true),
-    QGE(kQ4, 128, true, true, true), QGEG(kQ4, 64, false, true, false, true),
-    QGEG(kQ4, 64, false, false, false, true), QGEG(kQ4, 64, true, true, false, true),
-    QGEG(kQ4, 64, true, false, false, true), QGDL_BM(64), QGDL_BM(128)};
+static const QgemmEntry kTableG[] = {QGE(false, true), QGE(false, false), QGE(true, true),
+                                     QGE(true, false), QGDL_BM(64), QGDL_BM(128)};
 
 static constexpr int kCountG = (int)(sizeof(kTableG) / sizeof(kTableG[0]));
 
@@ -43,7 +34,7 @@ const QgemmEntry* qgemm_find(const QgemmConfig& c) {
   for (int i = 0; i < kCountG; ++i) {
     const QgemmConfig& q = kTableG[i].cfg;
     if (q.fmt == c.fmt && q.bm == c.bm && q.pair == c.pair && q.sf16 == c.sf16 &&
-        q.split == c.split && q.g16 == c.g16 && q.direct == c.direct)
+        q.g16 == c.g16 && q.direct == c.direct)
       return &kTableG[i];
   }
   return nullptr;

@@ -1,38 +1,23 @@
-// Tiled quantized GEMM for M > 32 activation rows on gfx950 MFMA:
-// Y[M][N] = X[M][K] W[N][K]^T for Q8 with one scale per row and Q4 with one
-// scale per multiple of 32 codes, K a multiple of 64.
+// Tiled quantized GEMM for M > 32 activation rows, register-staged: Q4 with
+// one scale per larger multiple of 32 codes (64, 96, ...; the LDS-direct
+// kernel of aexq_qgemm_dl.hpp covers Q8 and groups of 16 or 32), K a
+// multiple of 64.  Y[M][N] = X[M][K] W[N][K]^T.
 //
-// A workgroup owns one output tile: BM activation rows by 128 weight rows (a
+// A workgroup owns one output tile: 64 activation rows by 128 weight rows (a
 // SwiGLU pair: 64 gate rows and the same 64 up rows).  Per 64-wide K step its
 // 256 threads fetch the step's codes once -- each thread the 32 codes of one
-// row that one 16-byte (Q4) or two (Q8) loads bring -- and store them in LDS
-// as they are (in fragment order), beside the step's activation tile.  The four waves (2 x 2, each
-// BM/2 rows by 64 weight rows) read their MFMA B fragments as raw codes (8
-// bytes per lane for Q8, 4 for Q4: LDS carries a half or a quarter of what
-// fp16 weights would), expand them to exact fp16 integers in registers and run
-// v_mfma_f32_16x16x32_f16.  Q4 nibbles expand in (p, p + 4) pair order, so the
-// Q4 activation tile is stored in that order too (the products pair up as in
-// K order).  One Q4 scale group is one MFMA K extent: a group's product is
-// scaled in fp32 into the accumulator, so the dequantised weight stays exactly
-// float(q) * scale; Q8 accumulates the whole row in the MFMA and applies its
-// row scale once.  With SPLIT (Q4, fp16 scales of magnitude <= 4096) the scale
-// goes into B instead: s = s_hi + s_lo with s_hi the top 7 significand bits,
-// and q * s_hi, q * s_lo are exact fp16 values (|q| <= 8 has at most 3
-// significant bits), so two MFMAs accumulate x * (q * s) exactly in the fp32
-// accumulator with no per-output scaling -- the B expansion is shared by the
-// tile's BM / 32 A blocks, where the per-group FMAs were per output.  Global
-// loads are issued two steps ahead of the MFMAs (two register sets); LDS is
-// double-buffered with one barrier per step.  (In the conditional loop the
-// compiler's wait before each LDS store also covers the loads issued just
-// before it; the exact-wait form measured slower for these tiles.)
+// row that one 16-byte load brings -- and store them in LDS as they are (in
+// fragment order), beside the step's activation tile.  The four waves (2 x 2,
+// each 32 rows by 64 weight rows) read their MFMA B fragments as raw codes (4
+// bytes per lane), expand them to exact fp16 integers in registers and run
+// v_mfma_f32_16x16x32_f16.  Nibbles expand in (p, p + 4) pair order, so the
+// activation tile is stored in that order too (the products pair up as in K
+// order).  One 32-code MFMA K extent lies inside one scale group: its product
+// is scaled in fp32 into the accumulator, so the dequantised weight stays
+// exactly float(q) * scale.  Global loads are issued two steps ahead of the
+// MFMAs (two register sets); LDS is double-buffered with one barrier per step.
 //
-// G16 (Q4 with one scale per 16 codes, the reference's shipping format): an
-// MFMA K extent holds two groups, lanes l / 16 = 0, 1 the first and 2, 3 the
-// second; two MFMAs, each with the other group's lanes' codes zeroed, give
-// the two groups' products, each scaled in fp32 into the accumulator -- the
-// same exact float(q) * scale at twice the MFMA work.
-//
-// Workgroup b runs on XCD b % 8: the numbering puts the BM-row tiles of one
+// Workgroup b runs on XCD b % 8: the numbering puts the row tiles of one
 // weight tile on one XCD, whose L2 then fetches that weight tile once.
 //
 // MFMA 16x16x32 f16 lane layout (lane l): A[l % 16][8 (l / 16) + j],
@@ -43,11 +28,9 @@
 
 namespace aexq {
 
-template <int FMT, int BM, bool PAIR, bool SF16, bool SPLIT, bool G16>
+template <bool PAIR, bool SF16>
 struct QGemm {
-  static_assert(!SPLIT || (FMT == kQ4 && SF16), "split scales are for Q4 with fp16 scales");
-  static_assert(!G16 || (FMT == kQ4 && !SPLIT), "16-code groups are a Q4 per-group form");
-  static constexpr int GS = G16 ? 4 : 2;             // Q4 scale groups per K step
+  static constexpr int BM = 64;                      // activation rows of a tile
   static constexpr int BN = 128;                     // weight rows of a tile
   static constexpr int BK = 64;                      // K per step
   static constexpr int NOUT = PAIR ? BN / 2 : BN;    // output columns of a tile
@@ -60,16 +43,15 @@ struct QGemm {
   //   kk * KB + (row / 16) * 64 P + lk * 16 P + (row % 16) * P,
   // so the 64 lanes of a fragment read take one contiguous run, and group 1
   // is skewed by 64 bytes so the two groups' stores fall on different banks.
-  static constexpr int P = FMT == kQ8 ? 8 : 4;
+  static constexpr int P = 4;
   static constexpr int KB = (BN / 16) * 64 * P + 64;
   static constexpr int CB = 2 * KB;  // bytes of one code buffer
   static constexpr int XV = BM * BK / 8 / kThreads;  // 16-byte activation loads per thread
-  static constexpr int CV = FMT == kQ8 ? 2 : 1;      // 16-byte code loads per thread
 
   struct Regs {
     u32x4 x[XV];
-    u32x4 c[CV];
-    uint32_t s[G16 ? 2 : 1];  // Q4: raw bits of the thread's group scale(s)
+    u32x4 c;
+    uint32_t s;  // raw bits of the thread's group scale
   };
 
   // Per-workgroup resources of one tile (wave-uniform).
@@ -78,7 +60,7 @@ struct QGemm {
     int rs2;   // bytes between activation rows
     int rb;    // code bytes per weight row
     int brl;   // this thread's row inside its weight resource
-    int sub;   // Q4: group of the step; Q8: half of the step's codes
+    int sub;   // the thread's 32-code half of the step
   };
 
   // Weight rows of B block tn for wave column wn (rows of the tile's LDS block).
@@ -94,7 +76,7 @@ struct QGemm {
     const bool up = PAIR && wave >= 2;    // rows 64..127 of a pair tile: the up weight
     s.sub = tid & 1;
     s.brl = PAIR ? (row & 63) : row;
-    s.rb = FMT == kQ8 ? p.k : p.k / 2;
+    s.rb = p.k / 2;
     constexpr int sb = SF16 ? 2 : 4;
     const int rows = mt.n > n0 ? min(mt.n - n0, NOUT) : 0;
     const char* wb = (const char*)(up ? mt.w2 : mt.w) + (long long)b * mt.w_bstride * 4 +
@@ -102,8 +84,7 @@ struct QGemm {
     s.wr = __builtin_amdgcn_make_buffer_rsrc((void*)wb, (short)0, rows * s.rb, kBufferRsrcWord3);
     const char* sp = (const char*)(up ? mt.s2 : mt.s) +
                      ((long long)b * mt.s_bstride + (long long)n0 * p.groups_per_row) * sb;
-    s.sr = __builtin_amdgcn_make_buffer_rsrc((void*)sp, (short)0,
-                                             FMT == kQ8 ? 0 : rows * p.groups_per_row * sb,
+    s.sr = __builtin_amdgcn_make_buffer_rsrc((void*)sp, (short)0, rows * p.groups_per_row * sb,
                                              kBufferRsrcWord3);
     s.rs2 = (int)(p.x_rstride * 2);
     const char* xb = (const char*)mt.x + (long long)b * mt.x_bstride * 2 + (long long)m0 * s.rs2;
@@ -129,38 +110,14 @@ struct QGemm {
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                      s.xr, oob + (c >> 3) * s.rs2 + (st * BK + (c & 7) * 8) * 2, 0, 0));
     }
-    if constexpr (FMT == kQ8) {
-#pragma unroll
-      for (int i = 0; i < CV; ++i)
-        r.c[i] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       s.wr, oob + s.brl * s.rb + st * BK + 32 * s.sub + 16 * i, 0, 0));
-      r.s[0] = 0;
-    } else {
-      r.c[0] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                     s.wr, oob + s.brl * s.rb + st * 32 + 16 * s.sub, 0, 0));
-      const int g = (st * BK + 32 * s.sub) / p.group;
-      const int si = oob / 4 + s.brl * p.groups_per_row + g;
-      if constexpr (G16) {
-        // the two 16-code groups of the thread's 32 codes (si even: aligned)
-        if constexpr (SF16) {
-          const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(s.sr, si * 2, 0, 0);
-          r.s[0] = v & 0xFFFFu;
-          r.s[1] = v >> 16;
-        } else {
-          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          const u32x2 v =
-              __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(s.sr, si * 4, 0, 0));
-          r.s[0] = v[0];
-          r.s[1] = v[1];
-        }
-      } else if constexpr (SF16) {
-        r.s[0] = __builtin_amdgcn_raw_buffer_load_b16(s.sr, si * 2, 0, 0);
-      } else {
-        r.s[0] = __builtin_amdgcn_raw_buffer_load_b32(s.sr, si * 4, 0, 0);
-      }
-    }
+    r.c = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                        s.wr, oob + s.brl * s.rb + st * 32 + 16 * s.sub, 0, 0));
+    const int g = (st * BK + 32 * s.sub) / p.group;
+    const int si = oob / 4 + s.brl * p.groups_per_row + g;
+    if constexpr (SF16)
+      r.s = __builtin_amdgcn_raw_buffer_load_b16(s.sr, si * 2, 0, 0);
+    else
+      r.s = __builtin_amdgcn_raw_buffer_load_b32(s.sr, si * 4, 0, 0);
   }
 
   // Stores a step's registers into LDS buffer (xs, wc, ss): the activation
@@ -170,39 +127,16 @@ struct QGemm {
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       const int c = tid + kThreads * v;
-      u32x4 xv = r.x[v];
-      if constexpr (FMT == kQ4) {
-        uint32_t xp[4];
-        q4_xpairs(xv[0], xv[1], xv[2], xv[3], xp);
-        xv = u32x4{xp[0], xp[1], xp[2], xp[3]};
-      }
-      *(u32x4*)&xs[(c >> 3) * LS + (c & 7) * 8] = xv;
+      const u32x4 xv = r.x[v];
+      uint32_t xp[4];
+      q4_xpairs(xv[0], xv[1], xv[2], xv[3], xp);
+      *(u32x4*)&xs[(c >> 3) * LS + (c & 7) * 8] = u32x4{xp[0], xp[1], xp[2], xp[3]};
     }
     const int row = tid >> 1, sub = tid & 1;  // the thread holds group `sub` of the step
     uint8_t* dst = wc + sub * KB + (row >> 4) * 64 * P + (row & 15) * P;
 #pragma unroll
-    for (int lk = 0; lk < 4; ++lk) {
-      if constexpr (FMT == kQ8) {
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const u32x4& c = r.c[lk >> 1];
-        *(u32x2*)&dst[lk * 16 * P] = u32x2{c[2 * (lk & 1)], c[2 * (lk & 1) + 1]};
-      } else {
-        *(uint32_t*)&dst[lk * 16 * P] = r.c[0][lk];
-      }
-    }
-    if constexpr (SPLIT) {
-      // (s_hi, s_lo): s_hi keeps the top 7 significand bits, s_lo = s - s_hi exactly
-      const f16 sv = __builtin_bit_cast(f16, (uint16_t)r.s[0]);
-      const f16 hi = __builtin_bit_cast(f16, (uint16_t)(r.s[0] & 0xFFF0u));
-      const f16 lo = sv - hi;
-      const f16x2 pr = {hi, lo};
-      ((uint32_t*)ss)[row * 2 + sub] = as_u(pr);
-    } else if constexpr (G16) {
-      ss[row * 4 + 2 * sub] = scale_of(r.s[0], SF16);
-      ss[row * 4 + 2 * sub + 1] = scale_of(r.s[1], SF16);
-    } else if constexpr (FMT == kQ4) {
-      ss[row * 2 + sub] = scale_of(r.s[0], SF16);
-    }
+    for (int lk = 0; lk < 4; ++lk) *(uint32_t*)&dst[lk * 16 * P] = r.c[lk];
+    ss[row * 2 + sub] = scale_of(r.s, SF16);
   }
 
   // The MFMAs of one step from LDS buffer (xs, wc, ss).
@@ -216,75 +150,15 @@ struct QGemm {
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
         a[tm] = *(const f16x8*)&xs[(wm * WM + 16 * tm + l16) * LS + 32 * kk + 8 * lk];
-      if constexpr (SPLIT) {
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn) {
-          const uint8_t* src =
-              wc + kk * KB + (brow(wn, tn) >> 4) * 64 * P + lk * 16 * P + l16 * P;
-          uint32_t e[4];
-          q4_pairs(*(const uint32_t*)src, e);
-          const f16x2 sp = as_h2(((const uint32_t*)ss)[(brow(wn, tn) + l16) * 2 + kk]);
-          const f16x2 shi = {sp[0], sp[0]}, slo = {sp[1], sp[1]};
-          const f16x8 bhi = pack8(as_u(as_h2(e[0]) * shi), as_u(as_h2(e[1]) * shi),
-                                  as_u(as_h2(e[2]) * shi), as_u(as_h2(e[3]) * shi));
-          const f16x8 blo = pack8(as_u(as_h2(e[0]) * slo), as_u(as_h2(e[1]) * slo),
-                                  as_u(as_h2(e[2]) * slo), as_u(as_h2(e[3]) * slo));
-#pragma unroll
-          for (int tm = 0; tm < TM; ++tm) {
-            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bhi, acc[tm][tn], 0, 0, 0);
-            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], blo, acc[tm][tn], 0, 0, 0);
-          }
-        }
-        continue;
-      }
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
         // codes 32 kk + 8 lk .. + 7 of row brow + l16
         const uint8_t* src = wc + kk * KB + (brow(wn, tn) >> 4) * 64 * P + lk * 16 * P + l16 * P;
-        if constexpr (FMT == kQ8) {
-          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          const u32x2 raw = *(const u32x2*)src;
-          uint32_t e0, e1, e2, e3;
-          q8_pairs(raw[0], e0, e1);
-          q8_pairs(raw[1], e2, e3);
-          bq[tn] = pack8(e0, e1, e2, e3);
-        } else {
-          uint32_t e[4];
-          q4_pairs(*(const uint32_t*)src, e);
-          bq[tn] = pack8(e[0], e[1], e[2], e[3]);
-        }
+        uint32_t e[4];
+        q4_pairs(*(const uint32_t*)src, e);
+        bq[tn] = pack8(e[0], e[1], e[2], e[3]);
       }
-      if constexpr (FMT == kQ8) {
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-          for (int tn = 0; tn < TN; ++tn)
-            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bq[tn], acc[tm][tn], 0, 0, 0);
-      } else if constexpr (G16) {
-        // group 2 kk in lanes lk < 2, group 2 kk + 1 in lanes lk >= 2
-        // one B block's two operands at a time (register budget)
-        const bool first = lk < 2;
-        const f16x8 zero = {};
-        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn) {
-          const float s0 = ss[(brow(wn, tn) + l16) * 4 + 2 * kk];
-          const float s1 = ss[(brow(wn, tn) + l16) * 4 + 2 * kk + 1];
-          const f16x8 b0 = first ? bq[tn] : zero;
-          const f16x8 b1 = first ? zero : bq[tn];
-#pragma unroll
-          for (int tm = 0; tm < TM; ++tm) {
-            const f32x4 t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], b0, z, 0, 0, 0);
-            const f32x4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], b1, z, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              acc[tm][tn][r] = fmaf(s0, t0[r], acc[tm][tn][r]);
-              acc[tm][tn][r] = fmaf(s1, t1[r], acc[tm][tn][r]);
-            }
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      } else {
+      {
         float sc[TN];
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) sc[tn] = ss[(brow(wn, tn) + l16) * 2 + kk];
@@ -302,13 +176,12 @@ struct QGemm {
     }
   }
 
-  // Row scale (Q8), epilogue and store of the finished tile.
+  // Epilogue and store of the finished tile.
   static __device__ __forceinline__ void finish(const QmvParams& p, const QmvMat& mt, int b,
                                                 int n0, int m0, int lane, int wm, int wn,
                                                 const f32x4 (&acc)[TM][TN]) {
     const int l16 = lane & 15, lk = lane >> 4;
     const bool yf32 = (p.flags & kFlagYf32) != 0;
-    constexpr int sb = SF16 ? 2 : 4;
     char* yb = (char*)mt.y + (long long)b * mt.y_bstride * (yf32 ? 4 : 2);
     const char* rb =
         mt.res ? (const char*)mt.res + (long long)b * mt.r_bstride * (yf32 ? 4 : 2) : nullptr;
@@ -316,15 +189,6 @@ struct QGemm {
 #pragma unroll
     for (int to = 0; to < TO; ++to) {
       const int n = n0 + (PAIR ? 32 * wn + 16 * to : 64 * wn + 16 * to) + l16;
-      float rs0 = 1.0f, rs1 = 1.0f;
-      if constexpr (FMT == kQ8) {
-        const char* s0 = (const char*)mt.s + (long long)b * mt.s_bstride * sb;
-        rs0 = n < mt.n ? load_scale(s0, n, SF16) : 0.0f;
-        if constexpr (PAIR) {
-          const char* s1 = (const char*)mt.s2 + (long long)b * mt.s_bstride * sb;
-          rs1 = n < mt.n ? load_scale(s1, n, SF16) : 0.0f;
-        }
-      }
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
@@ -333,9 +197,8 @@ struct QGemm {
           if (m < p.m && n < mt.n_store && mt.y) {
             float v = 0.0f;
             if (n < mt.n) {
-              v = gemm_epilogue(p, p.m_base + m, n, acc[tm][to][r] * rs0);
-              if constexpr (PAIR)
-                v = silu(v) * gemm_epilogue(p, p.m_base + m, n, acc[tm][to + 2][r] * rs1);
+              v = gemm_epilogue(p, p.m_base + m, n, acc[tm][to][r]);
+              if constexpr (PAIR) v = silu(v) * gemm_epilogue(p, p.m_base + m, n, acc[tm][to + 2][r]);
               if (rb && (p.flags & kFlagResidual)) {
                 const long long ri = (long long)m * p.r_rstride + n;
                 v += yf32 ? ((const float*)rb)[ri] : (float)((const f16*)rb)[ri];
@@ -378,13 +241,14 @@ struct QGemm {
   }
 };
 
-template <int FMT, int BM, bool PAIR, bool SF16, bool SPLIT, bool G16>
+template <bool PAIR, bool SF16>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void qgemm_kernel(const QmvParams p, int mtiles) {
-  using G = QGemm<FMT, BM, PAIR, SF16, SPLIT, G16>;
+  using G = QGemm<PAIR, SF16>;
+  constexpr int BM = G::BM;
   __shared__ __align__(16) f16 xs[2][BM * G::LS];
   __shared__ __align__(16) uint8_t ws[2][G::CB];
-  __shared__ float ss[2][FMT == kQ8 ? 1 : G::BN * G::GS];  // Q4 group scales of a step
+  __shared__ float ss[2][G::BN * 2];  // the group scales of a step
   // weight tile tn, row tile tm and K chunk kc of this workgroup (see the
   // header; the chunks of a split K sit next to each other on one XCD)
   // (readfirstlane: the tile coordinates are workgroup-uniform, so the buffer
@@ -423,54 +287,26 @@ void qgemm_kernel(const QmvParams p, int mtiles) {
     for (int c = 0; c < G::TN; ++c) acc[a][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   typename G::Regs ra, rb;
-  if constexpr (!G16) {
-    // Two register sets rotate: while LDS buffer (st & 1) is consumed, step
-    // st + 1 waits in one set (stored after the MFMAs) and step st + 2 is being
-    // fetched into the other, so a load has two steps of MFMAs to land.
-    G::load(p, src, s0, true, tid, ra);
-    if (s0 + 1 < s1) G::load(p, src, s0 + 1, true, tid, rb);
-    G::store(tid, ra, xs[0], ws[0], ss[0]);
+  // Two register sets rotate: while LDS buffer (st & 1) is consumed, step
+  // st + 1 waits in one set (stored after the MFMAs) and step st + 2 is being
+  // fetched into the other, so a load has two steps of MFMAs to land.
+  G::load(p, src, s0, true, tid, ra);
+  if (s0 + 1 < s1) G::load(p, src, s0 + 1, true, tid, rb);
+  G::store(tid, ra, xs[0], ws[0], ss[0]);
+  __syncthreads();
+  for (int st = s0;;) {
+    if (st + 2 < s1) G::load(p, src, st + 2, true, tid, ra);
+    __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the MFMAs
+    G::compute(lane, wm, wn, xs[0], ws[0], ss[0], acc);
+    if (st + 1 < s1) G::store(tid, rb, xs[1], ws[1], ss[1]);
     __syncthreads();
-    for (int st = s0;;) {
-      if (st + 2 < s1) G::load(p, src, st + 2, true, tid, ra);
-      __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the MFMAs
-      G::compute(lane, wm, wn, xs[0], ws[0], ss[0], acc);
-      if (st + 1 < s1) G::store(tid, rb, xs[1], ws[1], ss[1]);
-      __syncthreads();
-      if (++st >= s1) break;
-      if (st + 2 < s1) G::load(p, src, st + 2, true, tid, rb);
-      __builtin_amdgcn_sched_barrier(0);
-      G::compute(lane, wm, wn, xs[1], ws[1], ss[1], acc);
-      if (st + 1 < s1) G::store(tid, ra, xs[0], ws[0], ss[0]);
-      __syncthreads();
-      if (++st >= s1) break;
-    }
-  } else {
-    // Group 16: the same rotation in a counted loop, two steps per
-    // iteration, with loads and stores on every path (past the range they
-    // move zeros into the buffer that is no longer read): the compiler then
-    // needs 128 registers here instead of 236 (four workgroups per CU
-    // instead of two), and no wait before a store covers the loads issued
-    // after it.  Buffer 0 holds step st and rb step st + 1 at the loop head.
-    G::load(p, src, s0, true, tid, ra);
-    G::load(p, src, s0 + 1, s0 + 1 < s1, tid, rb);
-    G::store(tid, ra, xs[0], ws[0], ss[0]);
+    if (++st >= s1) break;
+    if (st + 2 < s1) G::load(p, src, st + 2, true, tid, rb);
+    __builtin_amdgcn_sched_barrier(0);
+    G::compute(lane, wm, wn, xs[1], ws[1], ss[1], acc);
+    if (st + 1 < s1) G::store(tid, ra, xs[0], ws[0], ss[0]);
     __syncthreads();
-    int st = s0;
-    for (int it = (s1 - s0) >> 1; it > 0; --it) {
-      G::load(p, src, st + 2, st + 2 < s1, tid, ra);
-      __builtin_amdgcn_sched_barrier(0);
-      G::compute(lane, wm, wn, xs[0], ws[0], ss[0], acc);
-      G::store(tid, rb, xs[1], ws[1], ss[1]);
-      __syncthreads();
-      G::load(p, src, st + 3, st + 3 < s1, tid, rb);
-      __builtin_amdgcn_sched_barrier(0);
-      G::compute(lane, wm, wn, xs[1], ws[1], ss[1], acc);
-      G::store(tid, ra, xs[0], ws[0], ss[0]);
-      __syncthreads();
-      st += 2;
-    }
-    if ((s1 - s0) & 1) G::compute(lane, wm, wn, xs[0], ws[0], ss[0], acc);
+    if (++st >= s1) break;
   }
   if (S == 1)
     G::finish(p, mt, b, n0, m0, lane, wm, wn, acc);

@@ -1,7 +1,7 @@
 // Tiled quantized GEMM for M > 32 activation rows with LDS-direct loads
 // (gfx950 `buffer_load_dwordx4 ... lds`): Y[M][N] = X[M][K] W[N][K]^T for Q8
-// with one scale per row and Q4 with fp16 scales of magnitude <= 4096 in
-// groups of 16 or 32 codes, K a multiple of 64.
+// with one scale per row and Q4 with one scale (fp16 or fp32) per 16 or 32
+// codes, K a multiple of 64.
 //
 // A workgroup owns one output tile: BM activation rows by 128 weight rows (a
 // SwiGLU pair: 64 gate rows and the same 64 up rows), 256 threads.  Each
@@ -12,19 +12,20 @@
 // holds a step in transit.  Three LDS stages rotate with one barrier per
 // step, so a step's loads have two steps of MFMAs to land.
 //
-// The K order inside a step is permuted: the MFMA's lane group g (l / 16)
+// Q8 permutes the K order inside a step: the MFMA's lane group g (l / 16)
 // carries codes 16 g .. 16 g + 15 of the step, the first eight in the step's
-// first MFMA K extent and the rest in the second.  A lane's codes then sit
-// together (Q8: one 16-byte read for both halves; Q4: one 8-byte read), and
-// the activation fragments are read in the same order.  The products are
-// those of K order, summed in another order inside fp32 accumulators.
+// first MFMA K extent and the rest in the second, so a lane's codes for both
+// extents are one 16-byte read, and the activation fragments are read in the
+// same order (the products of K order, summed in another order in fp32).
+// Q4 keeps K order inside each 32-code extent, so that an extent holds one
+// scale group of 32 or two of 16.
 //
 // Codes become exact fp16 integers in registers.  Q8 accumulates the row in
-// the MFMA and applies its row scale once at the end.  Q4 splits each fp16
-// scale s into s_hi (its top 7 significand bits) and s_lo = s - s_hi; q * s_hi
-// and q * s_lo are exact fp16 values (|q| <= 8), so two MFMAs accumulate
-// x * (q * s) exactly; a lane's 16 codes lie in one scale group for groups of
-// 16 and 32 alike.
+// the MFMA and applies its row scale once at the end.  Q4 scales each
+// group's product in fp32 into the accumulator (the dequantised weight is
+// exactly float(q) * scale): one MFMA per 32-code extent, or for groups of 16
+// two, each with the other group's lanes' codes zeroed.  (Folding fp16
+// scales into B as two exact fp16 parts measured slower: twice the MFMAs.)
 //
 // Activation rows are 128 bytes per step in LDS with their 16-byte chunks
 // XOR-swizzled by the row (chunk c of row r at slot c ^ ((r & 7) ^ ((r >> 3) & 1))),
@@ -120,26 +121,30 @@ __device__ __forceinline__ void q4_pairs_seq(uint32_t w, uint32_t q[4]) {
 
 template <int FMT, int BM, bool PAIR, bool SF16, int G>
 struct QGemmDL {
-  static_assert(FMT == kQ8 ? G == 0 : (SF16 && (G == 16 || G == 32)),
-                "Q8 (row scales) or Q4 with fp16 scales in groups of 16 or 32");
+  static_assert(FMT == kQ8 ? G == 0 : (G == 16 || G == 32),
+                "Q8 (row scales) or Q4 in groups of 16 or 32");
   static_assert(BM == 64 || BM == 128, "64- or 128-row activation tiles");
   static constexpr int BN = 128;                  // weight rows of a tile
   static constexpr int BK = 64;                   // K per step
   static constexpr int NOUT = PAIR ? BN / 2 : BN;  // output columns of a tile
-  static constexpr int WGN = 4;                   // waves across the weight rows
-  static constexpr int WR = BN / WGN;             // weight rows per wave (32)
+  static constexpr int WR = BN / 4;               // weight rows per wave (32)
   static constexpr int TN = WR / 16;              // 16-row B blocks per wave (2)
   static constexpr int TM = BM / 16;              // 16-row A blocks per wave (every row)
   static constexpr int CP = FMT == kQ8 ? 64 : 32;  // code bytes per row and step
   static constexpr int A_BYTES = BM * 128;
   static constexpr int B_BYTES = BN * CP;
-  static constexpr int S_BYTES = FMT == kQ8 ? 0 : 1024;
-  static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+  static constexpr int SPR = FMT == kQ8 ? 0 : BK / G;    // Q4 scales per row and step
+  static constexpr int SB = SF16 ? 2 : 4;                // bytes per scale
+  static constexpr int S_BYTES = FMT == kQ8 ? 0 : BN * SPR * SB;
+  static constexpr int S_AREA = FMT == kQ8 ? 0 : (S_BYTES < 1024 ? 1024 : S_BYTES);
+  static constexpr int STAGE = A_BYTES + B_BYTES + S_AREA;
   static constexpr int A_INST = A_BYTES / 1024 / 4;  // direct loads per wave and step
   static constexpr int B_INST = B_BYTES / 1024 / 4;
-  static constexpr int S_INST = FMT == kQ8 ? 0 : 1;
+  // dword loads of the step's scales per wave (256 bytes each; with 512
+  // bytes of scales waves 2 and 3 load past the resource into spare LDS)
+  static constexpr int S_INST = FMT == kQ8 ? 0 : (S_BYTES <= 1024 ? 1 : S_BYTES / 1024);
+  static constexpr int S_RPI = FMT == kQ8 ? 1 : 256 / (SPR * SB);  // rows per scale load
   static constexpr int NL = A_INST + B_INST + S_INST;
-  static constexpr int SPR = FMT == kQ8 ? 0 : BK / G;  // scales per row and step
 
   // Tile row (0..127 of the code tile) of B block tn of wave column wn.
   static __device__ __forceinline__ int brow(int wn, int tn) {
@@ -152,7 +157,7 @@ struct QGemmDL {
     __amdgpu_buffer_rsrc_t xr, wr, sr;
     int oa[A_INST];  // per-lane byte offsets of step 0
     int ob[B_INST];
-    int os;
+    int os[S_INST > 0 ? S_INST : 1];
   };
 
   static __device__ __forceinline__ Src source(const QmvParams& p, const QmvMat& mt, int b,
@@ -193,28 +198,27 @@ struct QGemmDL {
       const int srows = __builtin_amdgcn_readfirstlane(min(max(rows - base_row, 0), 64));
       s.sr = __builtin_amdgcn_make_buffer_rsrc((void*)sreg(sp), (short)0, srows * sb,
                                                kBufferRsrcWord3);
-      s.os = 4 * lane;
+      s.os[0] = 4 * lane;
     } else {
       const int r = 32 * wave + 16 * (lane >> 5) + (lane & 15);
       s.ob[0] = (PAIR ? (r & 63) : r) * rb + 16 * ((lane >> 4) & 1);
-      // scales: G32 waves 0, 1 (64 rows x 2 scales each), G16 all four waves
-      // (32 rows x 4 scales); the other waves' loads fall past the resource
-      const bool sup = PAIR && (G == 32 ? wave == 1 : wave >= 2);
+      // scales: load i of wave w covers rows S_RPI (w S_INST + i) .. (every
+      // row's SPR scales of the step); one weight per wave (the up weight of
+      // a pair from row 64)
+      const int row0 = S_RPI * wave * S_INST;
+      const bool sup = PAIR && row0 >= 64;
       const char* sp = (const char*)(sup ? mt.s2 : mt.s) +
-                       ((long long)b * mt.s_bstride + (long long)n0 * p.groups_per_row) * 2;
+                       ((long long)b * mt.s_bstride + (long long)n0 * p.groups_per_row) * SB;
       s.sr = __builtin_amdgcn_make_buffer_rsrc((void*)sp, (short)0,
-                                               rows * p.groups_per_row * 2, kBufferRsrcWord3);
-      int srow, sdw;
-      if constexpr (G == 32) {
-        srow = 64 * wave + lane;
-        sdw = 0;
-      } else {
-        srow = 32 * wave + (lane >> 1);
-        sdw = lane & 1;
+                                               rows * p.groups_per_row * SB, kBufferRsrcWord3);
+#pragma unroll
+      for (int i = 0; i < S_INST; ++i) {
+        const int j = wave * S_INST + i;  // load index over the workgroup
+        const int byte = 256 * j + 4 * lane;  // in the step's scale block [row][SPR]
+        const int srow = byte / (SPR * SB), sin = byte % (SPR * SB);
+        const int wrow = PAIR ? (srow & 63) : srow;
+        s.os[i] = 256 * j >= S_BYTES ? (1 << 30) : wrow * p.groups_per_row * SB + sin;
       }
-      const int wrow = PAIR ? (srow & 63) : srow;
-      s.os = (G == 32 && wave >= 2) ? (1 << 30)
-                                    : (wrow * p.groups_per_row + 2 * sdw) * 2;
     }
     return s;
   }
@@ -227,15 +231,23 @@ struct QGemmDL {
 #pragma unroll
     for (int t = 0; t < B_INST; ++t)
       dma<16>(s.wr, base + A_BYTES + (wave * B_INST + t) * 1024, s.ob[t] + st * CP);
-    if constexpr (FMT == kQ4) dma<4>(s.sr, base + A_BYTES + B_BYTES + wave * 256, s.os + st * SPR * 2);
+    if constexpr (FMT == kQ4) {
+#pragma unroll
+      for (int i = 0; i < S_INST; ++i)
+        dma<4>(s.sr, base + A_BYTES + B_BYTES + (wave * S_INST + i) * 256,
+               s.os[i] + st * SPR * SB);
+    }
   }
 
   // Fragments of one step a wave reads from LDS: the activation blocks of one
   // K half and the raw codes (and Q4 scales) of both halves.
+  // (Q4: the lane's 8 codes of each MFMA extent and the row's scales of the
+  // step, one per extent or two for groups of 16)
+  static constexpr int NS = FMT == kQ8 ? 1 : SPR;
   struct Frag {
     f16x8 a[TM];
     typename std::conditional<FMT == kQ8, u32x4, u32x2>::type c[TN];
-    uint32_t s[FMT == kQ8 ? 1 : TN];
+    uint32_t s[TN][NS];
   };
 
   struct Lane {
@@ -249,17 +261,18 @@ struct QGemmDL {
     const int l16 = lane & 15, lk = lane >> 4;
     const int f = (l16 & 7) ^ (l16 >> 3);
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) L.a_off[kk] = l16 * 128 + (((2 * lk + kk) ^ f) << 4);
-    L.b_off = FMT == kQ8 ? 16 * lane : (lk >> 1) * 256 + l16 * 16 + 8 * (lk & 1);
-    L.s_off = FMT == kQ8 ? 0 : l16 * (2 * SPR) + 2 * (G == 32 ? (lk >> 1) : lk);
+    for (int kk = 0; kk < 2; ++kk)
+      L.a_off[kk] = l16 * 128 + (((FMT == kQ8 ? 2 * lk + kk : 4 * kk + lk) ^ f) << 4);
+    L.b_off = FMT == kQ8 ? 16 * lane : l16 * 16 + 4 * lk;  // Q4: + 256 kk
+    L.s_off = FMT == kQ8 ? 0 : l16 * (SPR * SB);
     return L;
   }
 
-  static __device__ __forceinline__ void read_a(const char* base, const Lane& L, int wm, int kk,
+  static __device__ __forceinline__ void read_a(const char* base, const Lane& L, int kk,
                                                 f16x8 (&a)[TM]) {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm)
-      a[tm] = *(const f16x8*)(base + (wm * 64 + 16 * tm) * 128 + L.a_off[kk]);
+      a[tm] = *(const f16x8*)(base + 16 * tm * 128 + L.a_off[kk]);
   }
 
   static __device__ __forceinline__ void read_b(const char* base, const Lane& L, int wn, Frag& f) {
@@ -269,8 +282,12 @@ struct QGemmDL {
       if constexpr (FMT == kQ8) {
         f.c[tn] = *(const u32x4*)(base + A_BYTES + blk * 1024 + L.b_off);
       } else {
-        f.c[tn] = *(const u32x2*)(base + A_BYTES + blk * 512 + L.b_off);
-        f.s[tn] = *(const uint16_t*)(base + A_BYTES + B_BYTES + blk * 16 * (2 * SPR) + L.s_off);
+        const char* bb = base + A_BYTES + blk * 512 + L.b_off;
+        f.c[tn] = u32x2{*(const uint32_t*)bb, *(const uint32_t*)(bb + 256)};
+        const char* sb = base + A_BYTES + B_BYTES + blk * 16 * (SPR * SB) + L.s_off;
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+          f.s[tn][i] = SF16 ? (uint32_t) * (const uint16_t*)(sb + SB * i) : *(const uint32_t*)(sb + 4 * i);
       }
     }
   }
@@ -289,22 +306,38 @@ struct QGemmDL {
         for (int tm = 0; tm < TM; ++tm)
           acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bq, acc[tm][tn], 0, 0, 0);
       } else {
+        // one group per extent (32) or two (16: lane groups 0-1 and 2-3, each
+        // MFMA with the other group's codes zeroed); each group's product is
+        // scaled in fp32 into the accumulator: exactly float(q) * scale
         uint32_t e[4];
         q4_pairs_seq(f.c[tn][kk], e);
-        // (s_hi, s_lo): s_hi keeps the top 7 significand bits, s_lo = s - s_hi exactly
-        const f16 sv = __builtin_bit_cast(f16, (uint16_t)f.s[tn]);
-        const f16 hi = __builtin_bit_cast(f16, (uint16_t)(f.s[tn] & 0xFFF0u));
-        const f16 lo = sv - hi;
-        const f16x2 shi = {hi, hi}, slo = {lo, lo};
-        const f16x8 bhi = pack8(as_u(as_h2(e[0]) * shi), as_u(as_h2(e[1]) * shi),
-                                as_u(as_h2(e[2]) * shi), as_u(as_h2(e[3]) * shi));
-        const f16x8 blo = pack8(as_u(as_h2(e[0]) * slo), as_u(as_h2(e[1]) * slo),
-                                as_u(as_h2(e[2]) * slo), as_u(as_h2(e[3]) * slo));
+        const f16x8 bq = pack8(e[0], e[1], e[2], e[3]);
+        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (G == 32) {
+          const float sc = scale_of(f.s[tn][kk], SF16);
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm) {
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bhi, acc[tm][tn], 0, 0, 0);
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], blo, acc[tm][tn], 0, 0, 0);
+          for (int tm = 0; tm < TM; ++tm) {
+            const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bq, z, 0, 0, 0);
+            acc[tm][tn] = __builtin_elementwise_fma(f32x4{sc, sc, sc, sc}, t, acc[tm][tn]);
+          }
+        } else {
+          const float s0 = scale_of(f.s[tn][2 * kk], SF16);
+          const float s1 = scale_of(f.s[tn][2 * kk + 1], SF16);
+          const bool first = (__lane_id() >> 4) < 2;
+          const f16x8 zero = {};
+          const f16x8 b0 = first ? bq : zero, b1 = first ? zero : bq;
+#pragma unroll
+          for (int tm = 0; tm < TM; ++tm) {
+            const f32x4 t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], b0, z, 0, 0, 0);
+            const f32x4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], b1, z, 0, 0, 0);
+            const f32x4 a0 = __builtin_elementwise_fma(f32x4{s0, s0, s0, s0}, t0, acc[tm][tn]);
+            acc[tm][tn] = __builtin_elementwise_fma(f32x4{s1, s1, s1, s1}, t1, a0);
+          }
         }
+        // the scaled sums are formed here, not deferred by the compiler (which
+        // would keep every MFMA result of the step alive: spills)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) asm volatile("" : "+v"(acc[tm][tn]));
       }
     }
   }
@@ -327,9 +360,25 @@ struct QGemmDL {
   static constexpr int RPP = kThreads / TPR;   // rows per pass
   static constexpr int C_BYTES = 64 * CW * 4;
 
+  // Rows 64 h .. 64 h + 63 of the tile's raw accumulators into C, then a
+  // barrier (a barrier first for h > 0: every thread has read the last half).
+  static __device__ __forceinline__ void stage_c(int h, int lane, int wn,
+                                                 const f32x4 (&acc)[TM][TN], float* C) {
+    const int l16 = lane & 15, lk = lane >> 4;
+    if (h > 0) bar();
+#pragma unroll
+    for (int tq = 0; tq < 4; ++tq)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          C[(16 * tq + 4 * lk + r) * CW + brow(wn, tn) + l16] = acc[4 * h + tq][tn][r];
+    wait_lgkm0();
+    bar();
+  }
+
   static __device__ __forceinline__ void finish(const QmvParams& p, const QmvMat& mt, int b,
-                                                int n0, int m0, int tid, int lane, int wm,
-                                                int wn, const f32x4 (&acc)[TM][TN], float* C,
+                                                int n0, int m0, int tid, int lane, int wn, const f32x4 (&acc)[TM][TN], float* C,
                                                 const char* qs) {
     const int l16 = lane & 15, lk = lane >> 4;
     // everything the loops below use, in registers (see sreg)
@@ -377,16 +426,7 @@ struct QGemmDL {
     }
 #pragma unroll
     for (int h = 0; h < BM / 64; ++h) {
-      if (h > 0) bar();  // every thread has read the previous half
-#pragma unroll
-      for (int tq = 0; tq < 4; ++tq)
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            C[(16 * tq + 4 * lk + r) * CW + brow(wn, tn) + l16] = acc[4 * h + tq][tn][r];
-      wait_lgkm0();
-      bar();
+      stage_c(h, lane, wn, acc, C);
 #pragma unroll 1
       for (int row = r0; row < 64; row += RPP) {
         const int m = m0 + 64 * h + row;
@@ -476,28 +516,42 @@ struct QGemmDL {
   }
 
   // Split K: the raw accumulators of K chunk c (no row scale, no epilogue)
-  // into partial plane c.
+  // into partial plane c, through C as in finish: 8 consecutive partials of
+  // a row per thread, two 16-byte stores where the plane is aligned.
   static __device__ __forceinline__ void spill(const QmvParams& p, const QmvMat& mt, int b,
-                                               int n0, int m0, int lane, int wm, int wn, int c,
-                                               const f32x4 (&acc)[TM][TN]) {
-    const int l16 = lane & 15, lk = lane >> 4;
+                                               int n0, int m0, int tid, int lane, int wn, int c,
+                                               const f32x4 (&acc)[TM][TN], float* C) {
     constexpr int NW = PAIR ? 2 : 1;
-    constexpr int TO = PAIR ? TN / 2 : TN;
-    float* base = p.sk_part + (long long)c * p.sk_plane + mt.sk_off +
-                  (long long)b * p.m * NW * mt.n_store;
+    const int nst = sreg(mt.n_store), mn = sreg(mt.n), pm = sreg(p.m);
+    float* const base = sreg(p.sk_part + (long long)c * p.sk_plane + mt.sk_off +
+                             (long long)b * p.m * NW * mt.n_store);
+    gchar* const gb = (gchar*)base;
+    const int cg = tid % TPR, r0 = tid / TPR;
+    const int nb = n0 + 8 * cg;
+    const bool vec = nb + 8 <= mn && (nst & 3) == 0 && ((uintptr_t)base & 15) == 0;
 #pragma unroll
-    for (int to = 0; to < TO; ++to) {
-      const int n = n0 + ocol(wn, to) + l16;
-      if (n >= mt.n) continue;
+    for (int h = 0; h < BM / 64; ++h) {
+      stage_c(h, lane, wn, acc, C);
+#pragma unroll 1
+      for (int row = r0; row < 64; row += RPP) {
+        const int m = m0 + 64 * h + row;
+        if (m >= pm) continue;
 #pragma unroll
-      for (int h = 0; h < NW; ++h)
+        for (int hh = 0; hh < NW; ++hh) {
+          const f32x4 v0 = *(const f32x4*)&C[row * CW + 64 * hh + 8 * cg];
+          const f32x4 v1 = *(const f32x4*)&C[row * CW + 64 * hh + 8 * cg + 4];
+          const long long o = ((long long)m * NW + hh) * nst + nb;
+          if (vec) {
+            *(gf32x4*)(gb + o * 4) = v0;
+            *(gf32x4*)(gb + o * 4 + 16) = v1;
+          } else {
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int m = m0 + wm * 64 + 16 * tm + 4 * lk + r;
-            if (m < p.m) base[((long long)m * NW + h) * mt.n_store + n] = acc[tm][to + TO * h][r];
+            for (int j = 0; j < 8; ++j)
+              if (nb + j < mn)
+                ((__attribute__((address_space(1))) float*)gb)[o + j] = j < 4 ? v0[j] : v1[j - 4];
           }
+        }
+      }
     }
   }
 };
@@ -507,11 +561,11 @@ struct QGemmDL {
 // step's codes and first-half activation blocks; on return, the next step's.
 template <typename G>
 __device__ __forceinline__ void qgemm_dl_step(const typename G::Src& src, const typename G::Lane& L,
-                                              char* cur, char* nxt, int wave, int wm, int wn,
+                                              char* cur, char* nxt, int wave, int wn,
                                               int st, int s1, typename G::Frag& f,
                                               f32x4 (&acc)[G::TM][G::TN]) {
   f16x8 a1[G::TM];
-  G::read_a(cur, L, wm, 1, a1);
+  G::read_a(cur, L, 1, a1);
   __builtin_amdgcn_sched_barrier(0);  // the reads go out ahead of the MFMAs
   G::mfma_half(0, f.a, f, acc);
   // this step's fragments are in registers before any wave refills `cur`;
@@ -525,7 +579,7 @@ __device__ __forceinline__ void qgemm_dl_step(const typename G::Src& src, const 
   if (st + 3 < s1) G::issue(src, lds_addr(cur), wave, st + 3);
   typename G::Frag g;
   if (st + 1 < s1) {
-    G::read_a(nxt, L, wm, 0, g.a);
+    G::read_a(nxt, L, 0, g.a);
     G::read_b(nxt, L, wn, g);
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -566,7 +620,7 @@ void qgemm_dl_kernel(const QmvParams p, int mtiles) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / Q::WGN, wn = wave % Q::WGN;
+  const int wn = wave;  // the wave's 32 weight rows
   const int steps = p.k / Q::BK;
   const int cs = S > 1 ? p.sk_cs : steps;
   const int s0 = kc * cs, s1 = min(s0 + cs, steps);  // this workgroup's K steps
@@ -585,7 +639,7 @@ void qgemm_dl_kernel(const QmvParams p, int mtiles) {
   // Q8: the tile's row scales go to LDS with the first step (waves 0 and 1:
   // rows 0-63 and 64-127, or the gate and up rows of a pair)
   if constexpr (FMT == kQ8)
-    if (S == 1 && wave < 2) dma<4>(src.sr, lds_addr(qs) + wave * 512, src.os);
+    if (S == 1 && wave < 2) dma<4>(src.sr, lds_addr(qs) + wave * 512, src.os[0]);
   Q::issue(src, lds_addr(st0), wave, s0);
   if (s0 + 1 < s1) Q::issue(src, lds_addr(st1), wave, s0 + 1);
   if (s0 + 2 < s1) Q::issue(src, lds_addr(st2), wave, s0 + 2);
@@ -597,25 +651,25 @@ void qgemm_dl_kernel(const QmvParams p, int mtiles) {
     wait_vm<0>();
   bar();
   typename Q::Frag f;
-  Q::read_a(st0, L, wm, 0, f.a);
+  Q::read_a(st0, L, 0, f.a);
   Q::read_b(st0, L, wn, f);
   // three steps per iteration: the stages rotate with compile-time names
   int st = s0;
   for (int it = (s1 - s0) / 3; it > 0; --it) {
-    qgemm_dl_step<Q>(src, L, st0, st1, wave, wm, wn, st, s1, f, acc);
-    qgemm_dl_step<Q>(src, L, st1, st2, wave, wm, wn, st + 1, s1, f, acc);
-    qgemm_dl_step<Q>(src, L, st2, st0, wave, wm, wn, st + 2, s1, f, acc);
+    qgemm_dl_step<Q>(src, L, st0, st1, wave, wn, st, s1, f, acc);
+    qgemm_dl_step<Q>(src, L, st1, st2, wave, wn, st + 1, s1, f, acc);
+    qgemm_dl_step<Q>(src, L, st2, st0, wave, wn, st + 2, s1, f, acc);
     st += 3;
   }
   const int tail = s1 - st;
-  if (tail >= 1) qgemm_dl_step<Q>(src, L, st0, st1, wave, wm, wn, st, s1, f, acc);
-  if (tail >= 2) qgemm_dl_step<Q>(src, L, st1, st2, wave, wm, wn, st + 1, s1, f, acc);
-  if (S == 1) {
-    wait_lgkm0();  // the last fragments are read before the stages become C
-    bar();
-    Q::finish(p, mt, b, n0, m0, threadIdx.x, lane, wm, wn, acc, (float*)lds, qs);
-  } else
-    Q::spill(p, mt, b, n0, m0, lane, wm, wn, kc, acc);
+  if (tail >= 1) qgemm_dl_step<Q>(src, L, st0, st1, wave, wn, st, s1, f, acc);
+  if (tail >= 2) qgemm_dl_step<Q>(src, L, st1, st2, wave, wn, st + 1, s1, f, acc);
+  wait_lgkm0();  // the last fragments are read before the stages become C
+  bar();
+  if (S == 1)
+    Q::finish(p, mt, b, n0, m0, threadIdx.x, lane, wn, acc, (float*)lds, qs);
+  else
+    Q::spill(p, mt, b, n0, m0, threadIdx.x, lane, wn, kc, acc, (float*)lds);
 }
 
 }  // namespace aexq

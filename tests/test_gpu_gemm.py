@@ -211,7 +211,8 @@ def test_gemm_stacked_copies_batched_x_match_single(ctx, aexq, orc, monkeypatch,
 def test_gemm_group16(ctx, aexq, orc, monkeypatch, scale_f16, n, k, m, swiglu, splitk):
     """Q4 with one scale per 16 codes on the tiled GEMM: two MFMAs per 32-code
     extent, each group's product scaled in fp32 (exact float(q) * scale).  With
-    three forced K chunks the chunks' step counts are odd and even alike."""
+    three forced K chunks the chunks' step counts differ (a tail of the
+    three-step loop, or none)."""
     if splitk:
         monkeypatch.setenv("AEXQ_SPLITK", splitk)
     _announce(f"qgemm group16 f16={scale_f16} n={n} k={k} m={m} swiglu={swiglu} splitk={splitk}")
@@ -226,10 +227,7 @@ def test_gemm_group16(ctx, aexq, orc, monkeypatch, scale_f16, n, k, m, swiglu, s
         wu, uf = _weight(ctx, aexq, orc, 4, n, k, 93 + m, group=16, scale_f16=scale_f16, code=0)
         kw = dict(up=wu)
     plan = ctx.plan_check(w, xd, yd, **kw)
-    # fp16 scales (all small) take the LDS-direct split-scale kernel, fp32 the
-    # per-group fp32 scaling of the 64-row register-staged one
-    assert plan.startswith("kernel=qgemm"), plan
-    assert ("direct=1" in plan) == scale_f16 and (scale_f16 or "bm=64" in plan), plan
+    assert plan.startswith("kernel=qgemm") and "direct=1" in plan, plan
     ctx.linear(w, xd, yd, **kw)
     torch.cuda.synchronize()
     g = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
@@ -245,57 +243,31 @@ def test_gemm_group16(ctx, aexq, orc, monkeypatch, scale_f16, n, k, m, swiglu, s
     assert normwise(got[:, :n], ref) <= TOL32
 
 
-@pytest.mark.parametrize("split", [True, False])
-def test_gemm_q4_split_scales_exact(ctx, aexq, orc, monkeypatch, split):
-    """Q4 with fp16 scales above 64 rows folds each scale into B as two exact
-    fp16 parts (s_hi = top 7 significand bits, s_lo = s - s_hi); with the split
-    switched off the per-group fp32 scaling runs.  Both meet the fp32-output
-    bar against the float64 oracle, with fp16-subnormal and large scales among
-    the groups."""
-    _announce(f"qgemm q4 split={split}")
+@pytest.mark.parametrize("group", [16, 32])
+def test_gemm_q4_extreme_scales_exact(ctx, aexq, orc, group):
+    """Per-group fp32 scaling keeps the dequantised weight exactly float(q) *
+    scale for every fp16 scale: subnormal, large and above 4096 (where q * s
+    would overflow an fp16 product) among the groups -- the fp32-output bar
+    against the float64 oracle."""
+    _announce(f"qgemm q4 extreme scales g={group}")
     from aiimage_amd import synth
-    if not split:
-        monkeypatch.setenv("AEXQ_QGEMM_NOSPLIT", "1")
     n, k, m = 512, 1024, 130
-    words, scales, _ = synth.q4_weights(n, k, 95, group=32, code=synth.NIBBLE_OFFSET8)
+    words, scales, _ = synth.q4_weights(n, k, 95, group=group, code=synth.NIBBLE_OFFSET8)
     bits = scales.view(np.uint16).copy()
     bits[:300] = np.arange(1, 301, dtype=np.uint16)              # subnormal scales
-    bits[300:310] = np.float16(1000.0).view(np.uint16)           # large, still <= 4096
-    bits[310:320] = np.float16(4096.0).view(np.uint16)           # the bound itself
+    bits[300:310] = np.float16(1000.0).view(np.uint16)
+    bits[310:320] = np.float16(4096.0).view(np.uint16)
+    bits[320:330] = np.float16(5000.0).view(np.uint16)           # q * s beyond fp16 range
     sc = bits.view(np.float16)
-    w = ctx.weight(aexq.QuantizedTensor(n * k, 32, words, sc, bits=4,
+    w = ctx.weight(aexq.QuantizedTensor(n * k, group, words, sc, bits=4,
                                         nibble_code=synth.NIBBLE_OFFSET8), n, k)
-    wf = orc.dequant_q4(words, sc, n, k, 32, synth.NIBBLE_OFFSET8, orc.SCALE_F16)
+    wf = orc.dequant_q4(words, sc, n, k, group, synth.NIBBLE_OFFSET8, orc.SCALE_F16)
     x16 = synth.activations(m, k, 96)
     y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
     xd = aexq.describe(dev(x16), m, k)
     yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
     plan = ctx.plan_check(w, xd, yd)
-    assert f"split={int(split)}" in plan, plan
-    ctx.linear(w, xd, yd)
-    torch.cuda.synchronize()
-    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
-    assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
-
-
-def test_gemm_q4_scale_above_bound_keeps_group_scaling(ctx, aexq, orc):
-    """A scale above 4096 could overflow q * s_hi in fp16: such a weight stays on
-    the per-group fp32 scaling."""
-    _announce("qgemm q4 scale > 4096")
-    from aiimage_amd import synth
-    n, k, m = 256, 512, 96
-    words, scales, _ = synth.q4_weights(n, k, 97, group=32, code=synth.NIBBLE_OFFSET8)
-    sc = scales.copy()
-    sc[5] = np.float16(5000.0)
-    w = ctx.weight(aexq.QuantizedTensor(n * k, 32, words, sc, bits=4,
-                                        nibble_code=synth.NIBBLE_OFFSET8), n, k)
-    wf = orc.dequant_q4(words, sc, n, k, 32, synth.NIBBLE_OFFSET8, orc.SCALE_F16)
-    x16 = synth.activations(m, k, 98)
-    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
-    xd = aexq.describe(dev(x16), m, k)
-    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
-    plan = ctx.plan_check(w, xd, yd)
-    assert "split=0" in plan, plan
+    assert "direct=1" in plan, plan
     ctx.linear(w, xd, yd)
     torch.cuda.synchronize()
     ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
@@ -328,30 +300,54 @@ def test_gemm_direct_step_counts(ctx, aexq, orc, bits, group, k, m):
     assert normwise(got[:, :n], ref) <= TOL32
 
 
-@pytest.mark.parametrize("bits,group", [(8, 0), (4, 16)])
+@pytest.mark.parametrize("bits,group,scale_f16", [(8, 0, True), (8, 0, False), (4, 16, True),
+                                                   (4, 16, False), (4, 32, True), (4, 32, False)])
 @pytest.mark.parametrize("m", [40, 100])
-def test_gemm_direct_pair_matches_register_staged(ctx, aexq, orc, monkeypatch, bits, group, m):
-    """gate/up pairs on the LDS-direct kernel against the oracle, and against
-    the register-staged kernel (AEXQ_QGEMM_DL=0) on the same inputs."""
-    _announce(f"qgemm direct pair q{bits} g={group} m={m}")
+def test_gemm_direct_pairs(ctx, aexq, orc, bits, group, scale_f16, m):
+    """gate/up pairs on the LDS-direct kernel, both tile heights, fp16 and fp32
+    scales, against the oracle."""
+    _announce(f"qgemm direct pair q{bits} g={group} f16={scale_f16} m={m}")
     from aiimage_amd import synth
     n, k = 320, 256
-    wg, gf = _weight(ctx, aexq, orc, bits, n, k, 301 + m, group=group or k, code=0)
-    wu, uf = _weight(ctx, aexq, orc, bits, n, k, 302 + m, group=group or k, code=0)
+    wg, gf = _weight(ctx, aexq, orc, bits, n, k, 301 + m, group=group or k,
+                     scale_f16=scale_f16, code=0)
+    wu, uf = _weight(ctx, aexq, orc, bits, n, k, 302 + m, group=group or k,
+                     scale_f16=scale_f16, code=0)
     x16 = synth.activations(m, k, 303)
     xd = aexq.describe(dev(x16), m, k)
-    outs = []
-    for dl in ("1", "0"):
-        monkeypatch.setenv("AEXQ_QGEMM_DL", dl)
-        y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
-        yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
-        plan = ctx.plan_check(wg, xd, yd, up=wu)
-        assert plan.startswith("kernel=qgemm") and f"direct={dl}" in plan, plan
-        ctx.linear(wg, xd, yd, up=wu)
-        torch.cuda.synchronize()
-        outs.append(y.cpu().numpy().reshape(m, -1)[:, :n].astype(np.float64))
+    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    plan = ctx.plan_check(wg, xd, yd, up=wu)
+    assert plan.startswith("kernel=qgemm") and "direct=1" in plan, plan
+    ctx.linear(wg, xd, yd, up=wu)
+    torch.cuda.synchronize()
     g = orc.gemm_gpu_semantics(x16.astype(np.float32), gf)
     u = orc.gemm_gpu_semantics(x16.astype(np.float32), uf)
     ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32)) for r in range(m)])
-    assert normwise(outs[0], ref) <= TOL32
-    assert normwise(outs[0], outs[1]) <= TOL32
+    assert normwise(y.cpu().numpy().reshape(m, -1)[:, :n], ref) <= TOL32
+
+
+@pytest.mark.parametrize("group,scale_f16", [(16, False), (32, False), (16, True)])
+@pytest.mark.parametrize("k", [64, 192, 320])
+@pytest.mark.parametrize("m", [40, 100])
+def test_gemm_direct_group_scaling(ctx, aexq, orc, group, scale_f16, k, m):
+    """Q4 per-group fp32 scaling on the LDS-direct kernel, fp32 and fp16
+    scales: 1, 3 and 5 K steps, both tile heights."""
+    _announce(f"qgemm direct per-group g={group} f16={scale_f16} k={k} m={m}")
+    from aiimage_amd import synth
+    n = 200
+    w, wf = _weight(ctx, aexq, orc, 4, n, k, 11 * k + m, group=group, scale_f16=scale_f16,
+                    code=0)
+    x16 = synth.activations(m, k, 3 * k + m)
+    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    plan = ctx.plan_check(w, xd, yd)
+    assert "direct=1" in plan, plan
+    ctx.linear(w, xd, yd)
+    torch.cuda.synchronize()
+    stride = aexq.storage_elements(aexq.LAYOUT_PACK4_LINEAR, m, n)
+    got = y.cpu().numpy().reshape(m, stride)
+    assert np.all(got[:, n:] == 0)
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    assert normwise(got[:, :n], ref) <= TOL32
