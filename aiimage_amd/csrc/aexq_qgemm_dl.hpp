@@ -196,7 +196,10 @@ struct QGemmDL {
       const char* sp = (const char*)(sup ? mt.s2 : mt.s) + (long long)b * mt.s_bstride * sb +
                        (long long)(n0 + base_row) * sb;
       const int srows = __builtin_amdgcn_readfirstlane(min(max(rows - base_row, 0), 64));
-      s.sr = __builtin_amdgcn_make_buffer_rsrc((void*)sreg(sp), (short)0, srows * sb,
+      // (the range in whole dwords: a dword only partly inside reads zero, which
+      // at an odd row count with fp16 scales would zero the last row's scale;
+      // a weight's scale storage runs at least 16 bytes past its last scale)
+      s.sr = __builtin_amdgcn_make_buffer_rsrc((void*)sreg(sp), (short)0, (srows * sb + 3) & ~3,
                                                kBufferRsrcWord3);
       s.os[0] = 4 * lane;
     } else {

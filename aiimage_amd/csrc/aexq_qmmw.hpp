@@ -453,13 +453,12 @@ void qmmw_kernel(const QmvParams p) {
   if (t0 >= t1) {  // the whole workgroup: no barrier is left waiting
     if constexpr (ARGMAX) {
       // an empty partial for each row (it never wins the merge)
+      // (and its arrival, when the launch merges the partials itself)
       const int row = threadIdx.x;
-      if (row < 16 * MT && row < p.m) {
-        const long long o = (long long)(p.m_base + row) * p.parts + blockIdx.x;
-        p.part_best[o] = __builtin_nanf("");
-        p.part_index[o] = 0x7fffffff;
-        p.part_second[o] = -INFINITY;
-      }
+      if (row < 16 * MT && row < p.m)
+        argmax_partial_store(p, (long long)(p.m_base + row) * p.parts + blockIdx.x,
+                             __builtin_nanf(""), 0x7fffffff, -INFINITY);
+      argmax_tail(p);
     }
     return;
   }

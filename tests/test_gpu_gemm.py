@@ -75,6 +75,7 @@ def _weight(ctx, aexq, orc, bits, n, k, seed, group=32, scale_f16=True, code=1):
     (4, 32, True, 1024, 3584, 512, False),   # down_proj at M = 512
     (8, 0, True, 1024, 2048, 512, False),    # Q8 o_proj at M = 512
     (8, 0, False, 1000, 1088, 200, True),    # ragged N and M, K = 17 steps (not a multiple of 128)
+    (8, 0, True, 1001, 1024, 100, False),    # odd N with fp16 row scales: the last row's scale
     (4, 64, False, 520, 1024, 97, True),     # one scale per 64 codes, fp32 scales
     (4, 32, True, 130, 64, 33, True),        # a single K step, 2 rows past a tile
     (4, 32, False, 256, 512, 129, True),     # reference nibble code below
