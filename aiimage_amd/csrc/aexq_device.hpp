@@ -236,6 +236,24 @@ __device__ __forceinline__ void argmax_tail(const QmvParams& p) {
   }
 }
 
+// The (tile, item) of a tiled-GEMM workgroup.  Workgroup b is dispatched to
+// XCD b % 8; XCD x takes the contiguous tile range [x T / 8, (x + 1) T / 8)
+// of the launch's `tiles` tiles, `per` consecutive workgroups per tile (its
+// row tiles and K chunks).  Consecutive tiles are the weight tiles of one
+// copy of a batched launch (or of one matrix), so a copy's activation tile is
+// fetched into one XCD's L2 and re-read there by every weight tile of the
+// copy, and a weight tile by every row tile; spreading a copy over the eight
+// XCDs would fetch its activations once per XCD through the shared fabric,
+// where they compete with the weight stream.  tile < 0: no work (the grid is
+// ceil(T / 8) * 8 * per workgroups).
+__device__ __forceinline__ void gemm_block_tile(int bid, int tiles, int per, int& tile, int& item) {
+  const int x = bid & 7, j = bid >> 3;
+  const int t0 = (x * tiles) >> 3, t1 = ((x + 1) * tiles) >> 3;
+  const int tl = j / per;
+  tile = t0 + tl < t1 ? t0 + tl : -1;
+  item = j - tl * per;
+}
+
 __device__ __forceinline__ float load_scale(const void* s, long long i, bool f16_scale) {
   return f16_scale ? (float)((const f16*)s)[i] : ((const float*)s)[i];
 }

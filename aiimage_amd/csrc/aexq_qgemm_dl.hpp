@@ -40,8 +40,9 @@
 // MFMAs cover the second half's fragment reads and the barrier wait, the
 // second half's MFMAs cover the next step's first fragment reads.
 //
-// Workgroup b runs on XCD b % 8: the numbering puts the BM-row tiles of one
-// weight tile on one XCD, whose L2 then fetches that weight tile once.
+// Workgroup b runs on XCD b % 8, which takes a contiguous range of tiles
+// (gemm_block_tile): the BM-row tiles of one weight tile, and the weight
+// tiles of one copy, share that XCD's L2.
 //
 // MFMA 16x16x32 f16 lane layout (lane l): A[l % 16][8 (l / 16) + j],
 // B[8 (l / 16) + j][l % 16], D[4 (l / 16) + r][l % 16], j < 8, r < 4.
@@ -605,12 +606,12 @@ void qgemm_dl_kernel(const QmvParams p, int mtiles) {
   // workgroup-uniform coordinates in scalar registers
   const int S = p.sk_chunks > 1 ? p.sk_chunks : 1;
   const int per = mtiles * S;
-  const int bid = blockIdx.x, i = bid >> 3;
-  const int tn = __builtin_amdgcn_readfirstlane((i / per) * 8 + (bid & 7));
-  const int rem = i - (i / per) * per;
+  int tile, rem;
+  gemm_block_tile(blockIdx.x, p.total_tiles, per, tile, rem);
+  const int tn = __builtin_amdgcn_readfirstlane(tile);
   const int tm = __builtin_amdgcn_readfirstlane(rem / S);
   const int kc = __builtin_amdgcn_readfirstlane(rem - (rem / S) * S);
-  if (tn >= p.total_tiles) return;
+  if (tn < 0) return;
   int j = 0;
   for (int q = 1; q < p.nmat; ++q)
     if (tn >= p.mat[q].tile_base) j = q;
