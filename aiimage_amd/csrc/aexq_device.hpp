@@ -236,6 +236,16 @@ __device__ __forceinline__ void argmax_tail(const QmvParams& p) {
   }
 }
 
+// Rank of workgroup bid among the grid's workgroups such that the ranks of
+// one XCD (bid % 8: workgroups are dispatched to the XCDs in turn) are one
+// contiguous run: persistent kernels that give workgroup rank r the r-th
+// contiguous range of work then keep neighbouring work -- the tiles of one
+// copy of a batched launch, and that copy's activation rows -- in one L2.
+__device__ __forceinline__ int xcd_rank(int bid, int grid) {
+  const int x = bid & 7, j = bid >> 3, q = grid >> 3, r = grid & 7;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + j;
+}
+
 // The (tile, item) of a tiled-GEMM workgroup.  Workgroup b is dispatched to
 // XCD b % 8; XCD x takes the contiguous tile range [x T / 8, (x + 1) T / 8)
 // of the launch's `tiles` tiles, `per` consecutive workgroups per tile (its

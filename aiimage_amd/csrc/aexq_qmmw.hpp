@@ -445,8 +445,9 @@ void qmmw_kernel(const QmvParams p) {
   const int S = !ARGMAX && p.sk_chunks > 1 ? p.sk_chunks : 1;
   const int cs = S > 1 ? p.sk_cs : steps;
   const long long items = (long long)p.total_tiles * S;
-  const long long i0 = (long long)blockIdx.x * items / gridDim.x;
-  const long long i1 = (long long)(blockIdx.x + 1) * items / gridDim.x;
+  const int rank = xcd_rank(blockIdx.x, gridDim.x);  // one XCD: one contiguous run of items
+  const long long i0 = (long long)rank * items / gridDim.x;
+  const long long i1 = (long long)(rank + 1) * items / gridDim.x;
   const int t0 = (int)((i0 / S) * steps + (i0 % S) * cs);
   const int t1 = i1 > i0 ? (int)(((i1 - 1) / S) * steps + min((int)((i1 - 1) % S + 1) * cs, steps))
                          : t0;
