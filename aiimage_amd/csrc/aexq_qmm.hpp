@@ -278,8 +278,10 @@ struct Qmm {
   }
 
   // Scale (Q8), epilogue and store of a finished tile; zeroes the accumulators.
+  // rs_pre: Q8 row scales the caller loaded ahead ([NW][NT], the lane's
+  // output row of each block); null: loaded here
   static __device__ __forceinline__ void finish(const QmvParams& p, const Cursor& cu, int lane,
-                                                Acc& acc) {
+                                                Acc& acc, const float* rs_pre = nullptr) {
     const QmvMat& mt = p.mat[cu.j];
     const int n_l = lane & 15, mq = lane >> 4;
     const bool yf32 = (p.flags & kFlagYf32) != 0;
@@ -295,8 +297,12 @@ struct Qmm {
       for (int h = 0; h < NW; ++h) {
         rs[h] = 1.0f;
         if constexpr (FMT == kQ8) {
-          const char* sp = (const char*)(h == 0 ? mt.s : mt.s2) + cu.b * mt.s_bstride * sb;
-          rs[h] = n < mt.n ? load_scale(sp, n, SF16) : 0.0f;
+          if (rs_pre) {
+            rs[h] = rs_pre[h * NT + nt];
+          } else {
+            const char* sp = (const char*)(h == 0 ? mt.s : mt.s2) + cu.b * mt.s_bstride * sb;
+            rs[h] = n < mt.n ? load_scale(sp, n, SF16) : 0.0f;
+          }
         }
       }
 #pragma unroll

@@ -53,6 +53,12 @@ struct QmmW {
   struct Buf {
     u32x4 w[NW][NT][WI];
     u32x4 s[NW][NT][SV > 0 ? SV : 1];
+    // Q8: the row scale (raw bits) of the lane's output row of each block,
+    // loaded with a tile's last step (the other steps load it from past the
+    // resource: no traffic), so the tile's epilogue waits for no load of its
+    // own -- a load there would also wait for the next step's codes, which
+    // are issued before it (the vector-memory counter counts in order)
+    uint32_t q8s[NW][NT];
   };
 
   static __device__ __forceinline__ Cursor locate(const QmvParams& p, int t) {
@@ -115,6 +121,20 @@ struct QmmW {
               u32x4,
               __builtin_amdgcn_raw_buffer_load_b128(wr, rr * row_bytes + cb, 0, kStreamAux));
         }
+      if constexpr (FMT == kQ8) {
+        const char* sbp = (const char*)(h == 0 ? mt.s : mt.s2) + cu.b * mt.s_bstride * sb;
+        // rows of the wave's blocks past N read zero (their outputs are never
+        // stored or compared); not the tile's last step: past the resource
+        const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)sbp, (short)0, (mt.n * sb + 3) & ~3, kBufferRsrcWord3);
+        const bool last = cu.s == p.k / 256 - 1;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int off = last ? (r0 + 16 * nt + n_l) * sb : (1 << 30);
+          buf.q8s[h][nt] = SF16 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(sr, off, 0, 0)
+                                : __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0);
+        }
+      }
       if constexpr (SV > 0) {
         const char* sbp = (const char*)(h == 0 ? mt.s : mt.s2) +
                           (cu.b * mt.s_bstride + (long long)r0 * sper + cu.s * GPS) * sb;
@@ -245,7 +265,8 @@ struct QmmW {
   }
 
   static __device__ __forceinline__ void best_update(const QmvParams& p, const Cursor& cu,
-                                                     int lane, const Acc& acc, Best& b) {
+                                                     int lane, const Acc& acc, const Buf& buf,
+                                                     Best& b) {
     const QmvMat& mt = p.mat[cu.j];
     const int n_l = lane & 15, mq = lane >> 4;
     constexpr int sb = SF16 ? 2 : 4;
@@ -254,8 +275,7 @@ struct QmmW {
       const int n = cu.rt * Base::TN + 16 * nt + n_l;
       if (n >= mt.n) continue;
       float rs = 1.0f;
-      if constexpr (FMT == kQ8)
-        rs = load_scale((const char*)mt.s + cu.b * mt.s_bstride * sb, n, SF16);
+      if constexpr (FMT == kQ8) rs = scale_of(buf.q8s[0][nt], SF16);
 #pragma unroll
       for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -483,12 +503,17 @@ void qmmw_kernel(const QmvParams p) {
   };
   // the last step of a K chunk: the whole tile's K finishes it here, a chunk
   // of a split tile leaves its partial (the host never splits an argmax launch)
-  auto segment_end = [&](const typename Q::Cursor& c) {
+  auto segment_end = [&](const typename Q::Cursor& c, const typename Q::Buf& bf) {
+    float rsp[Q::NW][NT];  // Q8: the tile's row scales, loaded with its last step
+#pragma unroll
+    for (int h = 0; h < Q::NW; ++h)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) rsp[h][nt] = FMT == kQ8 ? scale_of(bf.q8s[h][nt], SF16) : 1.0f;
     if constexpr (ARGMAX) {
-      Q::best_update(p, mine(c), lane, acc, best);
-      Q::Base::finish(p, mine(c), lane, acc);
+      Q::best_update(p, mine(c), lane, acc, bf, best);
+      Q::Base::finish(p, mine(c), lane, acc, &rsp[0][0]);
     } else if (S == 1) {
-      Q::Base::finish(p, mine(c), lane, acc);
+      Q::Base::finish(p, mine(c), lane, acc, &rsp[0][0]);
     } else {
       Q::Base::spill(p, mine(c), lane, c.s / cs, acc);
     }
@@ -515,7 +540,7 @@ void qmmw_kernel(const QmvParams p) {
     __builtin_amdgcn_sched_barrier(0);
     Q::compute(p, lane, lds, xs_all[sl], A, acc);
     if (--seg == 0 || cu.s == steps - 1) {
-      segment_end(cu);
+      segment_end(cu, A);
       seg = cs;
     }
     if (!more) break;
@@ -531,7 +556,7 @@ void qmmw_kernel(const QmvParams p) {
     __builtin_amdgcn_sched_barrier(0);
     Q::compute(p, lane, lds, xs_all[sl], B, acc);
     if (--seg == 0 || cu.s == steps - 1) {
-      segment_end(cu);
+      segment_end(cu, B);
       seg = cs;
     }
     if (!more) break;
