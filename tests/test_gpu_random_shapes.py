@@ -160,3 +160,110 @@ def test_random_linear_against_oracle(ctx, aexq, orc, case):
     err = normwise(got[:, :n], ref)
     assert err <= tol, (err, plan)
     w.release()
+
+
+def _group_cases(count=16, seed=2027):
+    g = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        bits = int(g.choice([4, 8]))
+        group = int(g.choice([16, 32, 64])) if bits == 4 else 0
+        k = int(g.choice(K_CHOICES))
+        if bits == 4 and k % group:
+            continue
+        out.append(dict(i=len(out), bits=bits, group=group, k=k, m=int(g.choice(M_CHOICES)),
+                        ns=[int(v) for v in g.integers(1, 2500, size=int(g.integers(2, 4)))],
+                        rms=bool(g.integers(0, 2)), sf16=bool(g.integers(0, 2)),
+                        y32=bool(g.integers(0, 2)), code=int(g.integers(0, 2)),
+                        seed=int(g.integers(1, 1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("case", _group_cases(), ids=lambda c: f"g{c['i']}")
+def test_random_grouped_linear_against_oracle(ctx, aexq, orc, case):
+    """aexq_linear_group: two or three weights of one format and K sharing one
+    x (the q/k/v form), optional RMSNorm-in, each output against the oracle."""
+    c = case
+    _announce("random group " + " ".join(f"{k}={v}" for k, v in c.items()))
+    from aiimage_amd import synth
+    m, k = c["m"], c["k"]
+    layout = aexq.LAYOUT_PACK4_LINEAR
+    ydt = torch.float32 if c["y32"] else torch.float16
+    ws, wfs, ys, yds = [], [], [], []
+    for i, n in enumerate(c["ns"]):
+        w, wf = _weight(ctx, aexq, orc, dict(c, n=n), c["seed"] + 7 * i)
+        y = aexq.new_activation(m, n, ydt, layout)
+        ws.append(w)
+        wfs.append(wf)
+        ys.append(y)
+        yds.append(aexq.describe(y, m, n, layout))
+    x16 = synth.activations(m, k, c["seed"] + 1)
+    xd = aexq.describe(dev(x16), m, k)
+    xr = x16.astype(np.float32)
+    kw, tol = {}, TOL32 if c["y32"] else TOL
+    if c["rms"]:
+        eps = 1e-6
+        gamma = synth.rms_gamma(k, c["seed"] + 2)
+        gd = dev(gamma)
+        kw.update(rmsnorm=True, rms_gamma=gd, rms_eps=eps)
+        xr = orc.rmsnorm(xr, eps, gamma).astype(np.float16).astype(np.float32)
+        tol = TOL
+    ctx.linear_group(ws, xd, yds, **kw)
+    torch.cuda.synchronize()
+    for i, n in enumerate(c["ns"]):
+        ref = orc.gemm_gpu_semantics(xr, wfs[i])
+        stride = aexq.storage_elements(layout, m, n)
+        got = ys[i].cpu().numpy().astype(np.float64).reshape(m, stride)[:, :n]
+        err = normwise(got, ref)
+        assert err <= tol, (i, n, err)
+    for w in ws:
+        w.release()
+
+
+def _batch_cases(count=16, seed=2028):
+    g = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        bits = int(g.choice([4, 8]))
+        group = int(g.choice([16, 32])) if bits == 4 else 0
+        k = int(g.choice(K_CHOICES))
+        if bits == 4 and k % group:
+            continue
+        out.append(dict(i=len(out), bits=bits, group=group, k=k, m=int(g.choice(M_CHOICES)),
+                        n=int(g.integers(1, 2000)), copies=int(g.integers(2, 5)),
+                        sf16=bool(g.integers(0, 2)), y32=bool(g.integers(0, 2)),
+                        code=int(g.integers(0, 2)), seed=int(g.integers(1, 1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("case", _batch_cases(), ids=lambda c: f"b{c['i']}")
+def test_random_batched_linear_against_oracle(ctx, aexq, orc, case):
+    """A replicated weight stack with one activation matrix per copy (batched
+    x and y, batch strides of whole matrices): every copy's output against the
+    oracle for that copy's activations."""
+    c = case
+    _announce("random batched " + " ".join(f"{k}={v}" for k, v in c.items()))
+    from aiimage_amd import synth
+    m, n, k, copies = c["m"], c["n"], c["k"], c["copies"]
+    base, wf = _weight(ctx, aexq, orc, c, c["seed"])
+    w = base.replicate(copies)
+    layout = aexq.LAYOUT_PACK4_LINEAR
+    ydt = torch.float32 if c["y32"] else torch.float16
+    per_y = aexq.tensor_elements(layout, m, n)
+    y = aexq.new_activation(m, n, ydt, layout, batch=copies)
+    xs = [synth.activations(m, k, c["seed"] + 10 + b) for b in range(copies)]
+    xd = aexq.describe(dev(np.concatenate([x.reshape(-1) for x in xs])), m, k,
+                       batch=copies, batch_stride=m * k)
+    yd = aexq.describe(y, m, n, layout, batch=copies, batch_stride=per_y)
+    ctx.linear(w, xd, yd)
+    torch.cuda.synchronize()
+    stride = aexq.storage_elements(layout, m, n)
+    tol = TOL32 if c["y32"] else TOL
+    out = y.cpu().numpy().astype(np.float64)
+    for b in range(copies):
+        ref = orc.gemm_gpu_semantics(xs[b].astype(np.float32), wf)
+        got = out[b * per_y:b * per_y + m * stride].reshape(m, stride)[:, :n]
+        err = normwise(got, ref)
+        assert err <= tol, (b, err)
+    w.release()
+    base.release()
