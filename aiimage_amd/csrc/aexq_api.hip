@@ -1027,9 +1027,10 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   // 64-wide K steps, fp16 activation rows 16-byte aligned; Q4 scale groups of
   // 16 (the reference's shipping Q4) or a multiple of 32
   const bool g16 = fmt == kQ4 && w0->block == 16;
-  const bool gemm_ok = M > 32 && K % 64 == 0 && (fmt == kQ8 || w0->block % 32 == 0 || g16) &&
-                       (rms_in || x_ok) && getenv("AEXQ_QGEMM_OFF") == nullptr;
-  if (gemm_ok && size_ok && !argmax) {
+  const bool gemm_shape_ok = K % 64 == 0 && (fmt == kQ8 || w0->block % 32 == 0 || g16) &&
+                             (rms_in || x_ok) && size_ok && !argmax &&
+                             getenv("AEXQ_QGEMM_OFF") == nullptr;
+  auto try_gemm = [&]() {
     const bool sf16 = w0->scale_dtype == AEXQ_DTYPE_F16;
     // the LDS-direct kernel: Q8 and Q4 groups of 16 or 32; larger Q4 groups
     // (multiples of 32) the register-staged one, 64-row tiles
@@ -1045,7 +1046,8 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       plan->kind = kPlanGemm;
       plan->rms_prepass = rms_in;
     }
-  }
+  };
+  if (M > 32 && gemm_shape_ok) try_gemm();
   if (plan->kind != kPlanGemm && mfma_ok && size_ok) {
     const int mt = M <= 16 ? 1 : 2;
     // 256-wide K steps whose code fetches cover 128 contiguous bytes of 8 rows
@@ -1074,6 +1076,10 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       plan->mblock = 16 * mt;
     }
   }
+  // M = 9..32 where the MFMA block kernel does not apply (K a multiple of 64
+  // but not of 128, Q4 scale groups of 64 or more): the tiled GEMM, its rows
+  // past M masked, rather than the generic kernel
+  if (plan->kind != kPlanMfma && plan->kind != kPlanGemm && M > 8 && gemm_shape_ok) try_gemm();
   if (plan->kind != kPlanMfma && plan->kind != kPlanGemm && chunked && group_ok && x_ok && m_ok && rms_ok && size_ok &&
       chunks > 0) {
     const int mmax = M == 1 ? 1 : 8;
@@ -1100,7 +1106,8 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   } else {
     if (swiglu)
       return fail(AEXQ_ERR_UNSUPPORTED, op,
-                  "SwiGLU-out needs K aligned to 16-byte code chunks, fp16 x and M<=8 | K=%d M=%d "
+                  "SwiGLU-out needs fp16 x and K aligned to 16-byte code chunks at M<=8, to 64 "
+                  "at larger M | K=%d M=%d "
                   "| rejectedFallback=SwiGLU",
                   K, M);
     plan->rows_per_tile = generic_rows_per_wg();

@@ -1,6 +1,7 @@
-"""GPU parity of the tiled GEMM path (M > 32 activation rows: aexq_qgemm_dl.hpp, the
-LDS-direct kernel, and aexq_qgemm.hpp, the register-staged one)
-against the CPU oracle, through the C ABI.
+"""GPU parity of the tiled GEMM path (M > 32 activation rows, and 9..32 rows
+where K or the Q4 scale groups rule out the MFMA block kernel:
+aexq_qgemm_dl.hpp, the LDS-direct kernel, and aexq_qgemm.hpp, the
+register-staged one) against the CPU oracle, through the C ABI.
 
 Bars as in the other parity tests: normwise max|y - r| / max|r| <= 1e-3 of the
 float64 oracle for fp16 outputs, 1e-5 for fp32 outputs; stacked weight copies
@@ -79,6 +80,11 @@ def _weight(ctx, aexq, orc, bits, n, k, seed, group=32, scale_f16=True, code=1):
     (4, 64, False, 520, 1024, 97, True),     # one scale per 64 codes, fp32 scales
     (4, 32, True, 130, 64, 33, True),        # a single K step, 2 rows past a tile
     (4, 32, False, 256, 512, 129, True),     # reference nibble code below
+    # 9..32 rows where the MFMA block kernel does not apply: the tiled GEMM
+    (8, 0, True, 1000, 1088, 16, False),     # K = 17 steps at M = 16
+    (4, 64, True, 768, 1024, 24, True),      # Q4 groups of 64 at M = 24
+    (4, 128, False, 515, 2048, 9, True),     # Q4 groups of 128 at M = 9
+    (8, 0, False, 257, 576, 32, True),       # K = 9 steps at M = 32
 ])
 def test_gemm_formats(ctx, aexq, orc, bits, group, scale_f16, n, k, m, y32):
     _announce(f"qgemm q{bits} g={group} f16={scale_f16} n={n} k={k} m={m}")
@@ -102,12 +108,15 @@ def test_gemm_formats(ctx, aexq, orc, bits, group, scale_f16, n, k, m, y32):
     assert normwise(got[:, :n], ref) <= (TOL32 if y32 else TOL)
 
 
-@pytest.mark.parametrize("bits,m,n", [(4, 64, 3584), (4, 150, 1000), (8, 96, 640)])
-def test_gemm_swiglu_rmsnorm(ctx, aexq, orc, bits, m, n):
-    """gate/up with RMSNorm-in (row pre-pass) and SwiGLU-out on the tiled path."""
-    _announce(f"qgemm swiglu rms q{bits} m={m} n={n}")
+@pytest.mark.parametrize("bits,m,n,k", [(4, 64, 3584, 1024), (4, 150, 1000, 1024),
+                                         (8, 96, 640, 1024), (8, 16, 640, 1088),
+                                         (4, 20, 1000, 576)])
+def test_gemm_swiglu_rmsnorm(ctx, aexq, orc, bits, m, n, k):
+    """gate/up with RMSNorm-in (row pre-pass) and SwiGLU-out on the tiled path,
+    also at 16 and 20 rows with K not a multiple of 128 (no MFMA block kernel)."""
+    _announce(f"qgemm swiglu rms q{bits} m={m} n={n} k={k}")
     from aiimage_amd import synth
-    k, eps = 1024, 1e-6
+    eps = 1e-6
     wg, gf = _weight(ctx, aexq, orc, bits, n, k, 61 + m)
     wu, uf = _weight(ctx, aexq, orc, bits, n, k, 62 + m)
     x16 = synth.activations(m, k, 63)
