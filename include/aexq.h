@@ -72,7 +72,10 @@ typedef int aexq_status;
 
 /* epilogue flags of aexq_linear_args.flags */
 #define AEXQ_EPI_RMSNORM_IN 0x1u   /* x' = fp16(x * rsqrt(max(mean(x^2)+eps,1e-20)) * gamma) (CC:4531-4557) */
-#define AEXQ_EPI_SWIGLU_OUT 0x2u   /* y = swish(x'.Wgate) * (x'.Wup) (MM:106-116, SP:819-831) */
+#define AEXQ_EPI_SWIGLU_OUT 0x2u   /* y = swish(x'.Wgate) * (x'.Wup) (MM:106-116, SP:819-831);
+                                    * runs with fp16 x and K a multiple of 16 code bytes at
+                                    * M <= 8, of 64 above; a shape no kernel takes returns
+                                    * AEXQ_ERR_UNSUPPORTED (no generic fallback) */
 #define AEXQ_EPI_RESIDUAL_ADD 0x4u /* y += residual (BinaryOp Add after o_proj/down) */
 
 typedef struct aexq_ctx aexq_ctx;
