@@ -1844,6 +1844,9 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
   if (!ctx || !cfg || !layers || !embedding || !out)
     return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "NULL argument");
   if (count <= 0) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "count=%d", count);
+  if (count > kStepMaxLayers)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "%d layers (the fused step stages at most %d layer "
+                "entries in LDS) | rejectedFallback=per-operator step", count, kStepMaxLayers);
   if (!cfg->rope_cos || !cfg->rope_sin)
     return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "rope tables are NULL");
   const int hq = cfg->heads_q, hkv = cfg->heads_kv, cap = cfg->capacity;

@@ -34,7 +34,7 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
-from . import aexq, synth
+from . import _abi, aexq, synth
 
 
 @dataclass
@@ -203,10 +203,21 @@ class DecodeSession:
         self.pos.fill_(position)
         self.position = position
 
-    def step(self, advance: bool = False):
+    def check_fused(self):
+        """Raises when a fused run since the last check gave up a bounded wait
+        (its outputs are then invalid).  Synchronizes the stream."""
+        if self.fused is not None and self.fused.error():
+            raise _abi.DeviceError(
+                _abi.ERR_DEVICE,
+                "aexq_decoder_run gave up a bounded wait: the step's outputs are invalid")
+
+    def step(self, advance: bool = False, check: bool = True):
         """One decode step for self.token at the device position ->
         self.next_token.  With `advance` the step also stores the argmax as the
-        next input token (and in self.history) and moves the position on."""
+        next input token (and in self.history) and moves the position on.  On
+        the fused path `check` synchronizes and raises if the run gave up a
+        bounded wait; hot loops and graph capture pass False and call
+        check_fused() once afterwards."""
         c, ctx, d = self.cfg, self.ctx, self.d
         if self.fused is not None:
             self.fused.run(self.token, self.pos, self.xa)
@@ -214,6 +225,8 @@ class DecodeSession:
                               rms_gamma=self.g_final, rms_eps=c.eps)
             if advance:
                 ctx.decode_advance(self.pos, self.token, self.next_token, self.history)
+            if check:
+                self.check_fused()
             return
         ctx.embed_q8(self.embed, self.token, self.xa)
         for L in self.layers:
@@ -244,11 +257,12 @@ class DecodeSession:
             stream.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(stream):
                 for _ in range(warmup):
-                    self.step()
+                    self.step(check=False)
             stream.synchronize()
+            self.check_fused()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
-                self.step(advance=advance)
+                self.step(advance=advance, check=False)
         finally:
             self.ctx.set_stream(old)
         torch.cuda.synchronize()
@@ -270,7 +284,8 @@ class DecodeSession:
             if graph is not None:
                 graph.replay()
             else:
-                self.step(advance=True)
+                self.step(advance=True, check=False)
         torch.cuda.synchronize()
+        self.check_fused()
         self.position = position + count
         return [int(t) for t in self.history[position:position + count].cpu().tolist()]

@@ -36,6 +36,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 # HBM bytes per dispatch of the dominant kernel, from two rocprofv3 --pmc runs of
 # this bench (FETCH_SIZE, WRITE_SIZE) scaled by the calibration kernel's counts
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmv_q4_layer_config2_traffic.json")
+# the sources the dominant launch's kernel is compiled from: the traffic record
+# holds their hash, and a record of other sources is not this build's traffic
+KERNEL_SOURCES = ("include/aexq.h", "aiimage_amd/csrc/aexq_internal.hpp",
+                  "aiimage_amd/csrc/aexq_device.hpp", "aiimage_amd/csrc/aexq_qmv.hpp",
+                  "aiimage_amd/csrc/aexq_qmv_q4.hip")
 LAYER_WEIGHT_BYTES = 9_142_272
 LAYER_ACT_BYTES = 46_080
 LAYER_BYTES = LAYER_WEIGHT_BYTES + LAYER_ACT_BYTES
@@ -67,6 +72,31 @@ def parse():
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def kernel_source_hash() -> str:
+    """sha256 over KERNEL_SOURCES (path, then contents, in order): names the
+    build of the streaming matvec whose traffic a record describes."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        h.update(rel.encode() + b"\0")
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def measured_traffic(launch: str, copies: int):
+    """(HBM bytes per dispatch, note) from the committed counter record, or
+    (None, why not) when the record is of another launch, copy count or build."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None, "no counter record"
+    rec = json.load(open(TRAFFIC_FILE))
+    if rec.get("launch") != launch or rec.get("copies") != copies:
+        return None, f"counter record is of {rec.get('launch')} x {rec.get('copies')} copies"
+    if rec.get("source_sha256") != kernel_source_hash():
+        return None, "counter record is of another build of the kernel sources"
+    return rec.get("hbm_bytes_per_dispatch"), rec.get("source")
 
 
 class Layer:
@@ -421,9 +451,9 @@ def config3(torch, aexq, ctx, steps: int = 30):
         sess.token.fill_(1)
         sess.set_position(cfg.capacity - 1)     # attends over all 2048 positions
         for _ in range(2):
-            sess.step()
+            sess.step(check=False)
         torch.cuda.synchronize()
-        eager_ms = timed(sess.step)
+        eager_ms = timed(lambda: sess.step(check=False))
         g = sess.capture()
         for _ in range(3):
             g.replay()
@@ -639,13 +669,10 @@ def main():
         per[name] = {"ms": avg, "ms_median": med, "bytes": b, "GBps": b / (avg * 1e-3) / 1e9}
     dom = max(per, key=lambda k: per[k]["ms"])
     ach = per[dom]["GBps"]
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        rec = json.load(open(TRAFFIC_FILE))
-        if rec.get("launch") == dom and rec.get("copies") == copies:
-            traffic = rec.get("hbm_bytes_per_dispatch")
+    traffic, traffic_note = measured_traffic(dom, copies)
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "traffic_source": traffic_note, "kernel_source_sha256": kernel_source_hash(),
                 "algorithmic_bytes": per[dom]["bytes"]}
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,

@@ -359,8 +359,9 @@ typedef struct aexq_decoder_config {
   int workgroups;          /* 0: chosen from the capacity */
 } aexq_decoder_config;
 /* Checks every layer (Q4 with one scale per 32 codes, one scale dtype, the
- * model's shapes; head_dim 128; the shapes the fused kernel takes) and the
- * tied Q8 embedding table; AEXQ_ERR_UNSUPPORTED names what it does not take. */
+ * model's shapes; head_dim 128; the shapes the fused kernel takes; at most 64
+ * layers) and the tied Q8 embedding table; AEXQ_ERR_UNSUPPORTED names what it
+ * does not take. */
 aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_config* cfg,
                                 const aexq_decoder_layer* layers, int count,
                                 const aexq_weight* embedding, aexq_decoder** out);

@@ -128,3 +128,112 @@ def test_decoder_rope_tables_equal_oracle_rows(orc, head_dim, base, capacity):
     for p in (0, 1, 2, 37, capacity // 2, capacity - 1):
         c, s = orc.rope_table(p, head_dim, base)
         assert np.array_equal(ct[p], c) and np.array_equal(st[p], s), p
+
+
+# ---------------------------------------------------------------- the C# binding
+
+
+def _cs_dir():
+    import os
+    return os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "bindings", "csharp")
+
+
+def _cs_structs():
+    """{struct: (size, {field: offset})} of every [StructLayout(LayoutKind.Explicit,
+    Size = N)] struct in bindings/csharp/*.cs, read from the source text."""
+    import glob
+    import re
+    out = {}
+    for path in sorted(glob.glob(_cs_dir() + "/*.cs")):
+        text = open(path).read()
+        for m in re.finditer(r"\[StructLayout\(LayoutKind\.Explicit, Size = (\d+)\)\]\s*public struct (\w+)\s*\{(.*?)\n    \}",
+                             text, re.S):
+            size, name, body = int(m.group(1)), m.group(2), m.group(3)
+            fields = {f: int(o) for o, f in re.findall(r"\[FieldOffset\((\d+)\)\] public [\w\.]+ (\w+);", body)}
+            out[name] = (size, fields)
+    return out
+
+
+def _snake(name: str) -> str:
+    import re
+    return re.sub(r"(?<=[a-z0-9])([A-Z])", r"_\1", name).lower()
+
+
+# C# struct -> (C type, {C# field: C member}); members not listed map camelCase -> snake_case
+_CS_TO_C = {
+    "AexqShape": ("aexq_shape", {}),
+    "AexqTensor": ("aexq_tensor", {}),
+    "AexqLinearArgs": ("aexq_linear_args", {}),
+    "AexqWeightInfo": ("aexq_weight_info", {}),
+    "AexqDecoderLayer": ("aexq_decoder_layer", {}),
+    "AexqDecoderConfig": ("aexq_decoder_config", {"attnScale": "attn_scale"}),
+    "HipExternalMemoryHandleDesc": ("hipExternalMemoryHandleDesc",
+                                    {"type": "type", "fd": "handle.fd", "win32Handle": "handle.win32.handle",
+                                     "win32Name": "handle.win32.name", "size": "size", "flags": "flags"}),
+    "HipExternalMemoryBufferDesc": ("hipExternalMemoryBufferDesc",
+                                    {"offset": "offset", "size": "size", "flags": "flags"}),
+    "HipExternalSemaphoreHandleDesc": ("hipExternalSemaphoreHandleDesc",
+                                       {"type": "type", "fd": "handle.fd", "win32Handle": "handle.win32.handle",
+                                        "win32Name": "handle.win32.name", "flags": "flags"}),
+    "HipExternalSemaphoreParams": ("hipExternalSemaphoreSignalParams",
+                                   {"fenceValue": "params.fence.value", "flags": "flags"}),
+}
+
+
+def test_csharp_struct_offsets_match_the_c_compiler(tmp_path):
+    """Every explicit-layout struct of the C# binding has the C compiler's size and
+    member offsets (aexq.h, and hip_runtime_api.h for the external-memory imports;
+    the semaphore wait parameters share the signal parameters' layout)."""
+    import os
+    import subprocess
+    cs = _cs_structs()
+    assert set(cs) == set(_CS_TO_C), sorted(set(cs) ^ set(_CS_TO_C))
+    lines = ["#include <stdio.h>", "#include <stddef.h>", "#include <hip/hip_runtime_api.h>",
+             '#include "aexq.h"', "int main(void){"]
+    for name, (ctype, names) in _CS_TO_C.items():
+        lines.append(f'printf("{name} %zu\\n", sizeof({ctype}));')
+        for f in cs[name][1]:
+            member = names.get(f, _snake(f))
+            lines.append(f'printf("{name}.{f} %zu\\n", offsetof({ctype}, {member}));')
+    lines.append('printf("wait %zu %zu %zu\\n", sizeof(hipExternalSemaphoreWaitParams), '
+                 'offsetof(hipExternalSemaphoreWaitParams, params.fence.value), '
+                 'offsetof(hipExternalSemaphoreWaitParams, flags));')
+    lines.append("return 0;}")
+    probe = tmp_path / "cs_probe.c"
+    probe.write_text("\n".join(lines))
+    exe = tmp_path / "cs_probe"
+    root = os.path.dirname(_cs_dir().rstrip("/").rsplit("/", 1)[0])
+    subprocess.run(["gcc", "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include", "-I",
+                    os.path.join(root, "include"), str(probe), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        k, *v = line.split()
+        got[k] = [int(x) for x in v]
+    for name, (size, fields) in cs.items():
+        assert got[name] == [size], (name, got[name], size)
+        for f, off in fields.items():
+            assert got[f"{name}.{f}"] == [off], (name, f, got[f"{name}.{f}"], off)
+    assert got["wait"] == [cs["HipExternalSemaphoreParams"][0], 0, cs["HipExternalSemaphoreParams"][1]["flags"]]
+
+
+def test_csharp_binding_imports_every_header_function():
+    """bindings/csharp/Native.cs has a DllImport for every function include/aexq.h
+    declares, with the C parameter count, and none the header lacks."""
+    import re
+    text = open(_cs_dir() + "/Native.cs").read()
+    imports = {}
+    for m in re.finditer(r"\[DllImport\(Lib(?:, EntryPoint = \"(\w+)\")?\)\] public static extern [\w\.]+ (\w+)\((.*?)\);",
+                         text, re.S):
+        entry = m.group(1) or m.group(2)
+        params = re.sub(r"/\*.*?\*/", "", m.group(3)).strip()
+        imports.setdefault(entry, set()).add(0 if not params else params.count(",") + 1)
+    header = open(_cs_dir().rsplit("/", 2)[0] + "/include/aexq.h").read()
+    header = re.sub(r"/\*.*?\*/", "", header, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"^(?:aexq_status|void|int|const char\*)\s+(aexq_\w+)\((.*?)\);", header, re.S | re.M):
+        params = m.group(2).strip()
+        decls[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    assert set(decls) == set(_abi.header_functions())
+    assert set(imports) == set(decls), sorted(set(imports) ^ set(decls))
+    for name, n in decls.items():
+        assert imports[name] == {n}, (name, imports[name], n)

@@ -245,3 +245,7 @@ def test_fused_rejects_shapes_it_does_not_take(ctx, aexq):
         ctx.decoder([layer], sess.embed, **dict(args, head_dim=64))
     with pytest.raises(aexq.NotSupportedError):          # cache beyond the split budget
         ctx.decoder([layer], sess.embed, **dict(args, capacity=1 << 16))
+    with pytest.raises(aexq.NotSupportedError, match="64"):  # more layers than the LDS table holds
+        ctx.decoder([layer] * 65, sess.embed, **args)
+    d = ctx.decoder([layer] * 64, sess.embed, **args)  # the largest table is accepted
+    d.close()

@@ -532,6 +532,30 @@ def test_sdpa_decode_properties(orc):
     np.testing.assert_allclose(o[0], orc.sdpa_decode(q8[:1], k2[:1], v2[:1], 0.3)[0], rtol=1e-12)
 
 
+@pytest.mark.parametrize("scale", [0.37, 0.23])
+def test_sdpa_decode_score_scale_closed_form(orc, scale):
+    """MM:477 multiplies each score q.k by the scale before the softmax.  Two
+    positions with scores s1, s2 give (v1 e^(a s1) + v2 e^(a s2)) / (e^(a s1) +
+    e^(a s2)) with a = scale, computed here in float64 from hand-chosen keys:
+    q = (1, 2, 0, 0), k1 = (3, 0, 0, 0) (s1 = 3), k2 = (0, -1, 0, 0) (s2 = -2).
+    A dropped, inverted or squared scale moves the output well past the
+    tolerance at both scales."""
+    q = np.array([[1.0, 2.0, 0.0, 0.0]], np.float32)
+    k = np.array([[[3.0, 0.0, 0.0, 0.0], [0.0, -1.0, 0.0, 0.0]]], np.float32)
+    v = np.array([[[1.0, -2.0, 0.5, 4.0], [-3.0, 1.0, 2.0, 0.25]]], np.float32)
+    s1, s2 = 3.0, -2.0
+
+    def expect(a):
+        e1, e2 = math.exp(a * s1), math.exp(a * s2)
+        return (v[0, 0].astype(np.float64) * e1 + v[0, 1].astype(np.float64) * e2) / (e1 + e2)
+
+    got = orc.sdpa_decode(q, k, v, scale)[0].astype(np.float64)
+    np.testing.assert_allclose(got, expect(scale), rtol=2e-6, atol=2e-6)
+    for wrong in (1.0, 1.0 / scale, scale * scale):
+        assert np.max(np.abs(expect(wrong) - expect(scale))) > 1e-2, wrong
+    assert np.max(np.abs(got - orc.sdpa_decode(q, k, v, 1.0)[0])) > 1e-2
+
+
 def test_head_packed_layout_positions(orc):
     """The attention head-packed layout against texel positions worked out by
     hand from MM:1192-1318 (texel (dim, row, head / 4), lane head % 4, lanes of
