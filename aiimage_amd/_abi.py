@@ -36,6 +36,7 @@ LAYOUT_HEAD_PACKED = 3
 EPI_RMSNORM_IN = 0x1
 EPI_SWIGLU_OUT = 0x2
 EPI_RESIDUAL_ADD = 0x4
+EPI_ARGMAX_F16 = 0x8
 
 
 class AexqError(RuntimeError):

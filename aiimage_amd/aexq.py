@@ -261,13 +261,17 @@ class Context:
     def lmhead_argmax(self, w: "QuantWeight", x: _abi.Tensor, logits: Optional[_abi.Tensor],
                       argmax: torch.Tensor, top2_gap: Optional[torch.Tensor] = None, *,
                       rms_gamma: Optional[torch.Tensor] = None, rms_eps: float = 1e-3,
-                      rmsnorm: bool = False):
+                      rmsnorm: bool = False, argmax_f16: bool = False):
         """Greedy token of the LM head; with rmsnorm=True the final RMSNorm
-        (gamma rms_gamma) is applied to x inside the same launch."""
+        (gamma rms_gamma) is applied to x inside the same launch; with
+        argmax_f16=True the argmax compares the logits rounded to fp16 (the
+        reference's ARGBHalf logits texture, GL:383-396)."""
         gap = ctypes.c_void_p(top2_gap.data_ptr()) if top2_gap is not None else None
         lg = ctypes.byref(logits) if logits is not None else None
-        if rmsnorm:
-            args = make_args(rms_gamma=rms_gamma, rms_eps=rms_eps, rmsnorm=True)
+        if rmsnorm or argmax_f16:
+            args = make_args(rms_gamma=rms_gamma, rms_eps=rms_eps, rmsnorm=rmsnorm)
+            if argmax_f16:
+                args.flags |= _abi.EPI_ARGMAX_F16
             check(self._lib.aexq_lmhead_argmax_ex(
                 self.handle, w.handle, ctypes.byref(x), lg, ctypes.byref(args),
                 ctypes.c_void_p(argmax.data_ptr()), gap), "aexq_lmhead_argmax_ex")

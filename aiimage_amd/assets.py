@@ -49,6 +49,8 @@ _DEFAULT_BITS = {MANIFEST_SCHEMA: 8, Q4_MANIFEST_SCHEMA: 4}
 
 ARCHIVE_HEADER_BYTES = 32   # AQSGET8 archive header (Q8A:26-33)
 RECORD_HEADER_BYTES = 24    # record header; payload byte count at offset 16 (Q8A:60-65)
+RECORD_MAGIC = 0x31523851   # "Q8R1" (Q8A:28)
+RECORD_RAW = 2              # raw fp32 record kind (Q8A:32)
 
 _HASH_BLOCK = 8 << 20
 
@@ -308,17 +310,60 @@ ShardReadStream = ShardedFile
 # ----------------------------------------------------------------- archive walk
 
 
+def read_archive_header(stream) -> Tuple[int, int, int]:
+    """The 32-byte AQSGET8 header at the stream's position, checked as the
+    reader's constructor does (Q8A:277-293): (quant_bits, default_block,
+    record_count)."""
+    from .aexq import archive_header
+    read = stream.read_exact if hasattr(stream, "read_exact") else stream.read
+    return archive_header(read(ARCHIVE_HEADER_BYTES))
+
+
+def read_float_record(stream, count: int):
+    """One raw fp32 record (kind 2, written by WriteFloat32Array, Q8A:216-223)
+    of `count` values, as ReadArray reads it with requireRaw (Q8A:295-306): the
+    RMSNorm weights and other small constants of an archive.  Returns a
+    float32 numpy array."""
+    import numpy as np
+    read = stream.read_exact if hasattr(stream, "read_exact") else stream.read
+    rh = read(RECORD_HEADER_BYTES)
+    if len(rh) != RECORD_HEADER_BYTES:
+        raise InvalidDataError("archive stream ends inside a record header")
+    magic, kind, elements, block, payload = struct.unpack_from("<Iiiii", rh, 0)
+    if magic != RECORD_MAGIC:
+        raise InvalidDataError("Invalid Q8 record magic.")
+    if elements != count:
+        raise InvalidDataError("Q8 record element count mismatch. expected=%d actual=%d."
+                               % (count, elements))
+    if block <= 0 or payload < 0:
+        raise InvalidDataError("Invalid Q8 record header.")
+    if kind != RECORD_RAW:
+        raise InvalidDataError("Expected a raw FP32 quantized archive record.")
+    if payload != count * 4:
+        raise InvalidDataError("Q8 raw float record size mismatch.")
+    body = read(payload)
+    if len(body) != payload:
+        raise InvalidDataError("archive stream ends inside a record payload")
+    return np.frombuffer(body, "<f4").astype(np.float32)
+
+
 def load_archive_weights(ctx, stream, shapes: Sequence[Tuple[int, int, int]]):
     """Walk an AQSGET8 archive (header, then one record per Gemm weight in model
     order) from `stream` into device weights: `shapes` gives (n, k, bits) of
     each record's layer (Q8A:277-293 header, GL:60-141 per record).  Returns
     (weights, (quant_bits, default_block, record_count))."""
-    from .aexq import archive_header
-    read = stream.read_exact if hasattr(stream, "read_exact") else stream.read
-    header = archive_header(read(ARCHIVE_HEADER_BYTES))
+    header = read_archive_header(stream)
     if len(shapes) > header[2]:
         raise InvalidDataError("archive holds %d records, %d layers asked for"
                                % (header[2], len(shapes)))
+    return read_weight_records(ctx, stream, shapes), header
+
+
+def read_weight_records(ctx, stream, shapes: Sequence[Tuple[int, int, int]]):
+    """The next len(shapes) Gemm weight records of an archive stream into
+    device weights, (n, k, bits) per record (GL:60-141).  On failure the
+    weights made so far are released."""
+    read = stream.read_exact if hasattr(stream, "read_exact") else stream.read
     weights = []
     try:
         for n, k, bits in shapes:
@@ -339,4 +384,4 @@ def load_archive_weights(ctx, stream, shapes: Sequence[Tuple[int, int, int]]):
             if hasattr(w, "release"):
                 w.release()
         raise
-    return weights, header
+    return weights

@@ -880,8 +880,11 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   def.broadcast_c = -1;
   def.rms_eps = 0.001f;
   const aexq_linear_args& a = args ? *args : def;
-  const unsigned known = AEXQ_EPI_RMSNORM_IN | AEXQ_EPI_SWIGLU_OUT | AEXQ_EPI_RESIDUAL_ADD;
-  if (a.flags & ~known) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "flags=0x%x", a.flags);
+  const unsigned known = AEXQ_EPI_RMSNORM_IN | AEXQ_EPI_SWIGLU_OUT | AEXQ_EPI_RESIDUAL_ADD |
+                         (argmax ? AEXQ_EPI_ARGMAX_F16 : 0u);
+  if (a.flags & ~known)
+    return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "flags=0x%x%s", a.flags,
+                (a.flags & AEXQ_EPI_ARGMAX_F16) && !argmax ? " (ARGMAX_F16 is for the LM head)" : "");
   const aexq_weight* w0 = ws[0];
   if (!w0) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "weight is NULL");
   for (int i = 0; i < count; ++i)
@@ -972,8 +975,8 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     if (ys[i]->layout != ys[0]->layout)
       return fail(AEXQ_ERR_UNSUPPORTED, op, "group outputs differ in layout");
   }
-  if (argmax && yv[0].dtype != AEXQ_DTYPE_F32)
-    return fail(AEXQ_ERR_UNSUPPORTED, op, "LM-head logits must be fp32");
+  if (argmax && yv[0].dtype != AEXQ_DTYPE_F32 && yv[0].dtype != AEXQ_DTYPE_F16)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "LM-head logits must be fp32 or fp16");
   if (yv[0].head_dim && (argmax || (a.flags & AEXQ_EPI_RESIDUAL_ADD)))
     return fail(AEXQ_ERR_UNSUPPORTED, op,
                 "head-packed y with %s | rejectedFallback=attention-head-packed Gemm",
@@ -1142,6 +1145,9 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   if (ylayout != AEXQ_LAYOUT_PACK4_TILED) flags |= kFlagAlphaIn;
   if (w0->scale_dtype == AEXQ_DTYPE_F16) flags |= kFlagScaleF16;
   if (xv.dtype == AEXQ_DTYPE_F32) flags |= kFlagXf32;
+  // the reference's argmax reads its logits texture: ARGBHalf holds fp16 values
+  if (argmax && ((a.flags & AEXQ_EPI_ARGMAX_F16) || yv[0].dtype == AEXQ_DTYPE_F16))
+    flags |= kFlagArgF16;
   p.flags = flags;
 
   int tiles_total = 0;
@@ -1448,14 +1454,16 @@ static aexq_status ensure_parts(aexq_ctx* ctx, long long need, const char* op) {
   return st;
 }
 
-static aexq_status argmax_over_logits(aexq_ctx* ctx, const float* logits, int m, int n,
+// mode: kLogitsF32, kLogitsF16 (fp16 logits), kLogitsF32AsF16 (fp32 logits
+// compared after rounding to fp16)
+static aexq_status argmax_over_logits(aexq_ctx* ctx, const void* logits, int mode, int m, int n,
                                       long long rstride, int32_t* argmax, float* gap,
                                       const char* op) {
   const int parts = (n + logits_argmax_cols_per_wg() - 1) / logits_argmax_cols_per_wg();
   aexq_status st = ensure_parts(ctx, (long long)parts * m, op);
   if (st) return st;
-  hipError_t e = logits_argmax_launch(logits, m, n, rstride, ctx->part_best, ctx->part_index,
-                                      ctx->part_second, parts, ctx->stream);
+  hipError_t e = logits_argmax_launch(logits, mode, m, n, rstride, ctx->part_best,
+                                      ctx->part_index, ctx->part_second, parts, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, op, "argmax launch");
   ArgmaxParams ap{ctx->part_best, ctx->part_index, ctx->part_second, parts, m, argmax, gap};
   e = argmax_finalize_launch(ap, ctx->stream);
@@ -1548,10 +1556,13 @@ static aexq_status lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w, const aexq
   if (lmhead_fused(plan)) return lmhead_fused_launch(ctx, plan, op, argmax, top2_gap, nullptr);
   // logits first (into the caller's tensor or a scratch buffer), then the argmax pass
   const int M = plan.p.m;
-  float* lg = nullptr;
+  void* lg = nullptr;
   long long rstride = plan.p.mat[0].y_rstride;
+  const bool f16_cmp = (plan.p.flags & kFlagArgF16) != 0;
+  int mode = f16_cmp ? kLogitsF32AsF16 : kLogitsF32;
   if (logits) {
-    lg = (float*)logits->data;
+    lg = logits->data;
+    if (logits->dtype == AEXQ_DTYPE_F16) mode = kLogitsF16;
   } else {
     const long long need = (long long)M * w->n;
     st = grow_scratch(ctx, (void**)&ctx->logits_scratch, &ctx->logits_cap,
@@ -1565,7 +1576,7 @@ static aexq_status lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w, const aexq
   }
   st = launch_plan(ctx, plan, op);
   if (st) return st;
-  return argmax_over_logits(ctx, lg, M, w->n, rstride, argmax, top2_gap, op);
+  return argmax_over_logits(ctx, lg, mode, M, w->n, rstride, argmax, top2_gap, op);
 }
 
 extern "C" aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w,
@@ -1579,9 +1590,10 @@ extern "C" aexq_status aexq_lmhead_argmax_ex(aexq_ctx* ctx, const aexq_weight* w
                                              const aexq_linear_args* args, int32_t* argmax,
                                              float* top2_gap) {
   const char* op = "aexq_lmhead_argmax_ex";
-  if (args && (args->flags & ~(unsigned)AEXQ_EPI_RMSNORM_IN))
+  if (args && (args->flags & ~(unsigned)(AEXQ_EPI_RMSNORM_IN | AEXQ_EPI_ARGMAX_F16)))
     return fail(AEXQ_ERR_UNSUPPORTED, op,
-                "epilogue flags 0x%x: the LM head takes RMSNorm-in only | rejectedFallback=epilogue",
+                "epilogue flags 0x%x: the LM head takes RMSNorm-in and the fp16-logit argmax only "
+                "| rejectedFallback=epilogue",
                 args->flags);
   return lmhead_argmax(ctx, w, x, logits, args, argmax, top2_gap, op);
 }
@@ -1625,11 +1637,11 @@ extern "C" aexq_status aexq_argmax(aexq_ctx* ctx, const aexq_tensor* logits, int
   TensorView v;
   aexq_status st = view_tensor(logits, op, "logits", &v);
   if (st) return st;
-  if (v.dtype != AEXQ_DTYPE_F32)
-    return fail(AEXQ_ERR_UNSUPPORTED, op, "logits dtype must be fp32 | rejectedFallback=dtype");
+  if (v.head_dim)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "head-packed logits | rejectedFallback=layout");
   HIP_TRY(op, hipSetDevice(ctx->device));
-  return argmax_over_logits(ctx, (const float*)v.data, v.rows, v.width, v.rstride, argmax,
-                            top2_gap, op);
+  return argmax_over_logits(ctx, v.data, v.dtype == AEXQ_DTYPE_F16 ? kLogitsF16 : kLogitsF32,
+                            v.rows, v.width, v.rstride, argmax, top2_gap, op);
 }
 
 extern "C" aexq_status aexq_dequant(aexq_ctx* ctx, const aexq_weight* w, float* out) {
@@ -1861,7 +1873,16 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
   const int hid = l0q->k, qw = hq * kStepHeadDim, kvw = hkv * kStepHeadDim;
   const int inter = layers[0].gate_proj ? layers[0].gate_proj->n : 0;
   const int sdt = l0q->scale_dtype;
-  // every layer: Q4, one scale per 32 codes, the model's shapes, one scale dtype
+  // the layer format of q_proj: Q4 with one scale per 32 or 16 codes, or Q8
+  // with one scale per row; every weight of every layer must share it
+  const int fmt = l0q->bits == 8 ? kQ8 : kQ4;
+  const int gmode = fmt == kQ8 ? kGRow : (l0q->block == 16 ? kG16 : kG32);
+  const bool fmt_ok = fmt == kQ8 ? l0q->block == l0q->k : (l0q->block == 16 || l0q->block == 32);
+  if (!fmt_ok)
+    return fail(AEXQ_ERR_UNSUPPORTED, op,
+                "layer 0 q_proj: bits=%d block=%d (the fused step takes Q4 with one scale per 32 "
+                "or 16 codes, or Q8 with one scale per row) | rejectedFallback=per-operator step",
+                l0q->bits, l0q->block);
   for (int l = 0; l < count; ++l) {
     const aexq_decoder_layer& L = layers[l];
     const aexq_weight* ws[7] = {L.q_proj, L.k_proj, L.v_proj, L.o_proj, L.gate_proj, L.up_proj,
@@ -1871,14 +1892,17 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
     for (int i = 0; i < 7; ++i) {
       const aexq_weight* w = ws[i];
       if (!w) return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "layer %d weight %d is NULL", l, i);
-      if (w->bits != 4 || w->block != 32 || w->batch != 1 || w->scale_dtype != sdt)
-        return fail(AEXQ_ERR_UNSUPPORTED, op,
-                    "layer %d weight %d: bits=%d block=%d batch=%d scale_dtype=%d (the fused step "
-                    "takes unstacked Q4 with one scale per 32 codes) | rejectedFallback=per-operator "
-                    "step", l, i, w->bits, w->block, w->batch, w->scale_dtype);
       if (w->n != nn[i] || w->k != kk[i])
         return fail(AEXQ_ERR_SHAPE, op, "layer %d weight %d is %dx%d, expected %dx%d", l, i,
                     w->n, w->k, nn[i], kk[i]);
+      const int want_block = fmt == kQ8 ? w->k : l0q->block;
+      if (w->bits != l0q->bits || w->block != want_block || w->batch != 1 ||
+          w->scale_dtype != sdt)
+        return fail(AEXQ_ERR_UNSUPPORTED, op,
+                    "layer %d weight %d: bits=%d block=%d batch=%d scale_dtype=%d, layer 0 q_proj "
+                    "bits=%d block=%d scale_dtype=%d (the fused step takes one unstacked format "
+                    "for every weight) | rejectedFallback=per-operator step", l, i, w->bits,
+                    w->block, w->batch, w->scale_dtype, l0q->bits, l0q->block, sdt);
       if (w->device != ctx->device)
         return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "layer %d weight %d lives on device %d", l, i,
                     w->device);
@@ -1889,12 +1913,13 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
   if (embedding->bits != 8 || embedding->k != hid || embedding->batch != 1)
     return fail(AEXQ_ERR_UNSUPPORTED, op, "embedding bits=%d k=%d batch=%d (Q8 of width %d)",
                 embedding->bits, embedding->k, embedding->batch, hid);
+  const int ce = fmt == kQ8 ? 16 : 32;  // codes per 16-byte chunk
   if (hid % 32 || hid > kStepMaxHidden || inter % 32 || inter > kStepMaxInter ||
-      !decode_layers_supported(hq / hkv, hid / 32, qw / 32, inter / 32))
+      !decode_layers_supported(fmt, gmode, hq / hkv, hid / ce, qw / ce, inter / ce))
     return fail(AEXQ_ERR_UNSUPPORTED, op,
-                "hidden=%d q width=%d intermediate=%d, %d q heads per kv head: no fused-step "
+                "hidden=%d q width=%d intermediate=%d, %d q heads per kv head, %s: no fused-step "
                 "kernel for these shapes | rejectedFallback=per-operator step",
-                hid, qw, inter, hq / hkv);
+                hid, qw, inter, hq / hkv, fmt == kQ8 ? "Q8" : "Q4");
   const int grid = decoder_grid(hkv, cap, cfg->workgroups);
   int splits = grid / hkv;
   if (splits > kStepMaxSplits) splits = kStepMaxSplits;
@@ -1914,7 +1939,7 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
                 cap, grid, splits, sp, merge, rq, rh, ri);
   HIP_TRY(op, hipSetDevice(ctx->device));
   int per_cu = 0;
-  HIP_TRY(op, decode_layers_occupancy(&per_cu));
+  HIP_TRY(op, decode_layers_occupancy(fmt, gmode, &per_cu));
   if ((long long)per_cu * ctx->cus < grid)
     return fail(AEXQ_ERR_UNSUPPORTED, op,
                 "%d workgroups are not co-resident (%d per CU x %d CUs) | rejectedFallback="
@@ -1961,6 +1986,8 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
   p.hq = hq;
   p.hkv = hkv;
   p.cap = cap;
+  p.fmt = fmt;
+  p.gmode = gmode;
   p.sf16 = sdt == AEXQ_DTYPE_F16;
   p.eps = cfg->rms_eps;
   p.scale = cfg->attn_scale;

@@ -308,6 +308,12 @@ __device__ __forceinline__ long long out_index(const QmvParams& p, const QmvMat&
 
 // The LM head's epilogue: gemm_epilogue without a C term (the argmax
 // launches take none), the same arithmetic.
+// The logit an argmax compares: fp16-rounded when the reference's logits
+// texture is ARGBHalf (GL:383-396; its argmax reads those values, MM:645-686).
+__device__ __forceinline__ float argmax_logit(const QmvParams& p, float v) {
+  return (p.flags & kFlagArgF16) ? (float)(f16)v : v;
+}
+
 __device__ __forceinline__ float argmax_epilogue(const QmvParams& p, float v) {
   return (p.flags & kFlagAlphaIn) ? p.alpha * (0.0f + v) : 0.0f + p.alpha * v;
 }

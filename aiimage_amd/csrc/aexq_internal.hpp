@@ -24,6 +24,7 @@ enum : int {
   kFlagScaleF16 = 16,  // scales are fp16 (else fp32)
   kFlagXf32 = 32,      // activations fp32 (generic kernel only)
   kFlagXShared = 64,   // M = 1 streaming RMSNorm-in: every tile multiplies the same row
+  kFlagArgF16 = 128,   // LM head: the argmax compares logits rounded to fp16 (ARGBHalf texture)
 };
 
 // Scale granularity of a streaming kernel: one per row (Q8), per 16 codes
@@ -185,8 +186,10 @@ hipError_t splitk_reduce_launch(const QmvParams& p, int nw, int q8_scale, int sf
                                 hipStream_t stream);
 int generic_rows_per_wg();
 hipError_t argmax_finalize_launch(const ArgmaxParams& a, hipStream_t stream);
-hipError_t logits_argmax_launch(const float* logits, int m, int n, long long rstride, float* pv,
-                                int* pi, float* ps, int parts, hipStream_t stream);
+// element type of the logits an argmax pass reads
+enum : int { kLogitsF32 = 0, kLogitsF16 = 1, kLogitsF32AsF16 = 2 };
+hipError_t logits_argmax_launch(const void* logits, int mode, int m, int n, long long rstride,
+                                float* pv, int* pi, float* ps, int parts, hipStream_t stream);
 int logits_argmax_cols_per_wg();
 // AQSGET8 Q8 / Q4 record payload (after its 24-byte header) into the device
 // codes and fp32 scales of a weight with `count` elements.
@@ -252,7 +255,8 @@ struct StepParams {
   const StepLayer* layers;  // device array [nlayers]
   int nlayers;
   int hidden, qw, kvw, inter, hq, hkv, cap;
-  int sf16;                 // Q4 scales fp16 (else fp32), one per 32 codes
+  int fmt, gmode;           // layer weights: kQ4 with kG32 / kG16 scale groups, or kQ8 per row
+  int sf16;                 // layer scales fp16 (else fp32)
   float eps, scale;
   const uint32_t* emb_codes;  // tied Q8 table [vocab][hidden] (device bytes q + 128)
   const void* emb_scales;
@@ -276,12 +280,13 @@ struct StepParams {
   int splits, split_pos;               // attention workgroups per kv head, positions each
   int merge_dims;                      // output dims per merging workgroup
 };
-// Whether the fused step has a kernel for q heads per kv head `gq` and the
-// code chunks (32 codes) per row of the hidden, q and intermediate widths.
-bool decode_layers_supported(int gq, int ch_hidden, int ch_q, int ch_inter);
+// Whether the fused step has a kernel for the layer format (fmt, gmode), q
+// heads per kv head `gq` and the 16-byte code chunks (32 Q4 or 16 Q8 codes) per
+// row of the hidden, q and intermediate widths.
+bool decode_layers_supported(int fmt, int gmode, int gq, int ch_hidden, int ch_q, int ch_inter);
 hipError_t decode_layers_launch(const StepParams& p, int grid, hipStream_t stream);
-// Resident workgroups of the fused step's kernel per CU.
-hipError_t decode_layers_occupancy(int* per_cu);
+// Resident workgroups per CU of the fused step's kernel for a layer format.
+hipError_t decode_layers_occupancy(int fmt, int gmode, int* per_cu);
 
 // One decode step's bookkeeping on the device: tokens_out[*position] (when
 // non-null and the position is below out_cap) and *token take *argmax, then

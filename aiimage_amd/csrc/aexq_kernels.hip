@@ -152,7 +152,8 @@ hipError_t rmsnorm_rows_launch(const void* x, int x_f32, long long x_rstride, lo
 // ---------------------------------------------------------------------------
 constexpr int kArgmaxCols = 4096;
 
-__global__ __launch_bounds__(kThreads) void logits_argmax_kernel(const float* logits, int n,
+template <typename T, bool ROUND>
+__global__ __launch_bounds__(kThreads) void logits_argmax_kernel(const T* logits, int n,
                                                                  long long rstride, float* pv,
                                                                  int* pi, float* ps, int parts) {
   const int m = blockIdx.y, part = blockIdx.x;
@@ -162,7 +163,8 @@ __global__ __launch_bounds__(kThreads) void logits_argmax_kernel(const float* lo
   int bix = 0x7fffffff;
   float bs = -INFINITY;
   for (int c = c0 + (int)threadIdx.x; c < c1; c += kThreads) {
-    argmax_merge(bv, bix, bs, logits[(long long)m * rstride + c], c, -INFINITY);
+    const float v = (float)logits[(long long)m * rstride + c];
+    argmax_merge(bv, bix, bs, ROUND ? (float)(f16)v : v, c, -INFINITY);
   }
   argmax_wave_reduce(bv, bix, bs);
   __shared__ float sv[kWaves], ss[kWaves];
@@ -417,10 +419,17 @@ hipError_t generic_launch(int fmt, const QmvParams& p, int grid, hipStream_t str
 
 int logits_argmax_cols_per_wg() { return kArgmaxCols; }
 
-hipError_t logits_argmax_launch(const float* logits, int m, int n, long long rstride, float* pv,
-                                int* pi, float* ps, int parts, hipStream_t stream) {
-  hipLaunchKernelGGL(logits_argmax_kernel, dim3(parts, m), dim3(kThreads), 0, stream, logits, n,
-                     rstride, pv, pi, ps, parts);
+hipError_t logits_argmax_launch(const void* logits, int mode, int m, int n, long long rstride,
+                                float* pv, int* pi, float* ps, int parts, hipStream_t stream) {
+  if (mode == kLogitsF16)
+    hipLaunchKernelGGL((logits_argmax_kernel<f16, false>), dim3(parts, m), dim3(kThreads), 0,
+                       stream, (const f16*)logits, n, rstride, pv, pi, ps, parts);
+  else if (mode == kLogitsF32AsF16)
+    hipLaunchKernelGGL((logits_argmax_kernel<float, true>), dim3(parts, m), dim3(kThreads), 0,
+                       stream, (const float*)logits, n, rstride, pv, pi, ps, parts);
+  else
+    hipLaunchKernelGGL((logits_argmax_kernel<float, false>), dim3(parts, m), dim3(kThreads), 0,
+                       stream, (const float*)logits, n, rstride, pv, pi, ps, parts);
   return hipGetLastError();
 }
 

@@ -282,7 +282,8 @@ struct QmmW {
         for (int r = 0; r < 4; ++r) {
           const int row = 16 * m + 4 * mq + r;
           if (row < p.m) {
-            const float v = gemm_epilogue(p, p.m_base + row, n, acc.v[0][m][nt][r] * rs);
+            const float v =
+                argmax_logit(p, gemm_epilogue(p, p.m_base + row, n, acc.v[0][m][nt][r] * rs));
             argmax_merge(b.v[m][r], b.i[m][r], b.s[m][r], v, n, -INFINITY);
           }
         }

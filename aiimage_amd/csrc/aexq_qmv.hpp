@@ -514,7 +514,7 @@ struct Qmv {
           if (sub == ((u * MMAX + m) & (LPR - 1)) && r < mt.n_store && m < p.m &&
               li < kArgLogitsMax)
             lg[li] = v;
-          if (sub == 0 && live) argmax_merge(bv[m], bi[m], bs[m], v, r, -INFINITY);
+          if (sub == 0 && live) argmax_merge(bv[m], bi[m], bs[m], argmax_logit(p, v), r, -INFINITY);
           continue;
         }
         if (live) {

@@ -49,8 +49,12 @@
 // exactly that load), the poll waves only loads, and the store wave only
 // stores.
 //
-// Arithmetic of the linears follows the streaming kernel (aexq_qmv.hpp) for
-// the same shapes (lanes per row, chunks per lane): the same RMSNorm-in
+// The layer weights are Q4 with one scale per 32 codes (the benchmark's
+// format), Q4 with one per 16 (the reference's shipping archives, Q8A:116-139)
+// or Q8 with one scale per row (Q8A:94-114), scales fp16 or fp32; the format
+// is a template parameter of the kernel.  Arithmetic of the linears follows
+// the streaming kernel (aexq_qmv.hpp) for the same format and shapes (lanes
+// per row, chunks per lane): the same RMSNorm-in
 // (sums of squares over 8-element slices, DPP wave sums, four partials in
 // order; fp16(x * inv * gamma)), the same per-chunk dot-product order and
 // group-scale fmaf, the same DPP row reduction and epilogue, so each linear's
@@ -183,9 +187,10 @@ __device__ __forceinline__ void pw_vec_plain(const uint32_t* src, int count, uin
 }
 
 // Poll wave pw of kPW: its share of a tagged fp16 vector of `count` words
-// (count % 8 == 0, count <= 256 * NV * kPW) into dst in the nibble-pair order
-// of q4_xpairs per 8 elements (the order row_dot consumes).
-template <int NV>
+// (count % 8 == 0, count <= 256 * NV * kPW) into dst in the order row_dot
+// consumes: the nibble-pair order of q4_xpairs per 8 elements for Q4 weights
+// (PAIRS), plain for Q8.
+template <int NV, bool PAIRS>
 __device__ __forceinline__ void pw_vec_pairs(const uint32_t* src, int count, uint32_t tag, f16* dst,
                                              int lane, int pw, int* err, bool& broken) {
   static_assert(NV % 2 == 0, "two groups per 8 elements");
@@ -204,17 +209,26 @@ __device__ __forceinline__ void pw_vec_pairs(const uint32_t* src, int count, uin
       uint32_t a, b, c, d, xp[4];
       halves(v[2 * i], a, b);
       halves(v[2 * i + 1], c, d);
-      q4_xpairs(a, b, c, d, xp);
+      if constexpr (PAIRS) {
+        q4_xpairs(a, b, c, d, xp);
+      } else {
+        xp[0] = a;
+        xp[1] = b;
+        xp[2] = c;
+        xp[3] = d;
+      }
       *(u32x4*)(dst + off[2 * i]) = u32x4{xp[0], xp[1], xp[2], xp[3]};
     }
 }
 
 // Poll wave: RMSNorm-in of the fp16 row x (LDS, plain, k <= 2048) into out
-// (LDS, nibble-pair order), bit-exact with the streaming kernel's staged path
+// (LDS, nibble-pair order for Q4 weights, plain for Q8), bit-exact with the
+// streaming kernel's staged path
 // (Qmv::stage_finish): that path's 256 threads each own the 8-element slice
 // vt * 8 and their sums of squares meet as four wave sums added in order;
 // lane l here stands in for threads l, l + 64, l + 128, l + 192.  Each element
 // is rounded once as fp16(x * inv * gamma[i]).
+template <bool PAIRS>
 __device__ __forceinline__ void pw_rms(const f16* x, const float* gamma, f16* out, int k, float eps,
                                        int lane) {
   u32x4 xv[4];
@@ -253,7 +267,14 @@ __device__ __forceinline__ void pw_rms(const f16* x, const float* gamma, f16* ou
         o[e] = as_u(r);
       }
       uint32_t xp[4];
-      q4_xpairs(o[0], o[1], o[2], o[3], xp);
+      if constexpr (PAIRS) {
+        q4_xpairs(o[0], o[1], o[2], o[3], xp);
+      } else {
+        xp[0] = o[0];
+        xp[1] = o[1];
+        xp[2] = o[2];
+        xp[3] = o[3];
+      }
       *(u32x4*)(out + e0) = u32x4{xp[0], xp[1], xp[2], xp[3]};
     }
   }
@@ -332,25 +353,40 @@ __device__ __forceinline__ void sw_copy(uint32_t* dst, const uint32_t* src, int 
   for (int i = lane; i < n; i += 64) st_word(dst + i, src[i]);
 }
 
+// Scale words a lane holds per row slot: one per row (Q8), one per 32-code
+// chunk (Q4, groups of 32) or two (Q4, groups of 16).
+template <int FMT, int GM, int CPL>
+constexpr int slot_scales() {
+  return FMT == kQ8 ? 1 : (GM == kG16 ? 2 * CPL : CPL);
+}
+// Scales per row of a matrix with `chunks` code chunks per row.
+template <int FMT, int GM>
+__device__ __forceinline__ int row_scales(int chunks) {
+  return FMT == kQ8 ? 1 : (GM == kG16 ? 2 * chunks : chunks);
+}
+
 // Prefetched codes and scale words of one row slot (NW = 2: a gate/up pair).
-template <int CPL, int NW>
+template <int FMT, int GM, int CPL, int NW>
 struct Slot {
   u32x4 w[NW][CPL];
-  uint32_t s[NW][CPL];
+  uint32_t s[NW][slot_scales<FMT, GM, CPL>()];
 };
 
 // Issues one wave's slot loads: rows r0 + slot of a matrix of n rows and
-// `chunks` 16-byte code chunks per row (32 codes, one scale each).  Rows past
-// n, chunks past K and a dead wave (live false) read zeros without traffic.
-template <int LPR, int CPL, int NW>
-__device__ __forceinline__ void issue_slot(Slot<CPL, NW>& sl, const uint32_t* w0, const void* s0,
-                                           const uint32_t* w1, const void* s1, int n, int r0,
-                                           int chunks, bool sf16, bool live, int t) {
+// `chunks` 16-byte code chunks per row (32 Q4 or 16 Q8 codes each).  Rows
+// past n, chunks past K and a dead wave (live false) read zeros without
+// traffic.
+template <int LPR, int CPL, int NW, int FMT, int GM>
+__device__ __forceinline__ void issue_slot(Slot<FMT, GM, CPL, NW>& sl, const uint32_t* w0,
+                                           const void* s0, const uint32_t* w1, const void* s1,
+                                           int n, int r0, int chunks, bool sf16, bool live,
+                                           int t) {
   const int lane = t & 63, sub = lane % LPR, slot = lane / LPR;
   const int row_bytes = chunks * 16;
   const int rows = live && n > r0 ? n - r0 : 0;
   const int sb = sf16 ? 2 : 4;
-  const int sbytes = live ? (n * chunks * sb + 3) & ~3 : 0;
+  const int spr = row_scales<FMT, GM>(chunks);
+  const int sbytes = live ? (n * spr * sb + 3) & ~3 : 0;
 #pragma unroll
   for (int h = 0; h < NW; ++h) {
     const char* wb = (const char*)(h ? w1 : w0) + (long long)(live ? r0 : 0) * row_bytes;
@@ -364,30 +400,46 @@ __device__ __forceinline__ void issue_slot(Slot<CPL, NW>& sl, const uint32_t* w0
       const int off = ci < chunks ? slot * row_bytes + ci * 16 : kNoOff;
       sl.w[h][c] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, kStreamAux));
-      const int soff = ci < chunks ? ((r0 + slot) * chunks + ci) * sb : kNoOff;
-      sl.s[h][c] = __builtin_amdgcn_raw_buffer_load_b32(sr, soff & ~3, 0, 0);
+    }
+    if constexpr (FMT == kQ8) {
+      sl.s[h][0] = __builtin_amdgcn_raw_buffer_load_b32(sr, ((r0 + slot) * sb) & ~3, 0, 0);
+    } else {
+      constexpr int SPC = GM == kG16 ? 2 : 1;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int ci = sub + c * LPR;
+#pragma unroll
+        for (int g = 0; g < SPC; ++g) {
+          const int soff = ci < chunks ? ((r0 + slot) * spr + SPC * ci + g) * sb : kNoOff;
+          sl.s[h][SPC * c + g] = __builtin_amdgcn_raw_buffer_load_b32(sr, soff & ~3, 0, 0);
+        }
+      }
     }
   }
 }
 
 // Dot product of one row slot with the fp16 activation row in LDS (stored in
-// the nibble-pair order of q4_xpairs per 8 elements), in the streaming
-// kernel's order (Qmv::compute, Q4, one scale per 32 codes), reduced over the
-// slot's LPR lanes.  Every lane of the slot returns the row's sum.
-template <int LPR, int CPL>
-__device__ __forceinline__ float row_dot(const u32x4 (&w)[CPL], const uint32_t (&s)[CPL],
+// the nibble-pair order of q4_xpairs per 8 elements for Q4, plain for Q8), in
+// the streaming kernel's order for the format (Qmv::compute: Q4 group partial
+// sums scaled into the accumulator, one or two groups per 32-code chunk; Q8
+// the whole row, scaled once after the reduction), reduced over the slot's
+// LPR lanes.  Every lane of the slot returns the row's sum.
+template <int LPR, int CPL, int FMT, int GM>
+__device__ __forceinline__ float row_dot(const u32x4 (&w)[CPL],
+                                         const uint32_t (&s)[slot_scales<FMT, GM, CPL>()],
                                          const f16* xl, int chunks, int row, bool sf16, int t) {
   const int sub = (t & 63) % LPR;
   const int sb = sf16 ? 2 : 4;
+  constexpr int XW = FMT == kQ8 ? 8 : 16;  // activation dwords per chunk
   float acc = 0.0f;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int ci = sub + c * LPR;
-    uint32_t xr[16];
+    uint32_t xr[XW];
     if (ci < chunks) {
-      const u32x4* src = (const u32x4*)(xl + ci * 32);
+      const u32x4* src = (const u32x4*)(xl + ci * (2 * XW));
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
+      for (int v = 0; v < XW / 4; ++v) {
         const u32x4 t4 = src[v];
         xr[4 * v + 0] = t4[0];
         xr[4 * v + 1] = t4[1];
@@ -396,23 +448,41 @@ __device__ __forceinline__ float row_dot(const u32x4 (&w)[CPL], const uint32_t (
       }
     } else {
 #pragma unroll
-      for (int d = 0; d < 16; ++d) xr[d] = 0u;
+      for (int d = 0; d < XW; ++d) xr[d] = 0u;
     }
-    float part = 0.0f;
+    if constexpr (FMT == kQ8) {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      uint32_t q[4];
-      q4_pairs(w[c][d], q);
-      float tt = part;
-      tt = dot2(q[0], xr[4 * d + 0], tt);
-      tt = dot2(q[1], xr[4 * d + 1], tt);
-      tt = dot2(q[2], xr[4 * d + 2], tt);
-      tt = dot2(q[3], xr[4 * d + 3], tt);
-      part = tt;
+      for (int d = 0; d < 4; ++d) {
+        uint32_t lo, hi;
+        q8_pairs(w[c][d], lo, hi);
+        acc = dot2(hi, xr[2 * d + 1], dot2(lo, xr[2 * d], acc));
+      }
+    } else {
+      constexpr int SPC = GM == kG16 ? 2 : 1;
+      float part[SPC];
+#pragma unroll
+      for (int g = 0; g < SPC; ++g) part[g] = 0.0f;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        uint32_t q[4];
+        q4_pairs(w[c][d], q);
+        const int g = GM == kG16 ? (d >> 1) : 0;
+        float tt = part[g];
+        tt = dot2(q[0], xr[4 * d + 0], tt);
+        tt = dot2(q[1], xr[4 * d + 1], tt);
+        tt = dot2(q[2], xr[4 * d + 2], tt);
+        tt = dot2(q[3], xr[4 * d + 3], tt);
+        part[g] = tt;
+      }
+#pragma unroll
+      for (int g = 0; g < SPC; ++g)
+        acc = fmaf(part[g], scale_at(s[SPC * c + g], (row * SPC * chunks + SPC * ci + g) * sb, sf16),
+                   acc);
     }
-    acc = fmaf(part, scale_at(s[c], (row * chunks + ci) * sb, sf16), acc);
   }
-  return group_sum<LPR>(acc);
+  float v = group_sum<LPR>(acc);
+  if constexpr (FMT == kQ8) v *= scale_at(s[0], row * sb, sf16);
+  return v;
 }
 
 // Rows of one phase for this workgroup and compute wave: [row0 + wave * slots, +slots).
@@ -430,9 +500,15 @@ __device__ __forceinline__ WaveRows wave_rows(int per_wg, int slots, int total) 
 
 }  // namespace
 
-template <int GQ, int L1, int C1, int L2, int C2, int L3, int C3>
+template <int FMT, int GM, int GQ, int L1, int C1, int L2, int C2, int L3, int C3>
 __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) {
   constexpr int S1 = 64 / L1, S2 = 64 / L2, S3 = 64 / L3;  // row slots per wave
+  constexpr int kCE = FMT == kQ8 ? 16 : 32;                  // codes per 16-byte chunk
+  constexpr bool kPairs = FMT == kQ4;                        // activations in q4_xpairs order
+  // Q4 weights are prefetched one to three phases ahead; Q8 rows are twice the
+  // bytes, so each matrix is issued two phases before its use (at most three
+  // matrices in flight), which keeps the wave within the register budget of
+  // three waves per SIMD
   // inputs of the phases (written by the poll wave one phase earlier)
   __shared__ __align__(16) f16 s_xa[kStepMaxHidden];   // layer input, plain (P3 residual)
   __shared__ __align__(16) f16 s_xb[kStepMaxHidden];   // after attention, plain (P5 residual)
@@ -460,13 +536,12 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
 
   const int b = blockIdx.x;
   const int wave_u = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const bool poll = wave_u > kSW;
   const bool store = wave_u == kSW;
   const bool compute = wave_u < kCW;
   const int pw = wave_u - kSW - 1;  // poll wave index (when poll)
   const bool sf16 = p.sf16 != 0;
   const int hid = p.hidden, qw = p.qw, kvw = p.kvw, inter = p.inter;
-  const int ch1 = hid / 32, ch2 = qw / 32, ch3 = inter / 32;  // code chunks per row
+  const int ch1 = hid / kCE, ch2 = qw / kCE, ch3 = inter / kCE;  // code chunks per row
   const int nqkv = qw + 2 * kvw;
   int* err = p.err;
   bool broken = false;
@@ -507,10 +582,10 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
   };
 
   // compute-wave registers: prefetched weights and the split's K/V rows
-  Slot<C1, 1> wqkv;
-  Slot<C2, 1> wo;
-  Slot<C1, 2> wgu;
-  Slot<C3, 1> wd;
+  Slot<FMT, GM, C1, 1> wqkv;
+  Slot<FMT, GM, C2, 1> wo;
+  Slot<FMT, GM, C1, 2> wgu;
+  Slot<FMT, GM, C3, 1> wd;
   u32x4 kreg[2], vreg[2];  // thread t < 8 kAP: position ap0 + t / 8, dims 16 (t % 8) .. + 16
 
   auto issue_qkv = [&](int l, int t) {
@@ -586,12 +661,13 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       {
         const int t = opaque_tid(), lane = t & 63;
         issue_o(l, t);
-        issue_d(l, t);
+        if constexpr (FMT != kQ8) issue_d(l, t);
         if (w1.live) {
           const uint32_t* w; const void* s; int n, lr;
           qkv_mat(L, w1.r0, w, s, n, lr);
           const int row = lr + lane / L1;
-          const float v = 0.0f + row_dot<L1, C1>(wqkv.w[0], wqkv.s[0], s_xn, ch1, row, sf16, t);
+          const float v =
+              0.0f + row_dot<L1, C1, FMT, GM>(wqkv.w[0], wqkv.s[0], s_xn, ch1, row, sf16, t);
           if (lane % L1 == 0 && row < n)
             s_out[w1.r0 + lane / L1 - b * p.rows_qkv] = tag_f16((f16)v, tg);
         }
@@ -710,10 +786,14 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       // ---------------- P3: o_proj + residual
       {
         const int t = opaque_tid(), lane = t & 63;
-        if (l + 1 < nl) issue_qkv(l + 1, t);
+        if constexpr (FMT == kQ8) {
+          issue_d(l, t);
+        } else {
+          if (l + 1 < nl) issue_qkv(l + 1, t);
+        }
         if (w3.live) {
           const int row = w3.r0 + lane / L2;
-          float v = 0.0f + row_dot<L2, C2>(wo.w[0], wo.s[0], s_at, ch2, row, sf16, t);
+          float v = 0.0f + row_dot<L2, C2, FMT, GM>(wo.w[0], wo.s[0], s_at, ch2, row, sf16, t);
           if (row < hid) v += (float)s_xa[row];
           if (lane % L2 == 0 && row < hid) s_out[row - b * p.rows_hid] = tag_f16((f16)v, tg + 3);
         }
@@ -723,11 +803,16 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       // ---------------- P4: gate/up + SwiGLU-out
       {
         const int t = opaque_tid(), lane = t & 63;
+        if constexpr (FMT == kQ8) {
+          if (l + 1 < nl) issue_qkv(l + 1, t);
+        }
         if (l + 1 < nl) issue_kv(l + 1, t, true, false);
         if (w4.live) {
           const int row = w4.r0 + lane / L1;
-          const float g = 0.0f + row_dot<L1, C1>(wgu.w[0], wgu.s[0], s_xn, ch1, row, sf16, t);
-          const float u = 0.0f + row_dot<L1, C1>(wgu.w[1], wgu.s[1], s_xn, ch1, row, sf16, t);
+          const float g =
+              0.0f + row_dot<L1, C1, FMT, GM>(wgu.w[0], wgu.s[0], s_xn, ch1, row, sf16, t);
+          const float u =
+              0.0f + row_dot<L1, C1, FMT, GM>(wgu.w[1], wgu.s[1], s_xn, ch1, row, sf16, t);
           const float v = silu(g) * u;
           if (lane % L1 == 0 && row < inter)
             s_out[row - b * p.rows_inter] = tag_f16((f16)v, tg + 4);
@@ -741,7 +826,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         if (l + 1 < nl) issue_kv(l + 1, t, false, true);
         if (w5.live) {
           const int row = w5.r0 + lane / L3;
-          float v = 0.0f + row_dot<L3, C3>(wd.w[0], wd.s[0], s_h, ch3, row, sf16, t);
+          float v = 0.0f + row_dot<L3, C3, FMT, GM>(wd.w[0], wd.s[0], s_h, ch3, row, sf16, t);
           if (row < hid) v += (float)s_xb[row];
           if (lane % L3 == 0 && row < hid) s_out[row - b * p.rows_hid] = tag_f16((f16)v, tg + 5);
         }
@@ -829,7 +914,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       for (int d = lane; d < hid; d += 64) s_xa[d] = (f16)((float)((int)row[d] - 128) * sc);
       pw_gamma_store(g, s_ga, hid, lane);
       __asm__ volatile("" ::: "memory");
-      pw_rms(s_xa, s_ga, s_xn, hid, p.eps, lane);
+      pw_rms<kPairs>(s_xa, s_ga, s_xn, hid, p.eps, lane);
     }
     __syncthreads();
     for (int l = 0; l < nl; ++l) {
@@ -935,13 +1020,13 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         cw_signal(&s_merge, lane);
       }
       // the attention output of the whole grid (the merges of every workgroup)
-      pw_vec_pairs<kStepMaxQ / 256 / kPW>(p.attn_t, qw, tg + 2, s_at, lane, pw, err, broken);
+      pw_vec_pairs<kStepMaxQ / 256 / kPW, kPairs>(p.attn_t, qw, tg + 2, s_at, lane, pw, err, broken);
       __syncthreads();
       // during P3: x after attention and its RMSNorm-in; the next layer's gamma
       if (pw == 0) {
         pw_vec_plain<kStepMaxHidden / 256>(p.xb_t, hid, tg + 3, s_xb, lane, err, broken);
         __asm__ volatile("" ::: "memory");
-        pw_rms(s_xb, s_gm, s_xn, hid, p.eps, lane);
+        pw_rms<kPairs>(s_xb, s_gm, s_xn, hid, p.eps, lane);
       } else if (l + 1 < nl) {
         f32x4 ga[4];
         pw_gamma_issue(lds_ptr(&s_layers[l + 1].g_attn), hid, ga, lane);
@@ -949,33 +1034,55 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       }
       __syncthreads();
       // during P4: the SwiGLU output
-      pw_vec_pairs<kStepMaxInter / 256 / kPW>(p.h_t, inter, tg + 4, s_h, lane, pw, err, broken);
+      pw_vec_pairs<kStepMaxInter / 256 / kPW, kPairs>(p.h_t, inter, tg + 4, s_h, lane, pw, err,
+                                                      broken);
       __syncthreads();
       // during P5: the next layer's input and its RMSNorm-in
       if (pw == 0 && l + 1 < nl) {
         pw_vec_plain<kStepMaxHidden / 256>(p.xa_t, hid, tg + 5, s_xa, lane, err, broken);
         __asm__ volatile("" ::: "memory");
-        pw_rms(s_xa, s_ga, s_xn, hid, p.eps, lane);
+        pw_rms<kPairs>(s_xa, s_ga, s_xn, hid, p.eps, lane);
       }
       __syncthreads();
     }
   }
 }
 
-bool decode_layers_supported(int gq, int ch1, int ch2, int ch3) {
-  return gq == 4 && ch1 > 16 && ch1 <= 32 && ch2 > 32 && ch2 <= 64 && ch3 > 64 && ch3 <= 128;
+// The instantiations: Q4 (groups of 32 or 16) at the streaming kernel's
+// shapes for rows of 17..32 / 33..64 / 65..128 chunks (16 x 2, 32 x 2, 64 x 2
+// lanes x chunks), Q8 at those for 33..64 / 65..128 / 129..256 chunks (16 x 4,
+// 32 x 4, 64 x 4), four q heads per kv head.
+#define AEXQ_STEP_Q4(GM) decode_layers_kernel<kQ4, GM, 4, 16, 2, 32, 2, 64, 2>
+#define AEXQ_STEP_Q8 decode_layers_kernel<kQ8, kGRow, 4, 16, 4, 32, 4, 64, 4>
+
+bool decode_layers_supported(int fmt, int gmode, int gq, int ch1, int ch2, int ch3) {
+  if (gq != 4) return false;
+  if (fmt == kQ4 && (gmode == kG32 || gmode == kG16))
+    return ch1 > 16 && ch1 <= 32 && ch2 > 32 && ch2 <= 64 && ch3 > 64 && ch3 <= 128;
+  if (fmt == kQ8 && gmode == kGRow)
+    return ch1 > 32 && ch1 <= 64 && ch2 > 64 && ch2 <= 128 && ch3 > 128 && ch3 <= 256;
+  return false;
 }
 
-hipError_t decode_layers_occupancy(int* per_cu) {
-  return hipOccupancyMaxActiveBlocksPerMultiprocessor(
-      per_cu, decode_layers_kernel<4, 16, 2, 32, 2, 64, 2>, kSt, 0);
+hipError_t decode_layers_occupancy(int fmt, int gmode, int* per_cu) {
+  if (fmt == kQ8)
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, AEXQ_STEP_Q8, kSt, 0);
+  if (gmode == kG16)
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, AEXQ_STEP_Q4(kG16), kSt, 0);
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, AEXQ_STEP_Q4(kG32), kSt, 0);
 }
 
 hipError_t decode_layers_launch(const StepParams& p, int grid, hipStream_t stream) {
-  if (!decode_layers_supported(p.hq / p.hkv, p.hidden / 32, p.qw / 32, p.inter / 32))
+  const int ce = p.fmt == kQ8 ? 16 : 32;
+  if (!decode_layers_supported(p.fmt, p.gmode, p.hq / p.hkv, p.hidden / ce, p.qw / ce,
+                               p.inter / ce))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL((decode_layers_kernel<4, 16, 2, 32, 2, 64, 2>), dim3(grid), dim3(kSt), 0,
-                     stream, p);
+  if (p.fmt == kQ8)
+    hipLaunchKernelGGL((AEXQ_STEP_Q8), dim3(grid), dim3(kSt), 0, stream, p);
+  else if (p.gmode == kG16)
+    hipLaunchKernelGGL((AEXQ_STEP_Q4(kG16)), dim3(grid), dim3(kSt), 0, stream, p);
+  else
+    hipLaunchKernelGGL((AEXQ_STEP_Q4(kG32)), dim3(grid), dim3(kSt), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -52,6 +52,29 @@ class ModelConfig:
     group: int = 32          # Q4 scale group
     seed: int = synth.SEED_BASE + 3
     scales_f32: bool = False  # layer scales fp32 (the reference archives' dtype) instead of fp16
+    layer_bits: int = 4       # 8: Q8 layer weights with one scale per row (Q8A:94-114)
+    nibble_code: int = synth.NIBBLE_OFFSET8  # Q4 code; the reference's archives: NIBBLE_TWOS
+
+    @classmethod
+    def reference_q4(cls, **kw) -> "ModelConfig":
+        """The reference's shipping Q4 layers: two's-complement nibbles, one fp32
+        scale per 16 codes (Qwen35MobileQ4AssetBuilder.cs:22-25, Q8A:116-139)."""
+        return cls(group=16, scales_f32=True, nibble_code=synth.NIBBLE_TWOS, **kw)
+
+    @classmethod
+    def reference_q8(cls, **kw) -> "ModelConfig":
+        """Q8 layers with one fp32 scale per output row (Q8A:94-114, GL:65-67)."""
+        return cls(layer_bits=8, scales_f32=True, **kw)
+
+    @property
+    def format_name(self) -> str:
+        if self.layer_bits == 8:
+            return "q8_row_" + ("f32" if self.scales_f32 else "f16")
+        return f"q4_g{self.group}_" + ("f32" if self.scales_f32 else "f16")
+
+    def weight_block(self, k: int) -> int:
+        """Scale block of a layer weight with reduction length k."""
+        return k if self.layer_bits == 8 else self.group
 
     @property
     def q_width(self):
@@ -72,7 +95,10 @@ class ModelConfig:
         positions: every weight code and scale once, each cached K and V row
         once, and the activations each launch reads and writes."""
         sb = 4 if self.scales_f32 else 2
-        weights = sum(n * k // 2 + n * (k // self.group) * sb for _, n, k in self.linears())
+        if self.layer_bits == 8:
+            weights = sum(n * k + n * sb for _, n, k in self.linears())
+        else:
+            weights = sum(n * k // 2 + n * (k // self.group) * sb for _, n, k in self.linears())
         kv_read = 2 * self.heads_kv * length * self.head_dim * 2
         h, qw, kw, i = self.hidden, self.q_width, self.kv_width, self.intermediate
         act = 2 * (h + qw + 2 * kw          # q/k/v: x in, q/k/v out
@@ -90,10 +116,13 @@ class ModelConfig:
 def host_weights(cfg: ModelConfig, layer: int):
     """Seeded numpy weights of one layer: {name: (words, scales, codes)} and the two norms."""
     out = {}
+    sdt = np.float32 if cfg.scales_f32 else np.float16
     for i, (name, n, k) in enumerate(cfg.linears()):
-        out[name] = synth.q4_weights(n, k, cfg.seed + 97 * layer + i, group=cfg.group,
-                                     code=synth.NIBBLE_OFFSET8,
-                                     scale_dtype=np.float32 if cfg.scales_f32 else np.float16)
+        if cfg.layer_bits == 8:
+            out[name] = synth.q8_weights(n, k, cfg.seed + 97 * layer + i, scale_dtype=sdt)
+        else:
+            out[name] = synth.q4_weights(n, k, cfg.seed + 97 * layer + i, group=cfg.group,
+                                         code=cfg.nibble_code, scale_dtype=sdt)
     g_attn = synth.rms_gamma(cfg.hidden, cfg.seed + 97 * layer + 50)
     g_mlp = synth.rms_gamma(cfg.hidden, cfg.seed + 97 * layer + 51)
     return out, g_attn, g_mlp
@@ -132,24 +161,119 @@ def host_kv_cache(cfg: ModelConfig, layer: int):
     return (g.standard_normal(shape).astype(np.float16), g.standard_normal(shape).astype(np.float16))
 
 
+# ----------------------------------------------------------------- model assets
+
+# Logical files of a mobile asset set (Qwen35MobileQ4AssetBuilder.cs:29, 189):
+# the decoder layers' archive and the tied token embedding, which stays Q8 with
+# one scale per row whatever the layers' format (B4:21-25).
+DECODER_FILE = "qwen3.5_decoder.ncnn.bin"
+EMBED_FILE = "qwen3.5_embed_token.ncnn.bin"
+
+
+@dataclass
+class ModelWeights:
+    """Device weights of the model: per layer the seven linears and the two
+    RMSNorm gammas (host float32), the tied Q8 embedding / LM head and the
+    final norm's gamma."""
+    layers: list          # [{"w": {name: QuantWeight}, "g_attn": np, "g_mlp": np}]
+    lm: object            # QuantWeight, Q8 per row [vocab][hidden]
+    g_final: np.ndarray
+
+
+def archive_records(cfg: ModelConfig) -> list:
+    """The decoder archive's record order for this model: per layer the
+    attention RMSNorm weights (a raw fp32 record), q/k/v/o, the MLP RMSNorm
+    weights, gate/up/down, then the final norm -- the order in which the
+    graph's layers read their weights (GL:15-162 per Gemm, RMS:24-46 per
+    RMSNorm).  Entries: ("norm", count) or (name, n, k)."""
+    out = []
+    lin = cfg.linears()
+    for _ in range(cfg.layers):
+        out.append(("norm", cfg.hidden))
+        out.extend(lin[:4])
+        out.append(("norm", cfg.hidden))
+        out.extend(lin[4:])
+    out.append(("norm", cfg.hidden))
+    return out
+
+
+def load_assets(ctx: aexq.Context, model_directory: str, cfg: ModelConfig,
+                verify_hashes: bool = True) -> ModelWeights:
+    """A mobile asset set (MAS:50-138: the Q4 manifest preferred over the Q8
+    one) into device weights: the decoder archive walked record by record
+    (Gemm weights through aexq_weight_from_record, GL:60-141; RMSNorm weights
+    as raw fp32 records, Q8A:295-306) and the tied Q8 embedding, whose device
+    copy is also the LM head (EMB:95-120).  The layers' Gemm records are read
+    as cfg.layer_bits weights: Q4 records for a Q4 model, Q8 records with a
+    block of K for a Q8 one; any other record is quantized per row."""
+    from . import assets
+    aset = assets.MobileAssetSet.try_load(model_directory, verify_hashes=verify_hashes)
+    if aset is None:
+        raise assets.InvalidDataError("no mobile asset manifest in " + model_directory)
+    for name in (DECODER_FILE, EMBED_FILE):
+        if not aset.contains(name):
+            raise assets.InvalidDataError(f"the asset set has no logical file {name}")
+    made = []
+    try:
+        with aset.open_read(EMBED_FILE) as s:
+            (lm,), _ = assets.load_archive_weights(ctx, s, [(cfg.vocab, cfg.hidden, 8)])
+        made.append(lm)
+        info = lm.info()
+        if info.block != cfg.hidden:
+            raise assets.InvalidDataError(
+                f"{EMBED_FILE}: the tied embedding has scale blocks of {info.block}, not one "
+                f"per row of {cfg.hidden}")
+        plan = archive_records(cfg)
+        layers, cur, norms = [], None, []
+        with aset.open_read(DECODER_FILE) as s:
+            header = assets.read_archive_header(s)
+            if header[2] != len(plan):
+                raise assets.InvalidDataError(
+                    f"{DECODER_FILE} holds {header[2]} records, the model reads {len(plan)}")
+            for item in plan:
+                if item[0] == "norm":
+                    norms.append(assets.read_float_record(s, item[1]))
+                    continue
+                name, n, k = item
+                if name == "q_proj":
+                    cur = {}
+                    layers.append(cur)
+                (w,) = assets.read_weight_records(ctx, s, [(n, k, cfg.layer_bits)])
+                made.append(w)
+                cur[name] = w
+        out = [{"w": w, "g_attn": norms[2 * l], "g_mlp": norms[2 * l + 1]}
+               for l, w in enumerate(layers)]
+        return ModelWeights(out, lm, norms[-1])
+    except BaseException:
+        for w in made:
+            w.release()
+        raise
+
+
 class DecodeSession:
-    """Device state of the synthetic model and one decode step (eager or graph)."""
+    """Device state of the model and one decode step (eager or graph)."""
 
     def __init__(self, ctx: aexq.Context, cfg: ModelConfig, device: str = "cuda",
-                 fused: bool = False, workgroups: int = 0):
+                 fused: bool = False, workgroups: int = 0, weights: ModelWeights = None):
         """fused: the layers run as one launch (aexq_decoder_run) instead of
-        five launches per layer."""
+        five launches per layer.  weights: the model's device weights (from
+        load_assets); None builds the seeded synthetic model of cfg."""
         self.ctx, self.cfg, self.device = ctx, cfg, device
         P4 = aexq.LAYOUT_PACK4_LINEAR
         c = cfg
         self.layers = []
         for l in range(c.layers):
-            ws, g_attn, g_mlp = host_weights(c, l)
-            dev_w = {}
-            for name, n, k in c.linears():
-                words, scales, _ = ws[name]
-                dev_w[name] = ctx.weight(aexq.QuantizedTensor(n * k, c.group, words, scales, bits=4,
-                                                              nibble_code=synth.NIBBLE_OFFSET8), n, k)
+            if weights is not None:
+                dev_w = weights.layers[l]["w"]
+                g_attn, g_mlp = weights.layers[l]["g_attn"], weights.layers[l]["g_mlp"]
+            else:
+                ws, g_attn, g_mlp = host_weights(c, l)
+                dev_w = {}
+                for name, n, k in c.linears():
+                    words, scales, _ = ws[name]
+                    dev_w[name] = ctx.weight(
+                        aexq.QuantizedTensor(n * k, c.weight_block(k), words, scales,
+                                             bits=c.layer_bits, nibble_code=c.nibble_code), n, k)
             kc, vc = host_kv_cache(c, l)
             self.layers.append({
                 "w": dev_w,
@@ -158,13 +282,18 @@ class DecodeSession:
                 "k_cache": torch.as_tensor(kc).to(device).reshape(-1),
                 "v_cache": torch.as_tensor(vc).to(device).reshape(-1),
             })
-        words, scales, _ = host_lm_head(c)
-        self.lm = ctx.weight(aexq.QuantizedTensor(c.vocab * c.hidden, c.hidden, words, scales, bits=8),
-                             c.vocab, c.hidden)
+        if weights is not None:
+            self.lm = weights.lm
+            g_final = weights.g_final
+        else:
+            words, scales, _ = host_lm_head(c)
+            self.lm = ctx.weight(aexq.QuantizedTensor(c.vocab * c.hidden, c.hidden, words, scales,
+                                                      bits=8), c.vocab, c.hidden)
+            g_final = host_final_gamma(c)
         # the embedding reads the LM head's device copy through a non-owning
         # alias (Qwen35SharedTokenEmbeddingWeights, EMB:95-120; GL:91-111)
         self.embed = self.lm.alias()
-        self.g_final = torch.as_tensor(host_final_gamma(c)).to(device)
+        self.g_final = torch.as_tensor(g_final).to(device)
         f16 = torch.float16
         z = lambda n, dt=f16: torch.zeros(n, dtype=dt, device=device)
         self.token = torch.zeros(1, dtype=torch.int32, device=device)

@@ -41,6 +41,7 @@ namespace Aexis.Hip
         public const uint EpiRmsNormIn = 0x1u;
         public const uint EpiSwiGluOut = 0x2u;
         public const uint EpiResidualAdd = 0x4u;
+        public const uint EpiArgmaxF16 = 0x8u;    // LM head: argmax over fp16-rounded logits (ARGBHalf)
 
         // the texture size limit the storage rules are written against (GS:10852)
         public const int TileWidthLimit = 8192;

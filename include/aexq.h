@@ -77,6 +77,12 @@ typedef int aexq_status;
                                     * M <= 8, of 64 above; a shape no kernel takes returns
                                     * AEXQ_ERR_UNSUPPORTED (no generic fallback) */
 #define AEXQ_EPI_RESIDUAL_ADD 0x4u /* y += residual (BinaryOp Add after o_proj/down) */
+#define AEXQ_EPI_ARGMAX_F16 0x8u   /* LM head only: the argmax (and the top-2 gap) compares the
+                                    * logits rounded to fp16, as the reference's ARGBHalf logits
+                                    * texture holds them (GL:383-396) when ArgMaxPack4LinearMat
+                                    * reads it (MM:645-686, DEC:792); fp32 logits written
+                                    * alongside keep the unrounded values.  Implied by an fp16
+                                    * logits tensor. */
 
 typedef struct aexq_ctx aexq_ctx;
 typedef struct aexq_weight aexq_weight;
@@ -226,17 +232,20 @@ aexq_status aexq_linear_group(aexq_ctx* ctx, int count, const aexq_weight* const
                               const aexq_linear_args* args);
 
 /* LM head with fused greedy argmax (DEC:734-809 -> tiled Gemm MM:2271-2302
- * -> ArgMaxPack4LinearMat MM:645-686).  logits (nullable) are fp32 in the
- * given layout; argmax is a device int32[M] using the first-maximum rule;
- * top2_gap (nullable) is a device float[M] = best - second best logit. */
+ * -> ArgMaxPack4LinearMat MM:645-686).  logits (nullable) are fp32 or fp16 in
+ * the given layout (fp16 logits: the argmax compares those fp16 values, as
+ * over the reference's ARGBHalf texture); argmax is a device int32[M] using
+ * the first-maximum rule; top2_gap (nullable) is a device float[M] = best -
+ * second best logit. */
 aexq_status aexq_lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
                                const aexq_tensor* logits, int32_t* argmax, float* top2_gap);
 
 /* aexq_lmhead_argmax with the final RMSNorm of the decoder (the norm layer the
  * reference's graph runs before the LM head, CC:4531-4557) fused as the
- * RMSNorm-in epilogue: args->flags may hold AEXQ_EPI_RMSNORM_IN only (with
- * rms_gamma / rms_eps) and alpha applies as for aexq_linear; the LM head takes
- * no C term (args->c must be NULL).  args NULL is aexq_lmhead_argmax. */
+ * RMSNorm-in epilogue: args->flags may hold AEXQ_EPI_RMSNORM_IN (with
+ * rms_gamma / rms_eps) and AEXQ_EPI_ARGMAX_F16 only, and alpha applies as for
+ * aexq_linear; the LM head takes no C term (args->c must be NULL).  args NULL
+ * is aexq_lmhead_argmax. */
 aexq_status aexq_lmhead_argmax_ex(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
                                   const aexq_tensor* logits, const aexq_linear_args* args,
                                   int32_t* argmax, float* top2_gap);
@@ -255,7 +264,8 @@ aexq_status aexq_lmhead_argmax_ex(aexq_ctx* ctx, const aexq_weight* w, const aex
 aexq_status aexq_lmhead_argmax_noalloc(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
                                        int32_t* argmax, float* top2_gap);
 
-/* Row-wise argmax of an existing logits tensor (OPS:9982-10004, MM:645-686). */
+/* Row-wise argmax of an existing fp32 or fp16 logits tensor (OPS:9982-10004,
+ * MM:645-686). */
 aexq_status aexq_argmax(aexq_ctx* ctx, const aexq_tensor* logits, int32_t* argmax,
                         float* top2_gap);
 

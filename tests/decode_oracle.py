@@ -27,15 +27,37 @@ class OracleDecoder:
         for l in range(cfg.layers):
             ws, g_attn, g_mlp = decoder.host_weights(cfg, l)
             W = {}
+            sd = orc.SCALE_F32 if cfg.scales_f32 else orc.SCALE_F16
             for name, n, k in cfg.linears():
                 words, scales, _ = ws[name]
-                W[name] = orc.dequant_q4(words, scales, n, k, cfg.group, synth.NIBBLE_OFFSET8,
-                                         orc.SCALE_F32 if cfg.scales_f32 else orc.SCALE_F16)
+                if getattr(cfg, "layer_bits", 4) == 8:
+                    W[name] = orc.dequant_q8(words, scales, n, k, scale_dtype=sd)
+                else:
+                    W[name] = orc.dequant_q4(words, scales, n, k, cfg.group,
+                                             getattr(cfg, "nibble_code", synth.NIBBLE_OFFSET8), sd)
             self.layers.append((W, g_attn, g_mlp))
         self.caches = []
         for l in range(cfg.layers):
             kc, vc = decoder.host_kv_cache(cfg, l)
             self.caches.append((kc.astype(np.float32), vc.astype(np.float32)))
+
+    @classmethod
+    def from_weights(cls, orc, cfg, model):
+        """The same composition over given dequantised weights (the oracle's
+        reading of an archive): model = {"layers": [(W, g_attn, g_mlp)],
+        "lm": [vocab][hidden], "g_final": [hidden]}; the caches are the seeded
+        synthetic ones DecodeSession fills."""
+        from aiimage_amd import decoder
+        self = cls.__new__(cls)
+        self.orc, self.cfg = orc, cfg
+        self.lm = np.asarray(model["lm"], np.float32)
+        self.g_final = np.asarray(model["g_final"], np.float32)
+        self.layers = list(model["layers"])
+        self.caches = []
+        for l in range(cfg.layers):
+            kc, vc = decoder.host_kv_cache(cfg, l)
+            self.caches.append((kc.astype(np.float32), vc.astype(np.float32)))
+        return self
 
     def step(self, tok: int, pos: int):
         """(final hidden state, logits) of one step; appends this position's

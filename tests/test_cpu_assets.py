@@ -143,3 +143,54 @@ def test_sharded_file_random_slices(tmp_path):
         s.seek(90)
         with pytest.raises(assets.InvalidDataError):
             s.read_exact(8)
+
+
+def test_load_assets_needs_both_logical_files(tmp_path, orc):
+    """decoder.load_assets refuses an asset set without the decoder archive or
+    the tied embedding before touching a device."""
+    import hashlib
+    import json
+    import os
+
+    from aiimage_amd import assets, decoder
+    blob = orc.archive_header(8, 1024, 0, 0)
+    rel = "weights/e.part000"
+    os.makedirs(tmp_path / "weights")
+    (tmp_path / rel).write_bytes(blob)
+    doc = {"schema": assets.Q4_MANIFEST_SCHEMA, "weight_only": True,
+           "logical_files": {decoder.EMBED_FILE: {"stored_bytes": len(blob), "parts": [
+               {"file": rel, "bytes": len(blob), "sha256": hashlib.sha256(blob).hexdigest()}]}}}
+    (tmp_path / assets.Q4_MANIFEST_FILE).write_text(json.dumps(doc))
+    with pytest.raises(assets.InvalidDataError, match=decoder.DECODER_FILE):
+        decoder.load_assets(None, str(tmp_path), decoder.ModelConfig(layers=1))
+    with pytest.raises(assets.InvalidDataError, match="no mobile asset manifest"):
+        decoder.load_assets(None, str(tmp_path / "weights"), decoder.ModelConfig(layers=1))
+
+
+def test_read_float_record_rules(orc):
+    """Raw fp32 records read back exactly; a quantized record, a wrong count, a
+    bad magic and a short payload are refused (Q8A:295-306, 445-463)."""
+    import io
+    import struct
+
+    import numpy as np
+
+    from aiimage_amd import assets
+    v = np.array([1.5, -2.25, 3e-8, 65504.0, -0.0], np.float32)
+    rec = orc.record_write_raw_f32(v)
+    got = assets.read_float_record(io.BytesIO(rec), v.size)
+    assert np.array_equal(got.view(np.uint32), v.view(np.uint32))
+    with pytest.raises(assets.InvalidDataError, match="element count"):
+        assets.read_float_record(io.BytesIO(rec), v.size + 1)
+    with pytest.raises(assets.InvalidDataError, match="raw FP32"):
+        assets.read_float_record(io.BytesIO(orc.record_write_q8(np.ones(8, np.float32), 8)), 8)
+    bad = bytearray(rec)
+    bad[0] ^= 1
+    with pytest.raises(assets.InvalidDataError, match="magic"):
+        assets.read_float_record(io.BytesIO(bytes(bad)), v.size)
+    with pytest.raises(assets.InvalidDataError):
+        assets.read_float_record(io.BytesIO(rec[:-1]), v.size)
+    bad = bytearray(rec)
+    struct.pack_into("<i", bad, 16, 4 * v.size + 4)
+    with pytest.raises(assets.InvalidDataError, match="size mismatch"):
+        assets.read_float_record(io.BytesIO(bytes(bad)), v.size)

@@ -12,6 +12,10 @@ AIImageApplicationExample/Runtime/Scripts/Qwen35DecoderSession.cs).
   * Graph replays equal to the eager fused step bit for bit; an 8-token
     Generate by graph replay equal to eager fused steps and to the oracle.
   * Config 3 at full size (24 layers, 2048 cached positions).
+  * The reference's own layer formats (Q4 with two's-complement nibbles and
+    an fp32 scale per 16 codes; Q8 with a scale per row; fp16 scale variants)
+    against the oracle and the per-operator step, and through a captured
+    Generate loop.
   * No run gives up a bounded wait (the decoder's error word stays 0), and
     shapes the kernel does not take are refused at creation.
 """
@@ -222,6 +226,73 @@ def test_fused_fp32_scales_and_grid(ctx, aexq, orc, workgroups):
         assert t_f == int(np.argmax(logits)) == t_p
 
 
+_FORMATS = {
+    # the reference's shipping Q4 archives: two's-complement nibbles, fp32 scale per 16
+    "q4_g16_f32": lambda **kw: _cfg().reference_q4(**kw),
+    "q4_g16_f16": lambda **kw: _cfg()(group=16, **kw),
+    # Q8 layers, one scale per output row
+    "q8_row_f32": lambda **kw: _cfg().reference_q8(**kw),
+    "q8_row_f16": lambda **kw: _cfg()(layer_bits=8, **kw),
+}
+
+
+def _cfg():
+    from aiimage_amd import decoder
+    return decoder.ModelConfig
+
+
+@pytest.mark.parametrize("fmt", sorted(_FORMATS))
+def test_fused_reference_formats(ctx, aexq, orc, fmt):
+    """The fused step on the reference's own layer formats: against the oracle
+    composition and the per-operator step (5e-3), layer 0's appended V row
+    equal to the per-operator step's bit for bit (the same per-format
+    arithmetic as aexq_linear), the greedy token unless a near-tie, at a
+    position past an attention split boundary."""
+    from aiimage_amd import decoder
+    from decode_oracle import OracleDecoder, top2_gap
+    cfg = _FORMATS[fmt](layers=2, capacity=192, vocab=8192)
+    assert cfg.format_name == fmt
+    sess = decoder.DecodeSession(ctx, cfg, fused=True)
+    _announce(f"fused step {fmt}: {sess.fused.info()}")
+    od = OracleDecoder(orc, cfg)
+    for tok, pos in ((4321, 150), (17, 151)):
+        x_p, t_p = _step(sess, tok, pos, fused=False)
+        v_p = _v_row(sess, 0, pos)
+        sess.layers[0]["v_cache"].view(cfg.heads_kv, cfg.capacity, cfg.head_dim)[:, pos] = 0
+        x_f, t_f = _step(sess, tok, pos)
+        assert sess.fused.error() == 0
+        assert torch.equal(_v_row(sess, 0, pos), v_p), (fmt, pos)
+        x_ref, logits = od.step(tok, pos)
+        assert normwise(x_f.cpu().numpy(), x_ref) <= 5e-3, fmt
+        assert normwise(x_f.cpu().numpy(), x_p.cpu().numpy()) <= 5e-3, fmt
+        if top2_gap(logits) >= ARGMAX_TIE:
+            assert t_f == int(np.argmax(logits)) == t_p, (fmt, pos)
+
+
+def test_fused_reference_q4_graph_generate(ctx, aexq, orc):
+    """The reference's Q4 format through the captured Generate loop: eight
+    tokens by graph replay equal to eager fused steps and to the oracle."""
+    from aiimage_amd import decoder
+    from decode_oracle import OracleDecoder, top2_gap
+    cfg = decoder.ModelConfig.reference_q4(layers=2, capacity=96, vocab=4096)
+    sess = decoder.DecodeSession(ctx, cfg, fused=True)
+    _announce("fused generate, reference Q4 format")
+    start, pos0, count = 99, 60, 8
+    eager = sess.generate(start, pos0, count)
+    g = sess.capture(advance=True)
+    for rep in range(2):
+        assert sess.generate(start, pos0, count, graph=g) == eager, rep
+    od = OracleDecoder(orc, cfg)
+    tok = start
+    for i in range(count):
+        _, logits = od.step(tok, pos0 + i)
+        if top2_gap(logits) < ARGMAX_TIE:
+            break
+        assert eager[i] == int(np.argmax(logits)), i
+        tok = eager[i]
+    del g
+
+
 def test_fused_rejects_shapes_it_does_not_take(ctx, aexq):
     _announce("fused step rejections")
     from aiimage_amd import decoder
@@ -238,9 +309,20 @@ def test_fused_rejects_shapes_it_does_not_take(ctx, aexq):
     bad = dict(layer, q_proj=L["w"]["k_proj"])          # wrong shape
     with pytest.raises(aexq.InvalidOperationError):
         ctx.decoder([bad], sess.embed, **args)
-    bad = dict(layer, o_proj=sess.lm)                   # a Q8 weight
+    bad = dict(layer, o_proj=sess.lm)                   # a Q8 weight among Q4 ones
     with pytest.raises((aexq.NotSupportedError, aexq.InvalidOperationError)):
         ctx.decoder([bad], sess.embed, **args)
+    # one layer in another format than layer 0's
+    cfg16 = decoder.ModelConfig.reference_q4(layers=1, capacity=64)
+    s16 = decoder.DecodeSession(ctx, cfg16)
+    L16 = s16.layers[0]
+    mixed = dict(L16["w"], attn_norm=L16["g_attn"], mlp_norm=L16["g_mlp"],
+                 k_cache=L16["k_cache"], v_cache=L16["v_cache"])
+    with pytest.raises(aexq.NotSupportedError, match="one unstacked format"):
+        ctx.decoder([layer, mixed], sess.embed, **args)
+    d = ctx.decoder([mixed, mixed], sess.embed, **args)  # all group 16: accepted
+    d.close()
+    del s16
     with pytest.raises(aexq.NotSupportedError):          # head_dim other than 128
         ctx.decoder([layer], sess.embed, **dict(args, head_dim=64))
     with pytest.raises(aexq.NotSupportedError):          # cache beyond the split budget
