@@ -37,6 +37,7 @@ EPI_RMSNORM_IN = 0x1
 EPI_SWIGLU_OUT = 0x2
 EPI_RESIDUAL_ADD = 0x4
 EPI_ARGMAX_F16 = 0x8
+EPI_EXACT_DEQUANT = 0x10
 
 
 class AexqError(RuntimeError):

@@ -236,8 +236,9 @@ class Context:
                beta: float = 1.0, c: Optional[torch.Tensor] = None, broadcast_c: int = -1,
                rms_gamma: Optional[torch.Tensor] = None, rms_eps: float = 1e-3,
                rmsnorm: bool = False, up: Optional["QuantWeight"] = None,
-               residual: Optional[_abi.Tensor] = None):
-        args = make_args(alpha, beta, c, broadcast_c, rms_gamma, rms_eps, rmsnorm, up, residual)
+               residual: Optional[_abi.Tensor] = None, exact: bool = False):
+        args = make_args(alpha, beta, c, broadcast_c, rms_gamma, rms_eps, rmsnorm, up, residual,
+                         exact)
         check(self._lib.aexq_linear(self.handle, w.handle, ctypes.byref(x), ctypes.byref(y),
                                     ctypes.byref(args)), "aexq_linear")
 
@@ -394,7 +395,9 @@ def archive_header(buf: bytes) -> tuple:
 def make_args(alpha: float = 1.0, beta: float = 1.0, c: Optional[torch.Tensor] = None,
               broadcast_c: int = -1, rms_gamma: Optional[torch.Tensor] = None,
               rms_eps: float = 1e-3, rmsnorm: bool = False, up: Optional["QuantWeight"] = None,
-              residual: Optional[_abi.Tensor] = None) -> _abi.LinearArgs:
+              residual: Optional[_abi.Tensor] = None, exact: bool = False) -> _abi.LinearArgs:
+    """aexq_linear_args; exact=True keeps Q4 dequantisation exact in the tiled
+    GEMM (AEXQ_EPI_EXACT_DEQUANT) instead of fp16 weight tiles."""
     a = _abi.LinearArgs()
     a.alpha = alpha
     a.beta = beta
@@ -412,6 +415,8 @@ def make_args(alpha: float = 1.0, beta: float = 1.0, c: Optional[torch.Tensor] =
         flags |= EPI_SWIGLU_OUT
     if residual is not None:
         flags |= EPI_RESIDUAL_ADD
+    if exact:
+        flags |= _abi.EPI_EXACT_DEQUANT
     a.flags = flags
     a._keep = (c, rms_gamma, up, residual)
     return a

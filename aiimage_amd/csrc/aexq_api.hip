@@ -99,6 +99,9 @@ struct aexq_weight {
   long long code_stride = 0;   // bytes between copies
   long long scale_stride = 0;  // bytes between copies
   bool owns = true;
+  // Q4: every scale's fp16(q * s) stays finite (8 |s| <= 65504), so the tiled
+  // GEMM may dequantise weight tiles to fp16 (set once the scales are on the device)
+  bool fp16_dequant_ok = false;
 };
 
 static long long round_up(long long v, long long a) { return (v + a - 1) / a * a; }
@@ -257,6 +260,27 @@ static aexq_status alloc_weight(aexq_ctx* ctx, const char* op, int bits, int sca
   return AEXQ_OK;
 }
 
+// Q4 weights: whether fp16(q * s) stays finite for every code |q| <= 8, from
+// the largest scale magnitude (a device reduction over the scales, once at
+// upload).  A NaN or infinite scale propagates the same in both GEMM forms.
+static aexq_status check_fp16_dequant(aexq_weight* w, const char* op) {
+  if (w->bits != 4) return AEXQ_OK;
+  unsigned* dev = nullptr;
+  unsigned host = 0;
+  hipError_t e = hipMalloc((void**)&dev, sizeof(unsigned));
+  if (e == hipSuccess) e = hipMemset(dev, 0, sizeof(unsigned));
+  if (e == hipSuccess)
+    e = scale_absmax_launch(w->scales, w->scale_count, w->scale_dtype == AEXQ_DTYPE_F16, dev,
+                            nullptr);
+  if (e == hipSuccess) e = hipMemcpy(&host, dev, sizeof(unsigned), hipMemcpyDeviceToHost);
+  (void)hipFree(dev);
+  if (e != hipSuccess) return hip_fail(e, op, "scale range check");
+  float mx;
+  memcpy(&mx, &host, sizeof(float));
+  w->fp16_dequant_ok = !(mx > 65504.0f / 8.0f);
+  return AEXQ_OK;
+}
+
 static void free_weight(aexq_weight* w) {
   (void)hipFree(w->codes);
   (void)hipFree(w->scales);
@@ -291,6 +315,11 @@ static aexq_status upload_weight(aexq_ctx* ctx, const char* op, int bits, const 
   if (e != hipSuccess) {
     free_weight(w);
     return hip_fail(e, op, "weight upload");
+  }
+  st = check_fp16_dequant(w, op);
+  if (st) {
+    free_weight(w);
+    return st;
   }
   *out = w;
   return AEXQ_OK;
@@ -554,6 +583,11 @@ extern "C" aexq_status aexq_weight_from_record(aexq_ctx* ctx, int bits, const vo
   if (e != hipSuccess) {
     free_weight(w);
     return hip_fail(e, op, "record repack");
+  }
+  st = check_fp16_dequant(w, op);
+  if (st) {
+    free_weight(w);
+    return st;
   }
   *out = w;
   return AEXQ_OK;
@@ -881,7 +915,7 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   def.rms_eps = 0.001f;
   const aexq_linear_args& a = args ? *args : def;
   const unsigned known = AEXQ_EPI_RMSNORM_IN | AEXQ_EPI_SWIGLU_OUT | AEXQ_EPI_RESIDUAL_ADD |
-                         (argmax ? AEXQ_EPI_ARGMAX_F16 : 0u);
+                         AEXQ_EPI_EXACT_DEQUANT | (argmax ? AEXQ_EPI_ARGMAX_F16 : 0u);
   if (a.flags & ~known)
     return fail(AEXQ_ERR_INVALID_ARGUMENT, op, "flags=0x%x%s", a.flags,
                 (a.flags & AEXQ_EPI_ARGMAX_F16) && !argmax ? " (ARGMAX_F16 is for the LM head)" : "");
@@ -1033,16 +1067,21 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
   const bool gemm_shape_ok = K % 64 == 0 && (fmt == kQ8 || w0->block % 32 == 0 || g16) &&
                              (rms_in || x_ok) && size_ok && !argmax &&
                              getenv("AEXQ_QGEMM_OFF") == nullptr;
+  // Q4 weight tiles dequantised to fp16 in the tiled GEMM unless the call asks
+  // for the exact form or a weight's scales could overflow fp16 there
+  bool fd = fmt == kQ4 && !(a.flags & AEXQ_EPI_EXACT_DEQUANT);
+  for (int i = 0; i < count && fd; ++i) fd = ws[i]->fp16_dequant_ok;
+  if (fd && swiglu) fd = a.up->fp16_dequant_ok;
   auto try_gemm = [&]() {
     const bool sf16 = w0->scale_dtype == AEXQ_DTYPE_F16;
     // the LDS-direct kernel: Q8 and Q4 groups of 16 or 32; larger Q4 groups
     // (multiples of 32) the register-staged one, 64-row tiles
-    QgemmConfig gc{fmt, 64, swiglu, sf16, false, false};
+    QgemmConfig gc{fmt, 64, swiglu, sf16, false, false, false};
     if (fmt == kQ8 || w0->block == 16 || w0->block == 32) {
       int bm = M <= 64 ? 64 : 128;
       const char* benv = getenv("AEXQ_QGEMM_BM");  // tuning override: 64 or 128
       if (benv && (atoi(benv) == 64 || atoi(benv) == 128)) bm = atoi(benv);
-      gc = QgemmConfig{fmt, bm, swiglu, sf16, g16, true};
+      gc = QgemmConfig{fmt, bm, swiglu, sf16, g16, true, fd};
     }
     plan->gentry = qgemm_find(gc);
     if (plan->gentry) {
@@ -1400,11 +1439,11 @@ extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, cons
       snprintf(diag, diag_len, "%s", g_last_error.c_str());
     else if (plan.kind == kPlanGemm)
       snprintf(diag, diag_len,
-               "kernel=qgemm bits=%d bm=%d swiglu=%d direct=%d rms_prepass=%d tiles=%d grid=%d "
-               "splitk=%d",
+               "kernel=qgemm bits=%d bm=%d swiglu=%d direct=%d fp16_dequant=%d rms_prepass=%d "
+               "tiles=%d grid=%d splitk=%d",
                w->bits, plan.gentry->cfg.bm, (int)plan.gentry->cfg.pair,
-               (int)plan.gentry->cfg.direct, (int)plan.rms_prepass, plan.p.total_tiles, plan.grid,
-               plan.sk_chunks);
+               (int)plan.gentry->cfg.direct, (int)plan.gentry->cfg.fd, (int)plan.rms_prepass,
+               plan.p.total_tiles, plan.grid, plan.sk_chunks);
     else if (plan.kind == kPlanMfma)
       snprintf(diag, diag_len, "kernel=qmm bits=%d mt=%d nt=%d swiglu=%d wide=%d rms_prepass=%d "
                "tiles=%d grid=%d mblock=%d splitk=%d",

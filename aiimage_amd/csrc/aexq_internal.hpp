@@ -162,6 +162,7 @@ struct QgemmConfig {
   bool pair, sf16;
   bool g16;    // Q4 with one scale per 16 codes
   bool direct; // LDS-direct pipeline (Q8; Q4 split scales in groups of 16 or 32)
+  bool fd;     // Q4 weight tiles dequantised to fp16 (fp16(q * s)) for the MFMA
 };
 typedef void (*QgemmFn)(const QmvParams, int);
 struct QgemmEntry {
@@ -191,6 +192,10 @@ enum : int { kLogitsF32 = 0, kLogitsF16 = 1, kLogitsF32AsF16 = 2 };
 hipError_t logits_argmax_launch(const void* logits, int mode, int m, int n, long long rstride,
                                 float* pv, int* pi, float* ps, int parts, hipStream_t stream);
 int logits_argmax_cols_per_wg();
+// The largest |scale| of `count` scales (fp16 or fp32) as fp32 bits, atomically
+// maxed into *out (which the caller zeroes).
+hipError_t scale_absmax_launch(const void* scales, long long count, int f16, unsigned* out,
+                               hipStream_t stream);
 // AQSGET8 Q8 / Q4 record payload (after its 24-byte header) into the device
 // codes and fp32 scales of a weight with `count` elements.
 hipError_t record_repack_launch(const void* payload, long long count, int block, int bits,

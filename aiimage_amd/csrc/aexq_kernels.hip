@@ -419,6 +419,44 @@ hipError_t generic_launch(int fmt, const QmvParams& p, int grid, hipStream_t str
 
 int logits_argmax_cols_per_wg() { return kArgmaxCols; }
 
+// ---------------------------------------------------------------------------
+// Largest scale magnitude of a weight (load time): |s| as fp32 bits orders
+// like the value, so one unsigned atomicMax per workgroup after a wave and
+// workgroup reduction.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void scale_absmax_kernel(const void* s, long long count,
+                                                                int f16s, unsigned* out) {
+  unsigned m = 0;
+  for (long long i = (long long)blockIdx.x * kThreads + threadIdx.x; i < count;
+       i += (long long)gridDim.x * kThreads) {
+    const float v = f16s ? (float)((const f16*)s)[i] : ((const float*)s)[i];
+    const unsigned b = __builtin_bit_cast(unsigned, v) & 0x7fffffffu;
+    m = b > m ? b : m;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned o = __shfl_xor(m, off, 64);
+    m = o > m ? o : m;
+  }
+  __shared__ unsigned wm[kWaves];
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWaves; ++w) m = wm[w] > m ? wm[w] : m;
+    atomicMax(out, m);
+  }
+}
+
+hipError_t scale_absmax_launch(const void* scales, long long count, int f16, unsigned* out,
+                               hipStream_t stream) {
+  if (count <= 0) return hipSuccess;
+  long long blocks = (count + kThreads - 1) / kThreads;
+  if (blocks > 1024) blocks = 1024;
+  hipLaunchKernelGGL(scale_absmax_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, scales,
+                     count, f16, out);
+  return hipGetLastError();
+}
+
 hipError_t logits_argmax_launch(const void* logits, int mode, int m, int n, long long rstride,
                                 float* pv, int* pi, float* ps, int parts, hipStream_t stream) {
   if (mode == kLogitsF16)

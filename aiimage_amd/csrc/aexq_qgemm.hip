@@ -9,21 +9,24 @@
 namespace aexq {
 
 // the register-staged kernel: Q4 with scale groups of 64 or more codes
-#define QGE(PAIR, SF16)                                                       \
-  QgemmEntry {                                                                \
-    QgemmConfig{kQ4, 64, PAIR, SF16, false, false}, &qgemm_kernel<PAIR, SF16> \
+#define QGE(PAIR, SF16)                                                              \
+  QgemmEntry {                                                                       \
+    QgemmConfig{kQ4, 64, PAIR, SF16, false, false, false}, &qgemm_kernel<PAIR, SF16> \
   }
-// LDS-direct forms (aexq_qgemm_dl.hpp): Q8; Q4 in groups of 16 or 32; fp16
-// or fp32 scales; 128-row tiles two workgroups per CU, 64-row tiles three
-#define QGDL(FMT, BM, PAIR, SF16, G)                                          \
+// LDS-direct forms (aexq_qgemm_dl.hpp): Q8; Q4 in groups of 16 or 32, with
+// fp16 dequantisation (FD) or exact per-group fp32 scaling; fp16 or fp32
+// scales; 128-row tiles two workgroups per CU, 64-row tiles three
+#define QGDL(FMT, BM, PAIR, SF16, G, FD)                                      \
   QgemmEntry {                                                                \
-    QgemmConfig{FMT, BM, PAIR, SF16, G == 16, true},                          \
-        &qgemm_dl_kernel<FMT, BM, PAIR, SF16, G, BM == 128 ? 2 : 3>           \
+    QgemmConfig{FMT, BM, PAIR, SF16, G == 16, true, FD},                      \
+        &qgemm_dl_kernel<FMT, BM, PAIR, SF16, G, FD, BM == 128 ? 2 : 3>       \
   }
-#define QGDL_PS(FMT, BM, G)                                                    \
-  QGDL(FMT, BM, false, true, G), QGDL(FMT, BM, false, false, G),              \
-      QGDL(FMT, BM, true, true, G), QGDL(FMT, BM, true, false, G)
-#define QGDL_BM(BM) QGDL_PS(kQ8, BM, 0), QGDL_PS(kQ4, BM, 32), QGDL_PS(kQ4, BM, 16)
+#define QGDL_PS(FMT, BM, G, FD)                                                \
+  QGDL(FMT, BM, false, true, G, FD), QGDL(FMT, BM, false, false, G, FD),      \
+      QGDL(FMT, BM, true, true, G, FD), QGDL(FMT, BM, true, false, G, FD)
+#define QGDL_BM(BM)                                                            \
+  QGDL_PS(kQ8, BM, 0, false), QGDL_PS(kQ4, BM, 32, false), QGDL_PS(kQ4, BM, 16, false), \
+      QGDL_PS(kQ4, BM, 32, true), QGDL_PS(kQ4, BM, 16, true)
 
 static const QgemmEntry kTableG[] = {QGE(false, true), QGE(false, false), QGE(true, true),
                                      QGE(true, false), QGDL_BM(64), QGDL_BM(128)};
@@ -34,7 +37,7 @@ const QgemmEntry* qgemm_find(const QgemmConfig& c) {
   for (int i = 0; i < kCountG; ++i) {
     const QgemmConfig& q = kTableG[i].cfg;
     if (q.fmt == c.fmt && q.bm == c.bm && q.pair == c.pair && q.sf16 == c.sf16 &&
-        q.g16 == c.g16 && q.direct == c.direct)
+        q.g16 == c.g16 && q.direct == c.direct && q.fd == c.fd)
       return &kTableG[i];
   }
   return nullptr;

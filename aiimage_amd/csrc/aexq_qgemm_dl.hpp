@@ -21,11 +21,21 @@
 // scale group of 32 or two of 16.
 //
 // Codes become exact fp16 integers in registers.  Q8 accumulates the row in
-// the MFMA and applies its row scale once at the end.  Q4 scales each
-// group's product in fp32 into the accumulator (the dequantised weight is
-// exactly float(q) * scale): one MFMA per 32-code extent, or for groups of 16
-// two, each with the other group's lanes' codes zeroed.  (Folding fp16
-// scales into B as two exact fp16 parts measured slower: twice the MFMAs.)
+// the MFMA and applies its row scale once at the end.  Q4 has two forms:
+//  * fp16 dequantisation (FD, the default): each lane's eight codes of an
+//    MFMA extent share one scale (lane group g holds codes 8 g .. 8 g + 7, so
+//    a group of 16 is lane groups 0-1 or 2-3), and the B fragment is formed as
+//    fp16(q * s) by one packed fp16 multiply (one rounding; fp32 scales are
+//    rounded to fp16 first), the weight tile dequantised to fp16 as the
+//    benchmark's batched case specifies; the MFMA then accumulates the whole
+//    row in fp32 with no per-group work, for groups of 16 as for 32.  The host
+//    takes this form only for weights whose scales keep 8 |s| within the fp16
+//    range.
+//  * exact (AEXQ_EPI_EXACT_DEQUANT): each group's product is scaled in fp32
+//    into the accumulator, so the dequantised weight is exactly
+//    float(q) * scale: one MFMA per 32-code extent, or for groups of 16 two,
+//    each with the other group's lanes' codes zeroed.  (Folding fp16 scales
+//    into B as two exact fp16 parts measured slower: twice the MFMAs.)
 //
 // Activation rows are 128 bytes per step in LDS with their 16-byte chunks
 // XOR-swizzled by the row (chunk c of row r at slot c ^ ((r & 7) ^ ((r >> 3) & 1))),
@@ -120,10 +130,11 @@ __device__ __forceinline__ void q4_pairs_seq(uint32_t w, uint32_t q[4]) {
   }
 }
 
-template <int FMT, int BM, bool PAIR, bool SF16, int G>
+template <int FMT, int BM, bool PAIR, bool SF16, int G, bool FD>
 struct QGemmDL {
   static_assert(FMT == kQ8 ? G == 0 : (G == 16 || G == 32),
                 "Q8 (row scales) or Q4 in groups of 16 or 32");
+  static_assert(!FD || FMT == kQ4, "fp16 dequantisation is a Q4 form");
   static_assert(BM == 64 || BM == 128, "64- or 128-row activation tiles");
   static constexpr int BN = 128;                  // weight rows of a tile
   static constexpr int BK = 64;                   // K per step
@@ -246,8 +257,9 @@ struct QGemmDL {
   // Fragments of one step a wave reads from LDS: the activation blocks of one
   // K half and the raw codes (and Q4 scales) of both halves.
   // (Q4: the lane's 8 codes of each MFMA extent and the row's scales of the
-  // step, one per extent or two for groups of 16)
-  static constexpr int NS = FMT == kQ8 ? 1 : SPR;
+  // step, one per extent or two for groups of 16; FD: the lane's own scale
+  // of each extent)
+  static constexpr int NS = FMT == kQ8 ? 1 : (FD ? 2 : SPR);
   struct Frag {
     f16x8 a[TM];
     typename std::conditional<FMT == kQ8, u32x4, u32x2>::type c[TN];
@@ -268,7 +280,8 @@ struct QGemmDL {
     for (int kk = 0; kk < 2; ++kk)
       L.a_off[kk] = l16 * 128 + (((FMT == kQ8 ? 2 * lk + kk : 4 * kk + lk) ^ f) << 4);
     L.b_off = FMT == kQ8 ? 16 * lane : l16 * 16 + 4 * lk;  // Q4: + 256 kk
-    L.s_off = FMT == kQ8 ? 0 : l16 * (SPR * SB);
+    // FD groups of 16: lane groups 2-3 take the extent's second scale
+    L.s_off = FMT == kQ8 ? 0 : l16 * (SPR * SB) + (FD && G == 16 ? (lk >> 1) * SB : 0);
     return L;
   }
 
@@ -289,9 +302,12 @@ struct QGemmDL {
         const char* bb = base + A_BYTES + blk * 512 + L.b_off;
         f.c[tn] = u32x2{*(const uint32_t*)bb, *(const uint32_t*)(bb + 256)};
         const char* sb = base + A_BYTES + B_BYTES + blk * 16 * (SPR * SB) + L.s_off;
+        // FD: extent kk's scale sits SPR / 2 scales after extent 0's
+        constexpr int SSTEP = FD ? SPR / 2 : 1;
 #pragma unroll
         for (int i = 0; i < NS; ++i)
-          f.s[tn][i] = SF16 ? (uint32_t) * (const uint16_t*)(sb + SB * i) : *(const uint32_t*)(sb + 4 * i);
+          f.s[tn][i] = SF16 ? (uint32_t) * (const uint16_t*)(sb + SB * SSTEP * i)
+                            : *(const uint32_t*)(sb + 4 * SSTEP * i);
       }
     }
   }
@@ -309,6 +325,19 @@ struct QGemmDL {
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
           acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bq, acc[tm][tn], 0, 0, 0);
+      } else if constexpr (FD) {
+        // fp16(q * s): the exact codes times the lane's scale, one rounding;
+        // the MFMA accumulates the row
+        uint32_t e[4];
+        q4_pairs_seq(f.c[tn][kk], e);
+        const f16 s16 = (f16)scale_of(f.s[tn][kk], SF16);
+        const f16x2 s2 = {s16, s16};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[j] = as_u(as_h2(e[j]) * s2);
+        const f16x8 bw = pack8(e[0], e[1], e[2], e[3]);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[tm], bw, acc[tm][tn], 0, 0, 0);
       } else {
         // one group per extent (32) or two (16: lane groups 0-1 and 2-3, each
         // MFMA with the other group's codes zeroed); each group's product is
@@ -591,10 +620,10 @@ __device__ __forceinline__ void qgemm_dl_step(const typename G::Src& src, const 
   f = g;
 }
 
-template <int FMT, int BM, bool PAIR, bool SF16, int G, int WPE>
+template <int FMT, int BM, bool PAIR, bool SF16, int G, bool FD, int WPE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WPE)))
 void qgemm_dl_kernel(const QmvParams p, int mtiles) {
-  using Q = QGemmDL<FMT, BM, PAIR, SF16, G>;
+  using Q = QGemmDL<FMT, BM, PAIR, SF16, G, FD>;
   static_assert(Q::C_BYTES <= 3 * Q::STAGE, "the accumulator tile reuses the stages");
   __shared__ __align__(1024) char lds[3 * Q::STAGE];
   __shared__ __align__(16) char qs[FMT == kQ8 ? 1024 : 16];  // Q8 row scales of the tile

@@ -510,6 +510,40 @@ def config3(torch, aexq, ctx, steps: int = 30):
     log(f"config3: {out['config3_decode']}")
     del sess
     torch.cuda.empty_cache()
+    # the same step on the reference's own layer formats (its shipping Q4
+    # archives: two's-complement nibbles with an fp32 scale per 16 codes; Q8
+    # layers with an fp32 scale per row), fused and per operator, as graphs
+    formats = {}
+    for mk in (decoder.ModelConfig.reference_q4, decoder.ModelConfig.reference_q8):
+        fc = mk()
+        fs = decoder.DecodeSession(ctx, fc, fused=True)
+        fs.token.fill_(1)
+        fs.set_position(fc.capacity - 1)
+        res = {}
+        for form in ("fused", "per_operator"):
+            keep = fs.fused
+            if form == "per_operator":
+                fs.fused = None
+            g = fs.capture()
+            for _ in range(3):
+                g.replay()
+            torch.cuda.synchronize()
+            res[form] = timed(g.replay)
+            del g
+            fs.fused = keep
+        fs.check_fused()
+        fb = fc.bytes_per_token(fc.capacity)
+        froof = HBM_PEAK_GBS * 1e9 / fb["total"]
+        formats[fc.format_name] = {
+            "tokens_per_s_graph": tps(res["fused"]), "ms_per_token_graph": round(res["fused"], 4),
+            "per_operator_tokens_per_s_graph": tps(res["per_operator"]),
+            "bytes_per_token": fb["total"], "roofline_tokens_per_s": round(froof, 1),
+            "frac_of_roofline": round(1000.0 / res["fused"] / froof, 4),
+            "fused_grid": fs.fused.info()}
+        log(f"config3 {fc.format_name}: {formats[fc.format_name]}")
+        del fs
+        torch.cuda.empty_cache()
+    out["config3_decode"]["formats"] = formats
     return out
 
 

@@ -42,6 +42,7 @@ namespace Aexis.Hip
         public const uint EpiSwiGluOut = 0x2u;
         public const uint EpiResidualAdd = 0x4u;
         public const uint EpiArgmaxF16 = 0x8u;    // LM head: argmax over fp16-rounded logits (ARGBHalf)
+        public const uint EpiExactDequant = 0x10u; // Q4 at M > 32: float(q) * scale kept exact
 
         // the texture size limit the storage rules are written against (GS:10852)
         public const int TileWidthLimit = 8192;

@@ -77,6 +77,13 @@ typedef int aexq_status;
                                     * M <= 8, of 64 above; a shape no kernel takes returns
                                     * AEXQ_ERR_UNSUPPORTED (no generic fallback) */
 #define AEXQ_EPI_RESIDUAL_ADD 0x4u /* y += residual (BinaryOp Add after o_proj/down) */
+#define AEXQ_EPI_EXACT_DEQUANT 0x10u /* numerics mode, any linear: Q4 weights at M > 32 keep
+                                     * float(q) * scale exact (each scale group's MFMA product
+                                     * scaled in fp32).  Without it the tiled GEMM dequantises
+                                     * Q4 weight tiles to fp16, fp16(q * s) with one rounding
+                                     * (fp32 scales rounded to fp16 first), and accumulates in
+                                     * fp32 -- normwise error about 2.5e-4, within the 1e-3
+                                     * bar -- whenever 8 |s| <= 65504 for every scale. */
 #define AEXQ_EPI_ARGMAX_F16 0x8u   /* LM head only: the argmax (and the top-2 gap) compares the
                                     * logits rounded to fp16, as the reference's ARGBHalf logits
                                     * texture holds them (GL:383-396) when ArgMaxPack4LinearMat

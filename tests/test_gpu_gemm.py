@@ -5,14 +5,18 @@ register-staged one) against the CPU oracle, through the C ABI.
 
 Bars as in the other parity tests: normwise max|y - r| / max|r| <= 1e-3 of the
 float64 oracle for fp16 outputs, 1e-5 for fp32 outputs; stacked weight copies
-equal the single launch bit for bit.  The dequantised weight inside the GEMM is
-exactly float(q) * scale (codes as exact fp16 integers, scales applied in fp32),
-so fp32 outputs carry only fp32 summation-order differences.
+equal the single launch bit for bit.  Q8, and Q4 under AEXQ_EPI_EXACT_DEQUANT,
+keep the dequantised weight exactly float(q) * scale (codes as exact fp16
+integers, scales applied in fp32); the default Q4 form multiplies fp16 weight
+tiles fp16(q * s), so its fp32 outputs are held to 1e-5 against the oracle of
+those fp16 weights (conftest.q4_reference, chosen by the plan's
+fp16_dequant field) and to 1e-3 against the exact oracle.
 """
 import sys
 
 import numpy as np
 import pytest
+from conftest import DequantRef, for_plan, q4_reference
 
 torch = pytest.importorskip("torch")
 
@@ -68,7 +72,7 @@ def _weight(ctx, aexq, orc, bits, n, k, seed, group=32, scale_f16=True, code=1):
     words, scales, _ = synth.q4_weights(n, k, seed, group=group, code=code, scale_dtype=sdt)
     w = ctx.weight(aexq.QuantizedTensor(n * k, group, words, scales, bits=4, nibble_code=code),
                    n, k)
-    return w, orc.dequant_q4(words, scales, n, k, group, nibble_code=code, scale_dtype=odt)
+    return w, q4_reference(orc, words, scales, n, k, group, code, scale_f16)
 
 
 @pytest.mark.parametrize("bits,group,scale_f16,n,k,m,y32", [
@@ -104,8 +108,11 @@ def test_gemm_formats(ctx, aexq, orc, bits, group, scale_f16, n, k, m, y32):
     stride = aexq.storage_elements(aexq.LAYOUT_PACK4_LINEAR, m, n)
     got = y.cpu().numpy().astype(np.float64).reshape(m, stride)
     assert np.all(got[:, n:] == 0)
-    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(wf, plan))
     assert normwise(got[:, :n], ref) <= (TOL32 if y32 else TOL)
+    if isinstance(wf, DequantRef):
+        exact = orc.gemm_gpu_semantics(x16.astype(np.float32), wf.exact)
+        assert normwise(got[:, :n], exact) <= TOL
 
 
 @pytest.mark.parametrize("bits,m,n,k", [(4, 64, 3584, 1024), (4, 150, 1000, 1024),
@@ -130,8 +137,8 @@ def test_gemm_swiglu_rmsnorm(ctx, aexq, orc, bits, m, n, k):
     ctx.linear(wg, xd, yd, **kw)
     torch.cuda.synchronize()
     xn = orc.rmsnorm(x16.astype(np.float32), eps, gamma).astype(np.float16).astype(np.float32)
-    g = orc.gemm_gpu_semantics(xn, gf)
-    u = orc.gemm_gpu_semantics(xn, uf)
+    g = orc.gemm_gpu_semantics(xn, for_plan(gf, plan))
+    u = orc.gemm_gpu_semantics(xn, for_plan(uf, plan))
     ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32)) for r in range(m)])
     got = y.cpu().numpy().astype(np.float64).reshape(m, -1)[:, :n]
     assert normwise(got, ref) <= TOL
@@ -193,8 +200,10 @@ def test_gemm_stacked_copies_batched_x_match_single(ctx, aexq, orc, monkeypatch,
     singles = []
     for c in range(copies):
         y1 = aexq.new_activation(m, n, torch.float16, aexq.LAYOUT_PACK4_LINEAR)
-        ctx.linear(w, aexq.describe(dev(xs[c * m:(c + 1) * m]), m, k),
-                   aexq.describe(y1, m, n, aexq.LAYOUT_PACK4_LINEAR))
+        x1 = aexq.describe(dev(xs[c * m:(c + 1) * m]), m, k)
+        y1d = aexq.describe(y1, m, n, aexq.LAYOUT_PACK4_LINEAR)
+        plan1 = ctx.plan_check(w, x1, y1d)
+        ctx.linear(w, x1, y1d)
         singles.append(y1)
     st = w.replicate(copies)
     ys = torch.zeros(copies * m * n, dtype=torch.float16, device="cuda")
@@ -205,7 +214,7 @@ def test_gemm_stacked_copies_batched_x_match_single(ctx, aexq, orc, monkeypatch,
     torch.cuda.synchronize()
     for c in range(copies):
         assert torch.equal(ys[c * m * n:(c + 1) * m * n], singles[c]), c
-    ref = orc.gemm_gpu_semantics(xs[:m].astype(np.float32), wf)
+    ref = orc.gemm_gpu_semantics(xs[:m].astype(np.float32), for_plan(wf, plan1))
     assert normwise(singles[0].cpu().numpy().reshape(m, n), ref) <= TOL
 
 
@@ -218,11 +227,13 @@ def test_gemm_stacked_copies_batched_x_match_single(ctx, aexq, orc, monkeypatch,
     (True, 384, 1216, 80, True),      # 19 K steps, gate/up pair
 ])
 @pytest.mark.parametrize("splitk", ["", "3"])
-def test_gemm_group16(ctx, aexq, orc, monkeypatch, scale_f16, n, k, m, swiglu, splitk):
-    """Q4 with one scale per 16 codes on the tiled GEMM: two MFMAs per 32-code
-    extent, each group's product scaled in fp32 (exact float(q) * scale).  With
-    three forced K chunks the chunks' step counts differ (a tail of the
-    three-step loop, or none)."""
+@pytest.mark.parametrize("exact", [False, True])
+def test_gemm_group16(ctx, aexq, orc, monkeypatch, scale_f16, n, k, m, swiglu, splitk, exact):
+    """Q4 with one scale per 16 codes on the tiled GEMM, in both forms: fp16
+    weight tiles (each lane's eight codes of an extent share one scale, one
+    MFMA per extent) and the exact one (two MFMAs per 32-code extent, each
+    group's product scaled in fp32).  With three forced K chunks the chunks'
+    step counts differ (a tail of the three-step loop, or none)."""
     if splitk:
         monkeypatch.setenv("AEXQ_SPLITK", splitk)
     _announce(f"qgemm group16 f16={scale_f16} n={n} k={k} m={m} swiglu={swiglu} splitk={splitk}")
@@ -232,17 +243,18 @@ def test_gemm_group16(ctx, aexq, orc, monkeypatch, scale_f16, n, k, m, swiglu, s
     y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
     xd = aexq.describe(dev(x16), m, k)
     yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
-    kw = {}
+    kw = dict(exact=exact)
     if swiglu:
         wu, uf = _weight(ctx, aexq, orc, 4, n, k, 93 + m, group=16, scale_f16=scale_f16, code=0)
-        kw = dict(up=wu)
+        kw["up"] = wu
     plan = ctx.plan_check(w, xd, yd, **kw)
     assert plan.startswith("kernel=qgemm") and "direct=1" in plan, plan
+    assert f"fp16_dequant={0 if exact else 1}" in plan, plan
     ctx.linear(w, xd, yd, **kw)
     torch.cuda.synchronize()
-    g = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    g = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(wf, plan))
     if swiglu:
-        u = orc.gemm_gpu_semantics(x16.astype(np.float32), uf)
+        u = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(uf, plan))
         ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32))
                         for r in range(m)])
     else:
@@ -276,12 +288,46 @@ def test_gemm_q4_extreme_scales_exact(ctx, aexq, orc, group):
     y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
     xd = aexq.describe(dev(x16), m, k)
     yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
-    plan = ctx.plan_check(w, xd, yd)
-    assert "direct=1" in plan, plan
-    ctx.linear(w, xd, yd)
+    plan = ctx.plan_check(w, xd, yd, exact=True)
+    assert "direct=1" in plan and "fp16_dequant=0" in plan, plan
+    ctx.linear(w, xd, yd, exact=True)
     torch.cuda.synchronize()
     ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
     assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
+
+
+@pytest.mark.parametrize("big", [8000.0, 9000.0, float("inf")])
+def test_gemm_fp16_dequant_needs_finite_products(ctx, aexq, orc, big):
+    """The fp16 weight tile is chosen only when 8 |s| fits fp16 for every scale
+    of the weight: a weight with one fp32 scale of 9000 (q * s up to 72000)
+    takes the exact form by itself and stays within the fp32 bar; 8000 (64000,
+    finite) keeps the fp16 tile; an infinite scale takes the exact form and
+    propagates to its output column as the oracle's does."""
+    _announce(f"qgemm fp16 dequant guard {big}")
+    from aiimage_amd import synth
+    n, k, m = 256, 512, 96
+    words, scales, _ = synth.q4_weights(n, k, 97, group=16, code=synth.NIBBLE_TWOS,
+                                        scale_dtype=np.float32)
+    scales = scales.copy()
+    scales[5] = np.float32(big)
+    w = ctx.weight(aexq.QuantizedTensor(n * k, 16, words, scales, bits=4,
+                                        nibble_code=synth.NIBBLE_TWOS), n, k)
+    x16 = synth.activations(m, k, 98)
+    y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
+    xd = aexq.describe(dev(x16), m, k)
+    yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    plan = ctx.plan_check(w, xd, yd)
+    want_fd = big < 65504.0 / 8
+    assert f"fp16_dequant={int(want_fd)}" in plan, plan
+    ctx.linear(w, xd, yd)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(m, n).astype(np.float64)
+    ref = orc.gemm_gpu_semantics(
+        x16.astype(np.float32),
+        for_plan(q4_reference(orc, words, scales, n, k, 16, synth.NIBBLE_TWOS, False), plan))
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(got), fin)
+    assert normwise(got[fin], ref[fin]) <= TOL32
 
 
 @pytest.mark.parametrize("bits,group", [(8, 0), (4, 32), (4, 16)])
@@ -306,7 +352,7 @@ def test_gemm_direct_step_counts(ctx, aexq, orc, bits, group, k, m):
     stride = aexq.storage_elements(aexq.LAYOUT_PACK4_LINEAR, m, n)
     got = y.cpu().numpy().reshape(m, stride)
     assert np.all(got[:, n:] == 0)
-    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(wf, plan))
     assert normwise(got[:, :n], ref) <= TOL32
 
 
@@ -331,8 +377,8 @@ def test_gemm_direct_pairs(ctx, aexq, orc, bits, group, scale_f16, m):
     assert plan.startswith("kernel=qgemm") and "direct=1" in plan, plan
     ctx.linear(wg, xd, yd, up=wu)
     torch.cuda.synchronize()
-    g = orc.gemm_gpu_semantics(x16.astype(np.float32), gf)
-    u = orc.gemm_gpu_semantics(x16.astype(np.float32), uf)
+    g = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(gf, plan))
+    u = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(uf, plan))
     ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32)) for r in range(m)])
     assert normwise(y.cpu().numpy().reshape(m, -1)[:, :n], ref) <= TOL32
 
@@ -340,9 +386,11 @@ def test_gemm_direct_pairs(ctx, aexq, orc, bits, group, scale_f16, m):
 @pytest.mark.parametrize("group,scale_f16", [(16, False), (32, False), (16, True)])
 @pytest.mark.parametrize("k", [64, 192, 320])
 @pytest.mark.parametrize("m", [40, 100])
-def test_gemm_direct_group_scaling(ctx, aexq, orc, group, scale_f16, k, m):
-    """Q4 per-group fp32 scaling on the LDS-direct kernel, fp32 and fp16
-    scales: 1, 3 and 5 K steps, both tile heights."""
+@pytest.mark.parametrize("exact", [False, True])
+def test_gemm_direct_group_scaling(ctx, aexq, orc, group, scale_f16, k, m, exact):
+    """Q4 scales on the LDS-direct kernel in both forms (fp16 weight tiles; exact
+    per-group fp32 scaling), fp32 and fp16 scales: 1, 3 and 5 K steps, both
+    tile heights."""
     _announce(f"qgemm direct per-group g={group} f16={scale_f16} k={k} m={m}")
     from aiimage_amd import synth
     n = 200
@@ -352,12 +400,12 @@ def test_gemm_direct_group_scaling(ctx, aexq, orc, group, scale_f16, k, m):
     y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
     xd = aexq.describe(dev(x16), m, k)
     yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
-    plan = ctx.plan_check(w, xd, yd)
-    assert "direct=1" in plan, plan
-    ctx.linear(w, xd, yd)
+    plan = ctx.plan_check(w, xd, yd, exact=exact)
+    assert "direct=1" in plan and f"fp16_dequant={0 if exact else 1}" in plan, plan
+    ctx.linear(w, xd, yd, exact=exact)
     torch.cuda.synchronize()
     stride = aexq.storage_elements(aexq.LAYOUT_PACK4_LINEAR, m, n)
     got = y.cpu().numpy().reshape(m, stride)
     assert np.all(got[:, n:] == 0)
-    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(wf, plan))
     assert normwise(got[:, :n], ref) <= TOL32

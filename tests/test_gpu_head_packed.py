@@ -11,6 +11,7 @@ import sys
 
 import numpy as np
 import pytest
+from conftest import for_plan, q4_reference
 
 torch = pytest.importorskip("torch")
 
@@ -56,7 +57,7 @@ def _q4(ctx, aexq, orc, n, k, seed):
     words, scales, _ = synth.q4_weights(n, k, seed, group=32, code=synth.NIBBLE_OFFSET8)
     w = ctx.weight(aexq.QuantizedTensor(n * k, 32, words, scales, bits=4,
                                         nibble_code=synth.NIBBLE_OFFSET8), n, k)
-    return w, orc.dequant_q4(words, scales, n, k, 32, synth.NIBBLE_OFFSET8, orc.SCALE_F16)
+    return w, q4_reference(orc, words, scales, n, k, 32, synth.NIBBLE_OFFSET8, True)
 
 
 def test_qkv_group_head_packed_m1_rmsnorm(ctx, aexq, orc):
@@ -81,7 +82,7 @@ def test_qkv_group_head_packed_m1_rmsnorm(ctx, aexq, orc):
     torch.cuda.synchronize()
     xn = orc.rmsnorm(x16.astype(np.float32), eps, gamma).astype(np.float16).astype(np.float32)
     for (name, heads), wf, y in zip(shapes, wfs, ys):
-        ref = orc.head_pack(orc.gemm_gpu_semantics(xn, wf).astype(np.float32), heads, hd)
+        ref = orc.head_pack(orc.gemm_gpu_semantics(xn, wf.exact).astype(np.float32), heads, hd)
         assert normwise(y.cpu().numpy(), ref) <= TOL, name
 
 
@@ -118,7 +119,8 @@ def test_head_packed_output_families(ctx, aexq, orc, monkeypatch, m, k, y32, ker
     ctx.linear(w, xd, yd, alpha=0.5)
     torch.cuda.synchronize()
     got = y.cpu().numpy().astype(np.float64)
-    ref = orc.head_pack((0.5 * orc.gemm_gpu_semantics(x16.astype(np.float32), wf)).astype(np.float32),
+    ref = orc.head_pack((0.5 * orc.gemm_gpu_semantics(x16.astype(np.float32),
+                                                      for_plan(wf, plan))).astype(np.float32),
                         heads, hd)
     tail = got.reshape(2, m, hd, 4)[1, :, :, 2:]
     assert np.all(tail == 0)
@@ -139,10 +141,11 @@ def test_head_packed_input_o_proj(ctx, aexq, orc, m, heads, hd, xdt):
     y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
     xd = aexq.describe(dev(xhp), m, k, aexq.LAYOUT_HEAD_PACKED, head_dim=hd)
     yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
+    plan = ctx.plan_check(w, xd, yd)
     ctx.linear(w, xd, yd)
     torch.cuda.synchronize()
     xr = orc.head_unpack(xhp.astype(np.float32), m, heads, hd)
-    ref = orc.gemm_gpu_semantics(xr, wf)
+    ref = orc.gemm_gpu_semantics(xr, for_plan(wf, plan))
     assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
 
 

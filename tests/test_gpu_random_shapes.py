@@ -15,6 +15,7 @@ import sys
 
 import numpy as np
 import pytest
+from conftest import for_plan, q4_reference
 
 torch = pytest.importorskip("torch")
 
@@ -88,8 +89,7 @@ def _weight(ctx, aexq, orc, c, seed):
                                         scale_dtype=sdt)
     w = ctx.weight(aexq.QuantizedTensor(n * k, c["group"], words, scales, bits=4,
                                         nibble_code=c["code"]), n, k)
-    return w, orc.dequant_q4(words, scales, n, k, c["group"], nibble_code=c["code"],
-                             scale_dtype=odt)
+    return w, q4_reference(orc, words, scales, n, k, c["group"], c["code"], c["sf16"])
 
 
 @pytest.mark.parametrize("case", _cases(), ids=lambda c: f"c{c['i']}")
@@ -117,23 +117,18 @@ def test_random_linear_against_oracle(ctx, aexq, orc, case):
         kw.update(rmsnorm=True, rms_gamma=gd, rms_eps=eps)
         xr = orc.rmsnorm(xr, eps, gamma).astype(np.float16).astype(np.float32)
         tol = TOL
-    ref = orc.gemm_gpu_semantics(xr, wf)
+    stride = aexq.storage_elements(layout, m, n)
     if epi == "swiglu":
         wu, uf = _weight(ctx, aexq, orc, c, c["seed"] + 3)
         keep.append(wu)
         kw["up"] = wu
-        u = orc.gemm_gpu_semantics(xr, uf)
-        ref = np.stack([orc.swiglu(ref[r].astype(np.float32), u[r].astype(np.float32))
-                        for r in range(m)])
     elif epi == "residual":
         res = synth.activations(m, n, c["seed"] + 4).astype(np.float32)
-        stride = aexq.storage_elements(layout, m, n)
         rbuf = np.zeros((m, stride), np.float32)
         rbuf[:, :n] = res
         rt = dev(rbuf.reshape(-1)).to(ydt)
         keep.append(rt)
         kw["residual"] = aexq.describe(rt, m, n, layout)
-        ref = ref + rt.cpu().numpy().astype(np.float64).reshape(m, stride)[:, :n]
     elif epi == "bias":
         per_col = bool(c["seed"] & 1)
         alpha, beta = 0.75, 1.25
@@ -146,12 +141,22 @@ def test_random_linear_against_oracle(ctx, aexq, orc, case):
         bt = dev(bias)
         keep.append(bt)
         kw.update(alpha=alpha, beta=beta, c=bt, broadcast_c=bc)
-        ref = orc.gemm_gpu_semantics(xr, wf, alpha=alpha, beta=beta, c=bias, broadcast_c=bc)
     try:
         plan = ctx.plan_check(w, xd, yd, **kw)
     except aexq.NotSupportedError as e:  # the strict plan's refusal (no fallback)
         w.release()
         pytest.skip(f"refused by the plan: {e}")
+    # the weights this plan multiplies (the tiled GEMM's fp16 Q4 tiles, or exact)
+    wf = for_plan(wf, plan)
+    ref = orc.gemm_gpu_semantics(xr, wf)
+    if epi == "swiglu":
+        u = orc.gemm_gpu_semantics(xr, for_plan(uf, plan))
+        ref = np.stack([orc.swiglu(ref[r].astype(np.float32), u[r].astype(np.float32))
+                        for r in range(m)])
+    elif epi == "residual":
+        ref = ref + rt.cpu().numpy().astype(np.float64).reshape(m, stride)[:, :n]
+    elif epi == "bias":
+        ref = orc.gemm_gpu_semantics(xr, wf, alpha=alpha, beta=beta, c=bias, broadcast_c=bc)
     ctx.linear(w, xd, yd, **kw)
     torch.cuda.synchronize()
     stride = aexq.storage_elements(layout, m, n)
@@ -208,10 +213,11 @@ def test_random_grouped_linear_against_oracle(ctx, aexq, orc, case):
         kw.update(rmsnorm=True, rms_gamma=gd, rms_eps=eps)
         xr = orc.rmsnorm(xr, eps, gamma).astype(np.float16).astype(np.float32)
         tol = TOL
+    plan = ctx.plan_check(ws[0], xd, yds[0], **kw)
     ctx.linear_group(ws, xd, yds, **kw)
     torch.cuda.synchronize()
     for i, n in enumerate(c["ns"]):
-        ref = orc.gemm_gpu_semantics(xr, wfs[i])
+        ref = orc.gemm_gpu_semantics(xr, for_plan(wfs[i], plan))
         stride = aexq.storage_elements(layout, m, n)
         got = ys[i].cpu().numpy().astype(np.float64).reshape(m, stride)[:, :n]
         err = normwise(got, ref)
@@ -255,13 +261,14 @@ def test_random_batched_linear_against_oracle(ctx, aexq, orc, case):
     xd = aexq.describe(dev(np.concatenate([x.reshape(-1) for x in xs])), m, k,
                        batch=copies, batch_stride=m * k)
     yd = aexq.describe(y, m, n, layout, batch=copies, batch_stride=per_y)
+    plan = ctx.plan_check(w, xd, yd)
     ctx.linear(w, xd, yd)
     torch.cuda.synchronize()
     stride = aexq.storage_elements(layout, m, n)
     tol = TOL32 if c["y32"] else TOL
     out = y.cpu().numpy().astype(np.float64)
     for b in range(copies):
-        ref = orc.gemm_gpu_semantics(xs[b].astype(np.float32), wf)
+        ref = orc.gemm_gpu_semantics(xs[b].astype(np.float32), for_plan(wf, plan))
         got = out[b * per_y:b * per_y + m * stride].reshape(m, stride)[:, :n]
         err = normwise(got, ref)
         assert err <= tol, (b, err)

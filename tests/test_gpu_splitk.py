@@ -13,6 +13,7 @@ import sys
 
 import numpy as np
 import pytest
+from conftest import for_plan, q4_reference
 
 torch = pytest.importorskip("torch")
 
@@ -67,7 +68,7 @@ def _weight(ctx, aexq, orc, bits, n, k, seed, group=32, scale_f16=True, code=1):
     words, scales, _ = synth.q4_weights(n, k, seed, group=group, code=code, scale_dtype=sdt)
     w = ctx.weight(aexq.QuantizedTensor(n * k, group, words, scales, bits=4, nibble_code=code),
                    n, k)
-    return w, orc.dequant_q4(words, scales, n, k, group, nibble_code=code, scale_dtype=odt)
+    return w, q4_reference(orc, words, scales, n, k, group, code, scale_f16)
 
 
 def _splitk(plan):
@@ -109,7 +110,7 @@ def test_split_matches_oracle(ctx, aexq, orc, monkeypatch, bits, scale_f16, n, k
     stride = aexq.storage_elements(lay, m, n)
     got = y.cpu().numpy().astype(np.float64).reshape(m, stride)
     assert np.all(got[:, n:] == 0)
-    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(wf, plan))
     assert normwise(got[:, :n], ref) <= (TOL32 if y32 else TOL)
     # the same launch again: bit-exact
     y2 = aexq.new_activation(m, n, ydt, lay)
@@ -152,9 +153,9 @@ def test_split_narrow_kernel(ctx, aexq, orc, monkeypatch, bits, group, n, k, m, 
     assert plan.startswith("kernel=qmm") and "wide=0" in plan and _splitk(plan) > 1, plan
     ctx.linear(w, xd, yd, **kw)
     torch.cuda.synchronize()
-    g = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    g = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(wf, plan))
     if pair:
-        u = orc.gemm_gpu_semantics(x16.astype(np.float32), uf)
+        u = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(uf, plan))
         ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32))
                         for r in range(m)])
     else:
@@ -192,9 +193,9 @@ def test_wide_kernel_group16(ctx, aexq, orc, scale_f16, m, pair, rms):
     xr = x16.astype(np.float32)
     if rms:
         xr = orc.rmsnorm(xr, eps, gamma).astype(np.float16).astype(np.float32)
-    g = orc.gemm_gpu_semantics(xr, wf)
+    g = orc.gemm_gpu_semantics(xr, for_plan(wf, plan))
     if pair:
-        u = orc.gemm_gpu_semantics(xr, uf)
+        u = orc.gemm_gpu_semantics(xr, for_plan(uf, plan))
         ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32))
                         for r in range(m)])
     else:
@@ -225,7 +226,7 @@ def test_forced_chunk_counts(ctx, aexq, orc, monkeypatch, chunks, kernel, m):
     assert plan.startswith(f"kernel={kernel}") and _splitk(plan) == -(-steps // cs), plan
     ctx.linear(w, xd, yd)
     torch.cuda.synchronize()
-    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), wf)
+    ref = orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(wf, plan))
     assert normwise(y.cpu().numpy().reshape(m, n), ref) <= TOL32
 
 
@@ -249,8 +250,8 @@ def test_split_swiglu_rmsnorm(ctx, aexq, orc, bits, m):
     ctx.linear(wg, xd, yd, **kw)
     torch.cuda.synchronize()
     xn = orc.rmsnorm(x16.astype(np.float32), eps, gamma).astype(np.float16).astype(np.float32)
-    g = orc.gemm_gpu_semantics(xn, gf)
-    u = orc.gemm_gpu_semantics(xn, uf)
+    g = orc.gemm_gpu_semantics(xn, for_plan(gf, plan))
+    u = orc.gemm_gpu_semantics(xn, for_plan(uf, plan))
     ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32)) for r in range(m)])
     got = y.cpu().numpy().astype(np.float64).reshape(m, -1)[:, :n]
     assert normwise(got, ref) <= TOL
@@ -303,14 +304,15 @@ def test_split_grouped_head_packed(ctx, aexq, orc, m):
     shapes = [(2048, 16), (512, 4), (512, 4)]
     ws, refs, ys, yds = [], [], [], []
     x16 = synth.activations(m, k, 61)
+    xd = aexq.describe(dev(x16), m, k)
     for i, (n, heads) in enumerate(shapes):
         w, wf = _weight(ctx, aexq, orc, 4, n, k, 62 + i)
         ws.append(w)
-        refs.append(orc.gemm_gpu_semantics(x16.astype(np.float32), wf))
         y = aexq.new_activation(m, n, torch.float16, aexq.LAYOUT_HEAD_PACKED, head_dim=hd)
         ys.append(y)
         yds.append(aexq.describe(y, m, n, aexq.LAYOUT_HEAD_PACKED, head_dim=hd))
-    xd = aexq.describe(dev(x16), m, k)
+        plan = ctx.plan_check(w, xd, yds[-1])
+        refs.append(orc.gemm_gpu_semantics(x16.astype(np.float32), for_plan(wf, plan)))
     ctx.linear_group(ws, xd, yds)
     torch.cuda.synchronize()
     for (n, heads), y, ref in zip(shapes, ys, refs):
@@ -435,9 +437,9 @@ def test_rmsnorm_in_kernel(ctx, aexq, orc, monkeypatch, bits, m, pair, group):
     xn = orc.rmsnorm(x16.astype(np.float32), eps, synth.rms_gamma(k, 122))
     xn = xn.astype(np.float16).astype(np.float32)
     for y, yp, wf, n in zip(ys, ys_pre, wfs, shapes):
-        g = orc.gemm_gpu_semantics(xn, wf)
+        g = orc.gemm_gpu_semantics(xn, for_plan(wf, plan))
         if pair:
-            u = orc.gemm_gpu_semantics(xn, uf)
+            u = orc.gemm_gpu_semantics(xn, for_plan(uf, plan))
             ref = np.stack([orc.swiglu(g[r].astype(np.float32), u[r].astype(np.float32))
                             for r in range(m)])
         else:
