@@ -1,8 +1,10 @@
 """aexq_lmhead_argmax_noalloc (the LM head for callers that cannot allocate)
 against aexq_lmhead_argmax on the same inputs, through the C ABI: two calls in
 a row, the second smaller, each equal to the allocating entry point bit for bit
-(argmax and top-2 gap), and the oracle's argmax unless near-tie.  Sizes the
-fixed scratch cannot take, and the logits path, are refused.
+(argmax and top-2 gap), and the oracle's argmax unless near-tie.  Its first
+call on a fresh context can be captured into a HIP graph (nothing grows), and
+the replays match.  Sizes the fixed scratch cannot take, and the logits path,
+are refused.
 """
 import sys
 
@@ -59,6 +61,55 @@ def test_noalloc_lmhead_matches_allocating_entry_point(aexq, orc):
         _announce("noalloc LM head: 151936 x 1024, M = 8, then 20000 x 1024, M = 1")
         _case(ctx, aexq, orc, 151936, 8, 1300)
         _case(ctx, aexq, orc, 20000, 1, 1310)
+    finally:
+        torch.cuda.synchronize()
+        ctx.close()
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_noalloc_first_call_under_capture(aexq, m):
+    """The entry point allocates nothing: on a fresh context (no scratch grown
+    yet) its very first call is made inside HIP graph capture on a side
+    stream, where any context allocation is refused.  The capture succeeds,
+    and every replay -- with eager work between replays -- gives the argmax and
+    gap of the allocating entry point."""
+    from aiimage_amd import synth
+    n, k = 151936, 1024
+    _announce(f"noalloc first call under graph capture, M = {m}")
+    ctx = aexq.Context(0)
+    try:
+        words, scales, _ = synth.q8_weights(n, k, 1330 + m)
+        w = ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
+        x = torch.as_tensor(synth.activations(m, k, 1331 + m)).cuda()
+        xd = aexq.describe(x, m, k)
+        am = torch.full((m,), -2, dtype=torch.int32, device="cuda")
+        gap = torch.full((m,), -2.0, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        stream = torch.cuda.Stream()
+        ctx.set_stream(stream)
+        g = torch.cuda.CUDAGraph()
+        try:
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+                ctx.lmhead_argmax_noalloc(w, xd, am, gap)
+        finally:
+            ctx.set_stream(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        am_ref = torch.full((m,), -1, dtype=torch.int32, device="cuda")
+        gap_ref = torch.full((m,), -1.0, dtype=torch.float32, device="cuda")
+        ctx.lmhead_argmax(w, xd, None, am_ref, gap_ref)
+        torch.cuda.synchronize()
+        for rep in range(3):
+            am.fill_(-2)
+            gap.fill_(-2.0)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(am, am_ref), (rep, am, am_ref)
+            assert torch.equal(gap, gap_ref), (rep, gap, gap_ref)
+            ctx.lmhead_argmax(w, xd, None, am_ref, gap_ref)   # eager work between replays
+            torch.cuda.synchronize()
+        del g
+        w.release()
     finally:
         torch.cuda.synchronize()
         ctx.close()
