@@ -71,15 +71,17 @@ struct aexq_ctx {
   // split-K partial planes of the MFMA kernels
   float* sk_part = nullptr;
   long long sk_cap = 0;
-  // arrival counters of the in-kernel argmax merge (zeroed at allocation;
-  // every launch leaves them zero)
-  int* am_count = nullptr;
-  long long am_count_cap = 0;
+  // tagged argmax partials of the in-kernel merge (three planes) and its epoch
+  // word (both zeroed at allocation)
+  unsigned long long* am_tagged = nullptr;
+  long long am_tagged_cap = 0;
+  unsigned* am_epoch = nullptr;
+  long long am_epoch_cap = 0;
   // scratch buffers replaced by larger ones: a HIP graph captured before the
   // growth still holds their addresses, so they live until aexq_destroy
   std::vector<void*> retired;
   // the device address of the no-allocation entry point's `scratch` array
-  float* noalloc = nullptr;
+  unsigned long long* noalloc = nullptr;
 };
 
 struct aexq_weight {
@@ -107,33 +109,33 @@ struct aexq_weight {
 static long long round_up(long long v, long long a) { return (v + a - 1) / a * a; }
 
 // ---------------------------------------------------------------------------
-// Scratch of aexq_lmhead_argmax_noalloc: the argmax partials of one launch
-// (best value, index, second best; kNoAllocParts entries each, i.e. workgroups
-// x activation rows) and the merge's arrival counters, in a file-scope device
-// array instead of memory the library allocates.  Each GPU holds its own copy from module load to process
-// exit; its address on a device comes from hipGetSymbolAddress, taken once per
-// device when the first context on that device is created.  Every entry the
-// argmax merge reads is written by the same call; the counters start at zero
-// (the array is zero-initialised at load) and every call leaves them zero.
-// Calls that overlap on one GPU (other streams or contexts) share the array
-// and race.
+// Scratch of aexq_lmhead_argmax_noalloc: the tagged argmax partials of one
+// launch (three planes of kNoAllocParts 64-bit words: best, index, second, one
+// word per workgroup and activation row) and the epoch word, in a file-scope
+// device array instead of memory the library allocates.  Each GPU holds its
+// own copy from module load to process exit; its address on a device comes
+// from hipGetSymbolAddress, taken once per device when the first context on
+// that device is created.  The array is zero-initialised at load; every call
+// tags its partials with the epoch plus one and leaves that tag as the next
+// epoch, so no call clears anything.  Calls that overlap on one GPU (other
+// streams or contexts) share the array and race.
 // ---------------------------------------------------------------------------
-constexpr long long kNoAllocParts = 32768;  // 3 x 128 KiB
-static __device__ __align__(256) float scratch[3 * kNoAllocParts + kArgCounterInts];
+constexpr long long kNoAllocParts = 16384;  // 3 x 128 KiB
+static __device__ __align__(256) unsigned long long scratch[3 * kNoAllocParts + kArgEpochInts / 2];
 constexpr int kMaxDevices = 64;
 static std::mutex g_noalloc_mu;
-static float* g_noalloc_ptr[kMaxDevices];      // device address of `scratch` per device
+static unsigned long long* g_noalloc_ptr[kMaxDevices];  // device address of `scratch` per device
 static hipError_t g_noalloc_err[kMaxDevices];  // why it is missing, if it is
 
 // With `device` current: the device address of `scratch` on it (once).
-static float* noalloc_scratch(int device) {
+static unsigned long long* noalloc_scratch(int device) {
   if (device < 0 || device >= kMaxDevices) return nullptr;
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
   if (!g_noalloc_ptr[device] && g_noalloc_err[device] == hipSuccess) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e == hipSuccess && p) {
-      g_noalloc_ptr[device] = (float*)p;
+      g_noalloc_ptr[device] = (unsigned long long*)p;
     } else {
       g_noalloc_err[device] = e != hipSuccess ? e : hipErrorInvalidSymbol;
       (void)hipGetLastError();  // leave no sticky error for the caller's next launch
@@ -203,7 +205,8 @@ extern "C" void aexq_destroy(aexq_ctx* ctx) {
   (void)hipFree(ctx->attn_part);
   (void)hipFree(ctx->attn_count);
   (void)hipFree(ctx->sk_part);
-  (void)hipFree(ctx->am_count);
+  (void)hipFree(ctx->am_tagged);
+  (void)hipFree(ctx->am_epoch);
   for (void* b : ctx->retired) (void)hipFree(b);
   delete ctx;
 }
@@ -1306,8 +1309,9 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     // Workgroups queued beyond the resident count stream best: Q4 16 of 4
     // waves per CU (config 2, against 6, 8, 12, 20, 24 and 32), Q8 12 (config
     // 1, against the resident count, 8 and 16).  Argmax launches stay at the
-    // resident count: every workgroup ends in a partial store and an arrival
-    // count, which queued workgroups would pay many times over.
+    // resident count (config 5, M = 1: 34.0 us against 36.0 at 8 per CU and
+    // 46.5 at 16): their waves split the vocabulary by rows, and queued
+    // workgroups would each pay the prologue and the partial store.
     int per_cu = qmv_blocks_per_cu(plan->entry);
     const bool fused_argmax = plan->entry->cfg.argmax;
     const int queued = fused_argmax ? per_cu : (fmt == kQ4 ? 16 : 12);
@@ -1318,10 +1322,10 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     long long cap = (long long)per_cu * ctx->cus;
     if (fused_argmax) {
       // every workgroup's logits fit its LDS buffer: at most kArgLogitsMax
-      // (rows x M) per workgroup
-      const long long per_tile = (long long)plan->entry->rw * plan->entry->cfg.mmax;
-      const long long tiles_max = kArgLogitsMax / per_tile;
-      const long long g = (tiles_total + tiles_max - 1) / tiles_max;
+      // (rows x M) per workgroup, the rows (Pack4 padding included) split
+      // evenly over the workgroups
+      const long long rows_max = kArgLogitsMax / plan->entry->cfg.mmax;
+      const long long g = ((long long)p.mat[0].n_store + rows_max - 1) / rows_max;
       if (g > cap) cap = g;
     }
     plan->grid = (int)(need < cap ? need : cap);
@@ -1510,13 +1514,12 @@ static aexq_status argmax_over_logits(aexq_ctx* ctx, const void* logits, int mod
   return AEXQ_OK;
 }
 
-// Where one LM-head launch writes its argmax partials: the context's growing
-// scratch, or a fixed buffer of `cap` entries per array.
+// Where one LM-head launch writes its tagged argmax partials: the context's
+// growing scratch, or a fixed buffer of `cap` words per plane.
 struct Partials {
-  float* best = nullptr;
-  int* index = nullptr;
-  float* second = nullptr;
-  int* count = nullptr;  // the merge's arrival counters (kArgCounterInts)
+  unsigned long long* tagged = nullptr;  // three planes of `plane` words
+  long long plane = 0;
+  unsigned* epoch = nullptr;
   long long cap = 0;
 };
 
@@ -1525,15 +1528,21 @@ static bool lmhead_fused(const Plan& plan) {
          (plan.kind == kPlanMfma && plan.mentry->cfg.argmax);
 }
 
-// The LM head with the argmax fused into the matvec: M = 1 on the streaming
-// kernel, M = 2..32 on the wide MFMA kernel; one (best, index, second)
-// partial per workgroup and row, then the merge.  `fixed` null: the
-// partials go to the context's scratch (grown as needed).
+// The LM head with the argmax fused into the matvec: M = 1..8 on the
+// streaming kernel, M >= 2 on the wide MFMA kernel (one launch per block of up
+// to 32 rows); one (best, index, second) partial per workgroup and row, merged
+// in the same launch by its last workgroup (no finalize launch).  `fixed`
+// null: the partials go to the context's scratch (grown as needed).
 static aexq_status lmhead_fused_launch(aexq_ctx* ctx, Plan& plan, const char* op,
                                        int32_t* argmax, float* top2_gap, const Partials* fixed) {
   const int M = plan.p.m;
   const int parts = plan.grid;  // one partial per workgroup and row
   const long long need = (long long)parts * M;
+  // the MFMA path launches once per block of mblock rows, each merging its own
+  const int rows = plan.kind == kPlanMfma && plan.mblock < M ? plan.mblock : M;
+  if (rows > kArgMergeRows)
+    return fail(AEXQ_ERR_UNSUPPORTED, op, "fused argmax over %d rows per launch (at most %d)",
+                rows, kArgMergeRows);
   Partials pt;
   if (fixed) {
     if (need > fixed->cap)
@@ -1543,42 +1552,29 @@ static aexq_status lmhead_fused_launch(aexq_ctx* ctx, Plan& plan, const char* op
                   parts, M, need, fixed->cap);
     pt = *fixed;
   } else {
-    aexq_status st = ensure_parts(ctx, need, op);
+    aexq_status st = grow_scratch(ctx, (void**)&ctx->am_tagged, &ctx->am_tagged_cap,
+                                  3 * need * (long long)sizeof(unsigned long long), op,
+                                  "tagged argmax partials", true);
     if (!st)
-      st = grow_scratch(ctx, (void**)&ctx->am_count, &ctx->am_count_cap,
-                        kArgCounterInts * (long long)sizeof(int), op, "argmax counters", true);
+      st = grow_scratch(ctx, (void**)&ctx->am_epoch, &ctx->am_epoch_cap,
+                        kArgEpochInts * (long long)sizeof(unsigned), op, "argmax epoch", true);
     if (st) return st;
-    pt.best = ctx->part_best;
-    pt.index = ctx->part_index;
-    pt.second = ctx->part_second;
-    pt.count = ctx->am_count;
+    pt.tagged = ctx->am_tagged;
+    pt.plane = ctx->am_tagged_cap / (3 * (long long)sizeof(unsigned long long));
+    pt.epoch = ctx->am_epoch;
   }
-  plan.p.part_best = pt.best;
-  plan.p.part_index = pt.index;
-  plan.p.part_second = pt.second;
   plan.p.parts = parts;
-  // M = 1: the last workgroup to finish merges the partials (no finalize
-  // launch).  More rows keep the finalize launch, which merges them all in
-  // one round trip; the in-kernel merge would take one per row.
-  const bool in_kernel = M == 1;
-  if (in_kernel) {
-    plan.p.am_count = pt.count;
-    plan.p.am_out = argmax;
-    plan.p.am_gap = top2_gap;
-  }
+  plan.p.am_tagged = pt.tagged;
+  plan.p.am_plane = pt.plane;
+  plan.p.am_epoch = pt.epoch;
+  plan.p.am_out = argmax;
+  plan.p.am_gap = top2_gap;
   if (plan.fast) {
     hipError_t e = qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, op, "lm head launch");
-  } else {
-    aexq_status st = launch_plan(ctx, plan, op);
-    if (st) return st;
+    return AEXQ_OK;
   }
-  if (!in_kernel) {
-    ArgmaxParams ap{pt.best, pt.index, pt.second, parts, M, argmax, top2_gap};
-    hipError_t e = argmax_finalize_launch(ap, ctx->stream);
-    if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
-  }
-  return AEXQ_OK;
+  return launch_plan(ctx, plan, op);
 }
 
 static aexq_status lmhead_argmax(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
@@ -1661,10 +1657,9 @@ extern "C" aexq_status aexq_lmhead_argmax_noalloc(aexq_ctx* ctx, const aexq_weig
                                       : hipErrorInvalidDevice));
   HIP_TRY(op, hipSetDevice(ctx->device));
   Partials fixed;
-  fixed.best = ctx->noalloc;
-  fixed.index = (int*)(ctx->noalloc + kNoAllocParts);
-  fixed.second = ctx->noalloc + 2 * kNoAllocParts;
-  fixed.count = (int*)(ctx->noalloc + 3 * kNoAllocParts);
+  fixed.tagged = ctx->noalloc;
+  fixed.plane = kNoAllocParts;
+  fixed.epoch = (unsigned*)(ctx->noalloc + 3 * kNoAllocParts);
   fixed.cap = kNoAllocParts;
   return lmhead_fused_launch(ctx, plan, op, argmax, top2_gap, &fixed);
 }

@@ -146,15 +146,32 @@ __device__ __forceinline__ void argmax_wave_reduce(float& bv, int& bi, float& bs
   }
 }
 
-// One (best, index, second) argmax partial of a workgroup; with the in-kernel
-// merge the stores are agent-coherent (written through to the level every
-// XCD reads), since the merging workgroup may run on another XCD.
+// The tag of this launch's argmax partials (in-kernel merge): the epoch the
+// previous merging launch left, plus one, never 0 (the words of a scratch
+// buffer start at tag 0).  Every workgroup reads it before its partial store;
+// the merging workgroup stores it back only after every partial of the launch
+// carries it, so the whole grid reads the same value.
+__device__ __forceinline__ uint32_t argmax_tag(const QmvParams& p) {
+  if (!p.am_tagged) return 0;
+  const uint32_t e = __hip_atomic_load(p.am_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return e == 0xffffffffu ? 1u : e + 1u;
+}
+
+// One (best, index, second) argmax partial of a workgroup.  In-kernel merge:
+// three tagged 64-bit words, each stored whole and agent-coherent (written
+// through to the level every XCD reads, since the merging workgroup may run on
+// another XCD); no fence and no arrival count.  Otherwise plain stores for the
+// finalize launch.
 __device__ __forceinline__ void argmax_partial_store(const QmvParams& p, long long o, float v, int i,
-                                                     float s) {
-  if (p.am_count) {
-    __hip_atomic_store(p.part_best + o, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.part_index + o, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.part_second + o, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                                     float s, uint32_t tag) {
+  if (p.am_tagged) {
+    const unsigned long long t = (unsigned long long)tag << 32;
+    __hip_atomic_store(p.am_tagged + o, t | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.am_tagged + p.am_plane + o, t | (uint32_t)i, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.am_tagged + 2 * p.am_plane + o, t | __float_as_uint(s), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   } else {
     p.part_best[o] = v;
     p.part_index[o] = i;
@@ -162,78 +179,171 @@ __device__ __forceinline__ void argmax_partial_store(const QmvParams& p, long lo
   }
 }
 
-// In-kernel merge of the argmax partials (p.am_count non-null), called by every
-// thread of every workgroup after its partial stores.  Each workgroup counts
-// in on its group's counter (workgroup b in group b % groups); the last of a
-// group counts in on the top counter, and the last of those merges all
-// partials of every row with the argmax comparator (the first-maximum rule of
-// MM:645-686; the merge order is free) and writes the index and top-2 gap.
-// The last arrivals reset the counters, so the launch replays without
-// clearing.  The merge result equals argmax_finalize_kernel's.
-__device__ __forceinline__ void argmax_tail(const QmvParams& p) {
-  if (!p.am_count) return;
-  __shared__ int s_last;
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-  __syncthreads();
+// Order-preserving map of a non-NaN float to an unsigned integer (-0 taken as
+// +0, which the argmax compares equal), and its inverse; the inverse of
+// 0xffffffff is a NaN.
+__device__ __forceinline__ uint32_t argmax_ord(float f) {
+  const uint32_t u = __float_as_uint(f == 0.0f ? 0.0f : f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float argmax_unord(uint32_t u) {
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+
+// Top-2 of packed argmax keys: insert a key into (k1 >= k2), and combine two
+// such pairs.  Every key but the largest reaches k2 (inserted directly, or
+// pushed down by a larger one), and k2 never exceeds the second-largest.
+__device__ __forceinline__ void argmax_top2_insert(unsigned long long& k1, unsigned long long& k2,
+                                                   unsigned long long key) {
+  const unsigned long long lo = k1 < key ? k1 : key;
+  k1 = k1 < key ? key : k1;
+  k2 = k2 < lo ? lo : k2;
+}
+__device__ __forceinline__ void argmax_top2_combine(unsigned long long& k1, unsigned long long& k2,
+                                                    uint32_t& ks, unsigned long long o1,
+                                                    unsigned long long o2, uint32_t os) {
+  argmax_top2_insert(k1, k2, o1);
+  k2 = k2 < o2 ? o2 : k2;
+  ks = ks < os ? os : ks;
+}
+
+// In-kernel merge of the argmax partials (p.am_tagged non-null), called by
+// every thread of every workgroup after its partial stores; only the grid's
+// last workgroup works.  Workgroups are dispatched in index order, so when the
+// last one runs every other has been dispatched and finishes without waiting
+// on anything: the last one's wait ends.
+//
+// Its threads split into one group per row (a power of two, 256 / rows or
+// less); a thread polls its share of the row's partials (agent-coherent loads,
+// kB partials in flight -- 8 in the register-tight streaming kernel, 16 in
+// the MFMA one --, a pause between polls, at most kArgSpinLimit
+// polls) and folds each partial whose three words carry the tag into its own
+//   k1, k2 = the two largest keys, key = ord(best) << 32 | ~index (a larger
+//            value wins, then the lower index; a NaN at index 0 takes the
+//            largest key, any other NaN none): k1 is the first-maximum rule of
+//            MM:645-686 whatever the order the partials arrive in;
+//   ks     = the largest second value.
+// The group combines them by lane shuffles (then through LDS across waves).
+// The top-2 gap is best - max(ks, value of k2): the best of all candidates but
+// the winner, as argmax_finalize_kernel forms it.  A wait that runs out writes
+// index -1 and a NaN gap for every row.  Then the tag becomes the next
+// launch's epoch.
+template <int kB>
+__device__ __forceinline__ void argmax_tail(const QmvParams& p, uint32_t tag) {
+  if (!p.am_tagged || blockIdx.x != gridDim.x - 1) return;
+  __shared__ unsigned long long s_k1[kArgMergeRows], s_k2[kArgMergeRows];
+  __shared__ uint32_t s_ks[kArgMergeRows];
+  __shared__ int s_fail;
+  const int rows = p.m;  // <= kArgMergeRows (host-checked)
   const int parts = p.parts;
-  if (threadIdx.x == 0) {
-    const int groups = parts < kArgGroups ? parts : kArgGroups;
-    const int g = blockIdx.x % groups;
-    const int members = (parts - 1 - g) / groups + 1;
-    int* gc = p.am_count + g * kArgCounterStride;
-    int* top = p.am_count + kArgGroups * kArgCounterStride;
-    int last = 0;
-    if (atomicAdd(gc, 1) == members - 1) {
-      atomicExch(gc, 0);
-      if (atomicAdd(top, 1) == groups - 1) {
-        atomicExch(top, 0);
-        last = 1;
+  int gsz = kThreads;  // threads per row
+  while (gsz > 8 && gsz * rows > kThreads) gsz >>= 1;
+  const int r = (int)threadIdx.x / gsz, gl = (int)threadIdx.x % gsz;
+  if (threadIdx.x == 0) s_fail = 0;
+  __syncthreads();
+  unsigned long long k1 = 0ull, k2 = 0ull;
+  uint32_t ks = argmax_ord(-INFINITY);
+  bool fail = false;
+  if (r < rows) {
+    const long long row0 = (long long)(p.m_base + r) * parts;
+    const unsigned long long* w0 = p.am_tagged + row0;
+    const unsigned long long* w1 = w0 + p.am_plane;
+    const unsigned long long* w2 = w0 + 2 * p.am_plane;
+    for (int i0 = gl; i0 < parts && !fail; i0 += gsz * kB) {
+      unsigned long long a[kB], b[kB], c[kB];
+      bool ok[kB];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int e = i0 + j * gsz;
+        ok[j] = e >= parts;
+        if (!ok[j]) {
+          a[j] = __hip_atomic_load(w0 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          b[j] = __hip_atomic_load(w1 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          c[j] = __hip_atomic_load(w2 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      for (int spin = 0;; ++spin) {
+        bool all = true;
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          if (!ok[j]) {
+            ok[j] = (uint32_t)(a[j] >> 32) == tag && (uint32_t)(b[j] >> 32) == tag &&
+                    (uint32_t)(c[j] >> 32) == tag;
+            all = all && ok[j];
+          }
+        }
+        if (all) break;
+        if (spin >= kArgSpinLimit) {
+          fail = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          const int e = i0 + j * gsz;
+          if (!ok[j]) {
+            a[j] = __hip_atomic_load(w0 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            b[j] = __hip_atomic_load(w1 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            c[j] = __hip_atomic_load(w2 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        if (i0 + j * gsz < parts) {
+          const float v = __uint_as_float((uint32_t)a[j]);
+          const float sv = __uint_as_float((uint32_t)c[j]);
+          const uint32_t ix = (uint32_t)b[j];
+          if (!__builtin_isnan(sv)) {
+            const uint32_t o = argmax_ord(sv);
+            ks = ks < o ? o : ks;
+          }
+          if (!__builtin_isnan(v))
+            argmax_top2_insert(k1, k2, ((unsigned long long)argmax_ord(v) << 32) | (uint32_t)~ix);
+          else if (ix == 0)
+            argmax_top2_insert(k1, k2, ~0ull);
+        }
       }
     }
-    s_last = last;
+  }
+  // combine within each group (aligned lanes of one wave), then per wave
+  const int span = gsz < 64 ? gsz : 64;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    if (off < span) {
+      const unsigned long long o1 = __shfl_xor(k1, off, 64), o2 = __shfl_xor(k2, off, 64);
+      const uint32_t os = __shfl_xor(ks, off, 64);
+      argmax_top2_combine(k1, k2, ks, o1, o2, os);
+    }
+  }
+  if (fail) s_fail = 1;  // benign race: every writer stores 1
+  // the leader of each group, or of each wave of a group wider than a wave
+  const int slot = (int)threadIdx.x / span;
+  if ((int)threadIdx.x % span == 0 && r < rows) {
+    s_k1[slot] = k1;
+    s_k2[slot] = k2;
+    s_ks[slot] = ks;
   }
   __syncthreads();
-  if (!s_last) return;
-  __shared__ float mv[kWaves], ms[kWaves];
-  __shared__ int mi[kWaves];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  constexpr int kBatch = 8;
-  for (int m = 0; m < p.m; ++m) {
-    const long long base = (long long)(p.m_base + m) * parts;
-    float bv = __builtin_nanf("");
-    int bi = 0x7fffffff;
-    float bs = -INFINITY;
-    for (int i0 = threadIdx.x; i0 < parts; i0 += kThreads * kBatch) {
-      float v[kBatch], sv[kBatch];
-      int ix[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int i = i0 + j * kThreads;
-        const bool in = i < parts;
-        v[j] = in ? __hip_atomic_load(p.part_best + base + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                  : __builtin_nanf("");
-        ix[j] = in ? __hip_atomic_load(p.part_index + base + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                   : 0x7fffffff;
-        sv[j] = in ? __hip_atomic_load(p.part_second + base + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                   : -INFINITY;
-      }
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) argmax_merge(bv, bi, bs, v[j], ix[j], sv[j]);
-    }
-    argmax_wave_reduce(bv, bi, bs);
-    if (lane == 0) {
-      mv[wave] = bv;
-      mi[wave] = bi;
-      ms[wave] = bs;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      for (int w = 1; w < kWaves; ++w) argmax_merge(bv, bi, bs, mv[w], mi[w], ms[w]);
-      p.am_out[p.m_base + m] = bi == 0x7fffffff ? 0 : bi;
-      if (p.am_gap) p.am_gap[p.m_base + m] = bs == -INFINITY ? INFINITY : bv - bs;
-    }
-    __syncthreads();
+  if ((int)threadIdx.x < rows) {
+    const int per = gsz / span;  // slots of one row
+    const int q0 = (int)threadIdx.x * per;
+    unsigned long long b1 = s_k1[q0], b2 = s_k2[q0];
+    uint32_t bks = s_ks[q0];
+    for (int q = 1; q < per; ++q)
+      argmax_top2_combine(b1, b2, bks, s_k1[q0 + q], s_k2[q0 + q], s_ks[q0 + q]);
+    const float bv = b1 ? argmax_unord((uint32_t)(b1 >> 32)) : __builtin_nanf("");
+    const int bi = b1 ? (int)~(uint32_t)b1 : 0;
+    float bs = argmax_unord(bks);
+    if (b2) bs = fmaxf(bs, argmax_unord((uint32_t)(b2 >> 32)));
+    const bool bad = s_fail != 0;
+    p.am_out[p.m_base + threadIdx.x] = bad ? -1 : bi;
+    if (p.am_gap)
+      p.am_gap[p.m_base + threadIdx.x] =
+          bad ? __builtin_nanf("") : (bs == -INFINITY ? INFINITY : bv - bs);
   }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(p.am_epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Rank of workgroup bid among the grid's workgroups such that the ranks of

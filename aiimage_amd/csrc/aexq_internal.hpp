@@ -77,10 +77,17 @@ struct QmvParams {
   int* part_index;
   float* part_second;
   int parts;
-  // in-kernel argmax merge (null: a separate finalize launch merges): arrival
-  // counters (kArgGroups lines, then the top counter; zero before the launch,
-  // left zero after it) and the merged index / top-2 gap per row
-  int* am_count;
+  // in-kernel argmax merge (am_tagged null: a separate finalize launch merges
+  // the float partials above).  Every workgroup stores its partial of row r
+  // as three tagged words, tag << 32 | bits of (best, index, second), at
+  // am_tagged[plane * am_plane + r * parts + workgroup]; the tag is the
+  // launch's epoch, am_epoch[0] + 1 (0 skipped), read by every workgroup at
+  // its start.  The last workgroup of the grid polls the words until all
+  // carry the tag, merges them, writes the index / top-2 gap per row and
+  // stores the tag back into am_epoch[0].
+  unsigned long long* am_tagged;
+  long long am_plane;
+  unsigned* am_epoch;
   int32_t* am_out;
   float* am_gap;
   // split K (MFMA kernels): the K steps of every tile run as sk_chunks chunks
@@ -95,12 +102,13 @@ struct QmvParams {
   int sk_cs;
 };
 
-// Arrival counters of the in-kernel argmax merge: kArgGroups groups of
-// workgroups, each counter on its own 256-byte line (device-scope atomics to
-// one line serialise), then one top counter.
-constexpr int kArgGroups = 64;
-constexpr int kArgCounterStride = 64;  // ints
-constexpr int kArgCounterInts = (kArgGroups + 1) * kArgCounterStride;
+// The in-kernel argmax merge: at most kArgMergeRows activation rows per
+// launch, the epoch word on a 256-byte line of its own (kArgEpochInts), and
+// the merging workgroup's bounded wait for each partial (polls with a pause
+// between them; about a second in all).
+constexpr int kArgMergeRows = 32;
+constexpr int kArgEpochInts = 64;
+constexpr int kArgSpinLimit = 1 << 20;
 
 struct ArgmaxParams {
   const float* pv;

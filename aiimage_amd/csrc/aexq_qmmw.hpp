@@ -293,7 +293,7 @@ struct QmmW {
   // One partial per row and workgroup: the 16 lanes of a row group, then the
   // four waves through LDS.  Every wave of the workgroup calls it.
   static __device__ __forceinline__ void best_write(const QmvParams& p, int lane, int wave,
-                                                    Best& b) {
+                                                    Best& b, uint32_t tag) {
     __shared__ float lv[16 * MT][kWaves], ls[16 * MT][kWaves];
     __shared__ int li[16 * MT][kWaves];
 #pragma unroll
@@ -323,7 +323,7 @@ struct QmmW {
       int ix = li[row][0];
 #pragma unroll
       for (int w = 1; w < kWaves; ++w) argmax_merge(v, ix, sv, lv[row][w], li[row][w], ls[row][w]);
-      argmax_partial_store(p, (long long)(p.m_base + row) * p.parts + blockIdx.x, v, ix, sv);
+      argmax_partial_store(p, (long long)(p.m_base + row) * p.parts + blockIdx.x, v, ix, sv, tag);
     }
   }
 
@@ -472,15 +472,15 @@ void qmmw_kernel(const QmvParams p) {
   const int t0 = (int)((i0 / S) * steps + (i0 % S) * cs);
   const int t1 = i1 > i0 ? (int)(((i1 - 1) / S) * steps + min((int)((i1 - 1) % S + 1) * cs, steps))
                          : t0;
+  const uint32_t tag = ARGMAX ? argmax_tag(p) : 0u;
   if (t0 >= t1) {  // the whole workgroup: no barrier is left waiting
     if constexpr (ARGMAX) {
       // an empty partial for each row (it never wins the merge)
-      // (and its arrival, when the launch merges the partials itself)
       const int row = threadIdx.x;
       if (row < 16 * MT && row < p.m)
         argmax_partial_store(p, (long long)(p.m_base + row) * p.parts + blockIdx.x,
-                             __builtin_nanf(""), 0x7fffffff, -INFINITY);
-      argmax_tail(p);
+                             __builtin_nanf(""), 0x7fffffff, -INFINITY, tag);
+      argmax_tail<16>(p, tag);
     }
     return;
   }
@@ -568,8 +568,8 @@ void qmmw_kernel(const QmvParams p) {
     sl ^= 1;
   }
   if constexpr (ARGMAX) {
-    Q::best_write(p, lane, wave, best);
-    argmax_tail(p);
+    Q::best_write(p, lane, wave, best, tag);
+    argmax_tail<16>(p, tag);
   }
 }
 

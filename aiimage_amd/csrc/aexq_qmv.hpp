@@ -37,9 +37,20 @@ struct Qmv {
 #endif
   static constexpr int kValuPerLoad = QMV_VALU_PER_LOAD;
 
+  // Wave-uniform: matrix, batch entry, row tile.  The LM head (ARGMAX) is one
+  // matrix of one batch entry (host-checked) and its waves own row ranges,
+  // not tile ranges: rt is then the tile's first row and rend the end of the
+  // wave's range (rows from rend on belong to the next wave).
   struct Cursor {
-    int j, b, rt;  // matrix, batch entry, row tile (wave-uniform)
+    int j, b, rt, rend;
   };
+
+  static __device__ __forceinline__ int row0(const Cursor& c) { return ARGMAX ? c.rt : c.rt * RW; }
+  // rows of the tile's matrix this wave loads and computes: below n and, for
+  // the LM head, below its range's end
+  static __device__ __forceinline__ int row_limit(const QmvMat& mt, const Cursor& c) {
+    return ARGMAX && c.rend < mt.n ? c.rend : mt.n;
+  }
 
   struct Buf {
     u32x4 w[NW][U][CPL];
@@ -49,16 +60,17 @@ struct Qmv {
 
   typedef uint32_t XRegs[MMAX][CPL][XW];
 
-  // The LM head (ARGMAX) is one matrix of one batch entry (host-checked): its
-  // cursor is the row tile alone, which keeps the tile loop's bookkeeping in
-  // plain scalar arithmetic.
+  // The LM head's cursor (rt the row, rend the range's end) keeps the tile
+  // loop's bookkeeping in plain scalar arithmetic; its kernel forms the first
+  // one itself.
   static __device__ __forceinline__ Cursor locate(const QmvParams& p, int t) {
-    if constexpr (ARGMAX) return Cursor{0, 0, t};
+    if constexpr (ARGMAX) return Cursor{0, 0, t, 0};
     int j = 0;
     for (int i = 1; i < p.nmat; ++i)
       if (t >= p.mat[i].tile_base) j = i;
     const int local = t - p.mat[j].tile_base;
     Cursor c;
+    c.rend = 0;
     c.j = j;
     c.b = local / p.mat[j].tiles;
     c.rt = local - c.b * p.mat[j].tiles;
@@ -66,7 +78,7 @@ struct Qmv {
   }
 
   static __device__ __forceinline__ Cursor advance(const QmvParams& p, Cursor c) {
-    if constexpr (ARGMAX) return Cursor{0, 0, c.rt + 1};
+    if constexpr (ARGMAX) return Cursor{0, 0, c.rt + RW, c.rend};
     if (++c.rt == p.mat[c.j].tiles) {
       c.rt = 0;
       if (++c.b == p.batch) {
@@ -129,7 +141,7 @@ struct Qmv {
   static __device__ __forceinline__ int scale_tile_offset(const QmvParams& p, const Cursor& cu) {
     const int sb = (p.flags & kFlagScaleF16) ? 2 : 4;
     const int sper = FMT == kQ8 ? 1 : p.groups_per_row;
-    return cu.rt * RW * sper * sb;
+    return row0(cu) * sper * sb;
   }
 
   // Issues the loads of one tile without a branch.  Codes: buffer loads
@@ -146,10 +158,12 @@ struct Qmv {
     const QmvMat& mt = p.mat[cu.j];
     const int sb = (p.flags & kFlagScaleF16) ? 2 : 4;
     const long long row_bytes = (long long)p.chunks * 16;
-    const int r0 = cu.rt * RW;
-    // rows of the matrix at or after the tile's first row; a tile inside the
-    // Pack4 padding rows (r0 >= n) gets an empty resource: every load reads 0
-    const int rows = live && mt.n > r0 ? mt.n - r0 : 0;
+    const int r0 = row0(cu);
+    // rows of the matrix at or after the tile's first row (and, for the LM
+    // head, before the wave's range ends); a tile inside the Pack4 padding rows
+    // (r0 >= n) gets an empty resource: every load reads 0
+    const int rlim = row_limit(mt, cu);
+    const int rows = live && rlim > r0 ? rlim - r0 : 0;
     const int sper = FMT == kQ8 ? 1 : p.groups_per_row;
     const int sbytes = live ? (mt.n * sper * sb + 3) & ~3 : 0;
     if constexpr (MMAX == 1 && !ARGMAX) {
@@ -499,19 +513,22 @@ struct Qmv {
     char* yb = (char*)mt.y + cu.b * mt.y_bstride * (yf32 ? 4 : 2);
     const char* rb =
         mt.res ? (const char*)mt.res + cu.b * mt.r_bstride * (yf32 ? 4 : 2) : nullptr;
+    const int rlim = row_limit(mt, cu);
+    // the LM head stores the wave's own rows, Pack4 padding included
+    const int rstore = ARGMAX && cu.rend < mt.n_store ? cu.rend : mt.n_store;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int r = cu.rt * RW + u * SLOTS + slot;
+      const int r = row0(cu) + u * SLOTS + slot;
 #pragma unroll
       for (int m = 0; m < MMAX; ++m) {
         float v = 0.0f;
-        const bool live = r < mt.n && m < p.m;
+        const bool live = r < rlim && m < p.m;
         if constexpr (ARGMAX) {
           // no C and no residual (host-checked); the logits wait in LDS until
           // the tile loop ends, so the loop issues loads only
           if (live) v = argmax_epilogue(p, acc[0][u][m]);
           const int li = (r - lg_r0) * MMAX + m;
-          if (sub == ((u * MMAX + m) & (LPR - 1)) && r < mt.n_store && m < p.m &&
+          if (sub == ((u * MMAX + m) & (LPR - 1)) && r < rstore && m < p.m &&
               li < kArgLogitsMax)
             lg[li] = v;
           if (sub == 0 && live) argmax_merge(bv[m], bi[m], bs[m], argmax_logit(p, v), r, -INFINITY);
@@ -560,8 +577,17 @@ void qmv_kernel(const QmvParams p) {
   const int sub = lane & (LPR - 1), slot = lane / LPR;
   const int gw = blockIdx.x * kWaves + wave;
   const int nw = gridDim.x * kWaves;
-  const int t0 = (int)((long long)gw * p.total_tiles / nw);
-  const int t1 = (int)((long long)(gw + 1) * p.total_tiles / nw);
+  // The LM head splits its rows (Pack4 padding included) evenly over the
+  // waves, so that no wave streams more than one row above the average; its
+  // tiles start at the range's first row and the last one stops at its end.
+  // Other launches split whole tiles.
+  const int n_rows = ARGMAX ? p.mat[0].n_store : 0;
+  const int wr0 = ARGMAX ? (int)((long long)gw * n_rows / nw) : 0;
+  const int wr1 = ARGMAX ? (int)((long long)(gw + 1) * n_rows / nw) : 0;
+  const int t0 = ARGMAX ? 0 : (int)((long long)gw * p.total_tiles / nw);
+  const int t1 = ARGMAX ? (wr1 - wr0 + Q::RW - 1) / Q::RW
+                        : (int)((long long)(gw + 1) * p.total_tiles / nw);
+  const uint32_t tag = ARGMAX ? argmax_tag(p) : 0u;
 
   float bv[MMAX], bs[MMAX];
   int bi[MMAX];
@@ -574,14 +600,14 @@ void qmv_kernel(const QmvParams p) {
 
   // a wave without tiles (t0 == t1) still takes part in the staging barrier
   const bool has_tiles = t0 < t1;
-  // the LM head's logits of this workgroup's rows (its waves' tile ranges are
+  // the LM head's logits of this workgroup's rows (its waves' row ranges are
   // contiguous), stored after the tile loop
   __shared__ float s_lg[ARGMAX ? kArgLogitsMax : 1];
-  const int lg_t0 = (int)((long long)blockIdx.x * kWaves * p.total_tiles / nw);
-  const int lg_r0 = lg_t0 * Q::RW;
+  const int lg_r0 = ARGMAX ? (int)((long long)blockIdx.x * kWaves * n_rows / nw) : 0;
   float* const lg = ARGMAX ? s_lg : nullptr;
   const typename Q::Offsets o = Q::offsets(p, sub, slot);
   typename Q::Cursor cu = Q::locate(p, has_tiles ? t0 : 0);
+  if constexpr (ARGMAX) cu = typename Q::Cursor{0, 0, wr0, wr1};
   typename Q::Buf A, B;
   typename Q::XRegs xr;
   const f16* xcur = (const f16*)p.mat[cu.j].x + cu.b * p.mat[cu.j].x_bstride;
@@ -661,8 +687,8 @@ void qmv_kernel(const QmvParams p) {
     __syncthreads();
     {
       const QmvMat& mt = p.mat[0];
-      const int lg_t1 = (int)((long long)(blockIdx.x + 1) * kWaves * p.total_tiles / nw);
-      const int rows_x_m = (lg_t1 - lg_t0) * Q::RW * MMAX;
+      const int lg_r1 = (int)((long long)(blockIdx.x + 1) * kWaves * n_rows / nw);
+      const int rows_x_m = (lg_r1 - lg_r0) * MMAX;
       const int cnt = rows_x_m < kArgLogitsMax ? rows_x_m : kArgLogitsMax;
       if (mt.y) {
         const bool yf32 = (p.flags & kFlagYf32) != 0;
@@ -684,9 +710,9 @@ void qmv_kernel(const QmvParams p) {
       int i = li[m][0];
 #pragma unroll
       for (int w = 1; w < kWaves; ++w) argmax_merge(v, i, s, lv[m][w], li[m][w], ls[m][w]);
-      argmax_partial_store(p, (long long)m * p.parts + blockIdx.x, v, i, s);
+      argmax_partial_store(p, (long long)m * p.parts + blockIdx.x, v, i, s, tag);
     }
-    argmax_tail(p);
+    argmax_tail<8>(p, tag);
   }
 }
 

@@ -7,7 +7,7 @@ greedy token is the first maximum of fp16-rounded logits.  AEXQ_EPI_ARGMAX_F16
   * A planted pair of rows whose logits differ in fp32 but round to the same
     fp16 value: the fp16 mode picks the lower index with a top-2 gap of 0, the
     fp32 mode the larger logit; at M = 1 (streaming kernel, in-launch merge),
-    M = 4 (wide MFMA kernel + finalize) and through the logits-then-argmax
+    M = 4 (wide MFMA kernel, in-launch merge) and through the logits-then-argmax
     path (K not a multiple of 16); with fp16 and fp32 logits tensors.
   * The full 151,936-row head at M = 1 and 8 against the first maximum of the
     oracle's logits rounded to fp16, allowing only a logit within the fp32

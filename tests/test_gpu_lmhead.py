@@ -1,6 +1,6 @@
 """The LM head with the argmax fused (Q8 row scales): the streaming kernel at
-M = 1 with the partials merged inside the launch, the wide MFMA kernel at
-M = 2..8 with the finalize launch.  Logits, indices and top-2 gaps against the
+M = 1 and the wide MFMA kernel at M = 2..8, both with the partials merged
+inside the launch by its last workgroup.  Logits, indices and top-2 gaps against the
 oracle (MM:645-686 first-maximum rule) at ragged vocabulary sizes (the last
 tile partly past N, odd N with fp16 row scales), K = 256..1024, fp16 and fp32
 row scales, the tiled Pack4 logits layout, RMSNorm-in at several rows with row
