@@ -51,11 +51,6 @@ struct aexq_ctx {
   int cus = 256;  // compute units of the device
   hipStream_t stream = nullptr;
   // Scratch buffers, grown on demand (capacities in bytes).
-  // argmax partials
-  float* part_best = nullptr;
-  int* part_index = nullptr;
-  float* part_second = nullptr;
-  long long part_best_cap = 0, part_index_cap = 0, part_second_cap = 0;
   float* logits_scratch = nullptr;
   long long logits_cap = 0;
   // RMS-normalised activation rows of the MFMA path
@@ -196,9 +191,6 @@ extern "C" aexq_status aexq_create(int device, void* hip_stream, aexq_ctx** out)
 extern "C" void aexq_destroy(aexq_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
-  (void)hipFree(ctx->part_best);
-  (void)hipFree(ctx->part_index);
-  (void)hipFree(ctx->part_second);
   (void)hipFree(ctx->logits_scratch);
   (void)hipFree(ctx->act_scratch);
   (void)hipFree(ctx->gather_scratch);
@@ -1108,7 +1100,10 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       if (gmode == kG16) wc.nt = nt > 1 ? nt / 2 : 1;  // twice the scales per block
       if (argmax) {
         // the LM head: argmax partials fused, one 16-row block per wave (more,
-        // shorter workgroups over the vocabulary measured faster)
+        // shorter workgroups over the vocabulary measured faster).  The plain
+        // kernel's logits and an argmax launch over them measured no faster
+        // (config 5, M = 8: 46-47 us against 45-47): a second launch costs as
+        // much as the fused form's epilogue and merge.
         wc.argmax = true;
         wc.nt = 1;
       }
@@ -1485,43 +1480,75 @@ extern "C" aexq_status aexq_linear_group(aexq_ctx* ctx, int count, const aexq_we
   return launch_plan(ctx, plan, "aexq_linear_group");
 }
 
-static aexq_status ensure_parts(aexq_ctx* ctx, long long need, const char* op) {
-  aexq_status st = grow_scratch(ctx, (void**)&ctx->part_best, &ctx->part_best_cap,
-                                need * (long long)sizeof(float), op, "argmax partials");
-  if (!st)
-    st = grow_scratch(ctx, (void**)&ctx->part_index, &ctx->part_index_cap,
-                      need * (long long)sizeof(int), op, "argmax partials");
-  if (!st)
-    st = grow_scratch(ctx, (void**)&ctx->part_second, &ctx->part_second_cap,
-                      need * (long long)sizeof(float), op, "argmax partials");
-  return st;
-}
-
-// mode: kLogitsF32, kLogitsF16 (fp16 logits), kLogitsF32AsF16 (fp32 logits
-// compared after rounding to fp16)
-static aexq_status argmax_over_logits(aexq_ctx* ctx, const void* logits, int mode, int m, int n,
-                                      long long rstride, int32_t* argmax, float* gap,
-                                      const char* op) {
-  const int parts = (n + logits_argmax_cols_per_wg() - 1) / logits_argmax_cols_per_wg();
-  aexq_status st = ensure_parts(ctx, (long long)parts * m, op);
-  if (st) return st;
-  hipError_t e = logits_argmax_launch(logits, mode, m, n, rstride, ctx->part_best,
-                                      ctx->part_index, ctx->part_second, parts, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, op, "argmax launch");
-  ArgmaxParams ap{ctx->part_best, ctx->part_index, ctx->part_second, parts, m, argmax, gap};
-  e = argmax_finalize_launch(ap, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, op, "argmax finalize");
-  return AEXQ_OK;
-}
-
-// Where one LM-head launch writes its tagged argmax partials: the context's
-// growing scratch, or a fixed buffer of `cap` words per plane.
+// Where an argmax launch writes its tagged partials: the context's growing
+// scratch, or a fixed buffer of `cap` words per plane.
 struct Partials {
   unsigned long long* tagged = nullptr;  // three planes of `plane` words
   long long plane = 0;
   unsigned* epoch = nullptr;
   long long cap = 0;
 };
+
+// The context's tagged partials for `need` (workgroup, row) entries.
+static aexq_status context_partials(aexq_ctx* ctx, long long need, const char* op, Partials* pt) {
+  aexq_status st = grow_scratch(ctx, (void**)&ctx->am_tagged, &ctx->am_tagged_cap,
+                                3 * need * (long long)sizeof(unsigned long long), op,
+                                "tagged argmax partials", true);
+  if (!st)
+    st = grow_scratch(ctx, (void**)&ctx->am_epoch, &ctx->am_epoch_cap,
+                      kArgEpochInts * (long long)sizeof(unsigned), op, "argmax epoch", true);
+  if (st) return st;
+  pt->tagged = ctx->am_tagged;
+  pt->plane = ctx->am_tagged_cap / (3 * (long long)sizeof(unsigned long long));
+  pt->epoch = ctx->am_epoch;
+  pt->cap = pt->plane;
+  return AEXQ_OK;
+}
+
+static void bind_partials(QmvParams& p, const Partials& pt, int32_t* argmax, float* gap) {
+  p.am_tagged = pt.tagged;
+  p.am_plane = pt.plane;
+  p.am_epoch = pt.epoch;
+  p.am_out = argmax;
+  p.am_gap = gap;
+}
+
+// The argmax (and top-2 gap) of M logits rows in one launch per block of
+// kArgMergeRows rows.  mode: kLogitsF32, kLogitsF16 (fp16 logits),
+// kLogitsF32AsF16 (fp32 logits compared after rounding to fp16).  About one
+// workgroup per CU in all, at least 1024 columns each; 16-byte loads where
+// the rows allow.  AEXQ_ARGMAX_WG_PER_CU overrides the workgroup count (tuning).
+static aexq_status argmax_over_logits(aexq_ctx* ctx, const void* logits, int mode, int m, int n,
+                                      long long rstride, int32_t* argmax, float* gap,
+                                      const char* op) {
+  const int esz = mode == kLogitsF16 ? 2 : 4;
+  const int vec = 16 / esz;
+  const bool vec_ok = ((uintptr_t)logits % 16) == 0 && (rstride * esz) % 16 == 0;
+  long long per_cu = 1;
+  const char* env = getenv("AEXQ_ARGMAX_WG_PER_CU");
+  if (env && atoi(env) > 0) per_cu = atoi(env);
+  for (int m0 = 0; m0 < m; m0 += kArgMergeRows) {
+    const int mb = m - m0 < kArgMergeRows ? m - m0 : kArgMergeRows;
+    long long parts = (per_cu * ctx->cus + mb - 1) / mb;
+    const long long most = (n + 1023) / 1024;
+    if (parts > most) parts = most;
+    if (parts < 1) parts = 1;
+    int cols = (int)((n + parts - 1) / parts);
+    if (vec_ok) cols = (cols + vec - 1) / vec * vec;
+    parts = (n + cols - 1) / cols;
+    Partials pt;
+    aexq_status st = context_partials(ctx, parts * mb, op, &pt);
+    if (st) return st;
+    QmvParams p{};
+    p.m = mb;
+    p.parts = (int)parts;
+    bind_partials(p, pt, argmax + m0, gap ? gap + m0 : nullptr);
+    hipError_t e = logits_argmax_launch((const char*)logits + (long long)m0 * rstride * esz, mode,
+                                        n, rstride, cols, vec_ok ? vec : 1, p, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, op, "argmax launch");
+  }
+  return AEXQ_OK;
+}
 
 static bool lmhead_fused(const Plan& plan) {
   return (plan.fast && plan.entry->cfg.argmax) ||
@@ -1531,8 +1558,8 @@ static bool lmhead_fused(const Plan& plan) {
 // The LM head with the argmax fused into the matvec: M = 1..8 on the
 // streaming kernel, M >= 2 on the wide MFMA kernel (one launch per block of up
 // to 32 rows); one (best, index, second) partial per workgroup and row, merged
-// in the same launch by its last workgroup (no finalize launch).  `fixed`
-// null: the partials go to the context's scratch (grown as needed).
+// in the same launch by its last workgroup.  `fixed` null: the partials go to
+// the context's scratch (grown as needed).
 static aexq_status lmhead_fused_launch(aexq_ctx* ctx, Plan& plan, const char* op,
                                        int32_t* argmax, float* top2_gap, const Partials* fixed) {
   const int M = plan.p.m;
@@ -1552,23 +1579,11 @@ static aexq_status lmhead_fused_launch(aexq_ctx* ctx, Plan& plan, const char* op
                   parts, M, need, fixed->cap);
     pt = *fixed;
   } else {
-    aexq_status st = grow_scratch(ctx, (void**)&ctx->am_tagged, &ctx->am_tagged_cap,
-                                  3 * need * (long long)sizeof(unsigned long long), op,
-                                  "tagged argmax partials", true);
-    if (!st)
-      st = grow_scratch(ctx, (void**)&ctx->am_epoch, &ctx->am_epoch_cap,
-                        kArgEpochInts * (long long)sizeof(unsigned), op, "argmax epoch", true);
+    aexq_status st = context_partials(ctx, need, op, &pt);
     if (st) return st;
-    pt.tagged = ctx->am_tagged;
-    pt.plane = ctx->am_tagged_cap / (3 * (long long)sizeof(unsigned long long));
-    pt.epoch = ctx->am_epoch;
   }
   plan.p.parts = parts;
-  plan.p.am_tagged = pt.tagged;
-  plan.p.am_plane = pt.plane;
-  plan.p.am_epoch = pt.epoch;
-  plan.p.am_out = argmax;
-  plan.p.am_gap = top2_gap;
+  bind_partials(plan.p, pt, argmax, top2_gap);
   if (plan.fast) {
     hipError_t e = qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, op, "lm head launch");

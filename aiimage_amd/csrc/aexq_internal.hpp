@@ -72,13 +72,10 @@ struct QmvParams {
   int gamma_size;
   float eps;
   int flags;
-  // argmax partials (LM head): [m][parts]
-  float* part_best;
-  int* part_index;
-  float* part_second;
+  // argmax partials (LM head): workgroups per row
   int parts;
-  // in-kernel argmax merge (am_tagged null: a separate finalize launch merges
-  // the float partials above).  Every workgroup stores its partial of row r
+  // in-kernel argmax merge (am_tagged non-null for every argmax launch).
+  // Every workgroup stores its partial of row r
   // as three tagged words, tag << 32 | bits of (best, index, second), at
   // am_tagged[plane * am_plane + r * parts + workgroup]; the tag is the
   // launch's epoch, am_epoch[0] + 1 (0 skipped), read by every workgroup at
@@ -109,16 +106,6 @@ struct QmvParams {
 constexpr int kArgMergeRows = 32;
 constexpr int kArgEpochInts = 64;
 constexpr int kArgSpinLimit = 1 << 20;
-
-struct ArgmaxParams {
-  const float* pv;
-  const int* pi;
-  const float* ps;
-  int parts;
-  int m;
-  int32_t* out_index;
-  float* out_gap;
-};
 
 // Streaming kernel registry (instantiated in aexq_qmv_q8.hip / aexq_qmv_q4.hip).
 struct QmvConfig {
@@ -194,12 +181,14 @@ hipError_t generic_launch(int fmt, const QmvParams& p, int grid, hipStream_t str
 hipError_t splitk_reduce_launch(const QmvParams& p, int nw, int q8_scale, int sf16,
                                 hipStream_t stream);
 int generic_rows_per_wg();
-hipError_t argmax_finalize_launch(const ArgmaxParams& a, hipStream_t stream);
 // element type of the logits an argmax pass reads
 enum : int { kLogitsF32 = 0, kLogitsF16 = 1, kLogitsF32AsF16 = 2 };
-hipError_t logits_argmax_launch(const void* logits, int mode, int m, int n, long long rstride,
-                                float* pv, int* pi, float* ps, int parts, hipStream_t stream);
-int logits_argmax_cols_per_wg();
+// Argmax of p.m logits rows (row r at logits + r * rstride elements, n
+// columns) in one launch of p.parts workgroups per row, `cols` columns each,
+// merged in the launch through p's tagged partials into p.am_out / p.am_gap.
+// vec > 1: 16-byte loads (logits, rstride and cols 16-byte aligned).
+hipError_t logits_argmax_launch(const void* logits, int mode, int n, long long rstride, int cols,
+                                int vec, const QmvParams& p, hipStream_t stream);
 // The largest |scale| of `count` scales (fp16 or fp32) as fp32 bits, atomically
 // maxed into *out (which the caller zeroes).
 hipError_t scale_absmax_launch(const void* scales, long long count, int f16, unsigned* out,

@@ -148,67 +148,61 @@ hipError_t rmsnorm_rows_launch(const void* x, int x_f32, long long x_rstride, lo
 }
 
 // ---------------------------------------------------------------------------
-// Argmax over existing fp32 logits rows, and the final merge of partials.
+// Argmax over existing logits rows in one launch: workgroup b takes row
+// b / parts and that row's column slice b % parts, forms the slice's (best,
+// index, second) with the first-maximum rule (MM:645-686), stores it as a
+// tagged partial, and the grid's last workgroup merges every row's partials
+// (argmax_tail).  VEC logits per load (16 bytes when the rows and slices are
+// 16-byte aligned, else 1), kArgmaxLoads loads per thread in flight.
 // ---------------------------------------------------------------------------
-constexpr int kArgmaxCols = 4096;
+constexpr int kArgmaxLoads = 8;
 
-template <typename T, bool ROUND>
+template <typename T, bool ROUND, int VEC>
 __global__ __launch_bounds__(kThreads) void logits_argmax_kernel(const T* logits, int n,
-                                                                 long long rstride, float* pv,
-                                                                 int* pi, float* ps, int parts) {
-  const int m = blockIdx.y, part = blockIdx.x;
-  const int c0 = part * kArgmaxCols;
-  const int c1 = min(n, c0 + kArgmaxCols);
+                                                                 long long rstride, int cols,
+                                                                 const QmvParams p) {
+  const uint32_t tag = argmax_tag(p);
+  const int m = blockIdx.x / p.parts, part = blockIdx.x % p.parts;
+  const int c0 = part * cols;
+  const int c1 = min(n, c0 + cols);
+  const T* row = logits + (long long)m * rstride;
   float bv = __builtin_nanf("");
   int bix = 0x7fffffff;
   float bs = -INFINITY;
-  for (int c = c0 + (int)threadIdx.x; c < c1; c += kThreads) {
-    const float v = (float)logits[(long long)m * rstride + c];
-    argmax_merge(bv, bix, bs, ROUND ? (float)(f16)v : v, c, -INFINITY);
-  }
-  argmax_wave_reduce(bv, bix, bs);
-  __shared__ float sv[kWaves], ss[kWaves];
-  __shared__ int si[kWaves];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) {
-    sv[wave] = bv;
-    si[wave] = bix;
-    ss[wave] = bs;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < kWaves; ++w) argmax_merge(bv, bix, bs, sv[w], si[w], ss[w]);
-    const long long o = (long long)m * parts + part;
-    pv[o] = bv;
-    pi[o] = bix;
-    ps[o] = bs;
-  }
-}
-
-__global__ __launch_bounds__(kThreads) void argmax_finalize_kernel(const ArgmaxParams a) {
-  const int m = blockIdx.x;
-  float bv = __builtin_nanf("");
-  int bix = 0x7fffffff;
-  float bs = -INFINITY;
-  // kFinalizeBatch partials per thread per pass, all loads issued before the
-  // first merge (the merge order is free: it is a total order plus a max)
-  constexpr int kFinalizeBatch = 8;
-  const float* pv = a.pv + (long long)m * a.parts;
-  const int* pi = a.pi + (long long)m * a.parts;
-  const float* ps = a.ps + (long long)m * a.parts;
-  for (int i0 = threadIdx.x; i0 < a.parts; i0 += kThreads * kFinalizeBatch) {
-    float v[kFinalizeBatch], s[kFinalizeBatch];
-    int ix[kFinalizeBatch];
+  auto take = [&](float v, int c) { argmax_merge(bv, bix, bs, ROUND ? (float)(f16)v : v, c, -INFINITY); };
+  constexpr int kStep = kThreads * VEC;
+  for (int c = c0 + (int)threadIdx.x * VEC; c < c1; c += kStep * kArgmaxLoads) {
+    if constexpr (VEC == 1) {
+      float v[kArgmaxLoads];
 #pragma unroll
-    for (int j = 0; j < kFinalizeBatch; ++j) {
-      const int i = i0 + j * kThreads;
-      const bool in = i < a.parts;
-      v[j] = in ? pv[i] : __builtin_nanf("");
-      ix[j] = in ? pi[i] : 0x7fffffff;
-      s[j] = in ? ps[i] : -INFINITY;
+      for (int j = 0; j < kArgmaxLoads; ++j) {
+        const int cj = c + j * kStep;
+        v[j] = cj < c1 ? (float)row[cj] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < kArgmaxLoads; ++j)
+        if (c + j * kStep < c1) take(v[j], c + j * kStep);
+    } else {
+      // whole vectors inside the slice; the row's last partial vector
+      // element by element
+      u32x4 w[kArgmaxLoads];
+#pragma unroll
+      for (int j = 0; j < kArgmaxLoads; ++j) {
+        const int cj = c + j * kStep;
+        w[j] = cj + VEC <= c1 ? *(const u32x4*)(row + cj) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int j = 0; j < kArgmaxLoads; ++j) {
+        const int cj = c + j * kStep;
+        if (cj + VEC <= c1) {
+          const T* e = (const T*)&w[j];
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) take((float)e[i], cj + i);
+        } else {
+          for (int i = 0; cj + i < c1; ++i) take((float)row[cj + i], cj + i);
+        }
+      }
     }
-#pragma unroll
-    for (int j = 0; j < kFinalizeBatch; ++j) argmax_merge(bv, bix, bs, v[j], ix[j], s[j]);
   }
   argmax_wave_reduce(bv, bix, bs);
   __shared__ float sv[kWaves], ss[kWaves];
@@ -222,9 +216,9 @@ __global__ __launch_bounds__(kThreads) void argmax_finalize_kernel(const ArgmaxP
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < kWaves; ++w) argmax_merge(bv, bix, bs, sv[w], si[w], ss[w]);
-    a.out_index[m] = bix == 0x7fffffff ? 0 : bix;
-    if (a.out_gap) a.out_gap[m] = bs == -INFINITY ? INFINITY : bv - bs;
+    argmax_partial_store(p, (long long)m * p.parts + part, bv, bix, bs, tag);
   }
+  argmax_tail<8>(p, tag);
 }
 
 // ---------------------------------------------------------------------------
@@ -417,8 +411,6 @@ hipError_t generic_launch(int fmt, const QmvParams& p, int grid, hipStream_t str
   return hipGetLastError();
 }
 
-int logits_argmax_cols_per_wg() { return kArgmaxCols; }
-
 // ---------------------------------------------------------------------------
 // Largest scale magnitude of a weight (load time): |s| as fp32 bits orders
 // like the value, so one unsigned atomicMax per workgroup after a wave and
@@ -457,22 +449,23 @@ hipError_t scale_absmax_launch(const void* scales, long long count, int f16, uns
   return hipGetLastError();
 }
 
-hipError_t logits_argmax_launch(const void* logits, int mode, int m, int n, long long rstride,
-                                float* pv, int* pi, float* ps, int parts, hipStream_t stream) {
-  if (mode == kLogitsF16)
-    hipLaunchKernelGGL((logits_argmax_kernel<f16, false>), dim3(parts, m), dim3(kThreads), 0,
-                       stream, (const f16*)logits, n, rstride, pv, pi, ps, parts);
-  else if (mode == kLogitsF32AsF16)
-    hipLaunchKernelGGL((logits_argmax_kernel<float, true>), dim3(parts, m), dim3(kThreads), 0,
-                       stream, (const float*)logits, n, rstride, pv, pi, ps, parts);
-  else
-    hipLaunchKernelGGL((logits_argmax_kernel<float, false>), dim3(parts, m), dim3(kThreads), 0,
-                       stream, (const float*)logits, n, rstride, pv, pi, ps, parts);
-  return hipGetLastError();
-}
-
-hipError_t argmax_finalize_launch(const ArgmaxParams& a, hipStream_t stream) {
-  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(a.m), dim3(kThreads), 0, stream, a);
+hipError_t logits_argmax_launch(const void* logits, int mode, int n, long long rstride, int cols,
+                                int vec, const QmvParams& p, hipStream_t stream) {
+  const dim3 grid(p.parts * p.m);
+#define AEXQ_ARGMAX_LAUNCH(T, ROUND, VEC)                                                       \
+  hipLaunchKernelGGL((logits_argmax_kernel<T, ROUND, VEC>), grid, dim3(kThreads), 0, stream,  \
+                     (const T*)logits, n, rstride, cols, p)
+  if (mode == kLogitsF16) {
+    if (vec > 1) AEXQ_ARGMAX_LAUNCH(f16, false, 8);
+    else AEXQ_ARGMAX_LAUNCH(f16, false, 1);
+  } else if (mode == kLogitsF32AsF16) {
+    if (vec > 1) AEXQ_ARGMAX_LAUNCH(float, true, 4);
+    else AEXQ_ARGMAX_LAUNCH(float, true, 1);
+  } else {
+    if (vec > 1) AEXQ_ARGMAX_LAUNCH(float, false, 4);
+    else AEXQ_ARGMAX_LAUNCH(float, false, 1);
+  }
+#undef AEXQ_ARGMAX_LAUNCH
   return hipGetLastError();
 }
 

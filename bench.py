@@ -277,10 +277,10 @@ def extras(torch, aexq, synth, ctx):
         b = n * k + n * 2 + m * k * 2 + m * n * 4
         out[f"config5_lmhead_m{m}"] = {"bytes": b, "ms_per_call": avg,
                                        "GBps": b / (avg * 1e-3) / 1e9,
-                                       "note": ("one launch: matvec, logits and argmax, the "
-                                                "partials merged by the last workgroup" if m == 1
-                                                else "matvec with argmax partials, then the "
-                                                "finalize launch")}
+                                       "note": ("one launch: " + ("streaming matvec" if m == 1
+                                                                  else "MFMA matvec") +
+                                                ", logits and argmax, the tagged partials "
+                                                "merged by the last workgroup")}
     for h in heads:
         h.release()
     return out

@@ -180,3 +180,42 @@ def test_merge_grids_shrink_and_grow(ctx, aexq, orc, monkeypatch, m, k):
         wi, wg = _expect(orc, ref)
         _check(_run(ctx, aexq, w, x16, m, k, noalloc=noalloc), (wi, wg))
     w.release()
+
+
+@pytest.mark.parametrize("dtype,rows,width,packed", [
+    (torch.float32, 40, 151936, False),   # two launches of up to 32 rows, 16-byte loads
+    (torch.float32, 3, 100003, False),    # odd row stride: element loads
+    (torch.float16, 5, 151936, False),    # fp16 logits, 16-byte loads
+    (torch.float16, 2, 4099, True),       # Pack4 rows of 4100 fp16: 8-byte aligned, element loads
+])
+def test_argmax_over_logits_one_launch(ctx, aexq, orc, dtype, rows, width, packed):
+    """aexq_argmax: the argmax launch over existing logits rows merges its
+    partials in the launch too; rows of any stride and count, fp32 or fp16,
+    planted NaN / tie cases in the first rows."""
+    _announce(f"argmax over logits {dtype} rows={rows} width={width} packed={packed}")
+    layout = aexq.LAYOUT_PACK4_LINEAR if packed else aexq.LAYOUT_LINEAR
+    g = torch.Generator(device="cpu").manual_seed(0xAE1E4000 + rows)
+    vals = torch.randn(rows, width, generator=g).to(dtype)
+    vals[0, 0] = float("nan")                          # NaN at index 0 wins row 0
+    if rows > 1:
+        vals[1, 3] = float("nan")                      # NaN elsewhere never wins
+        vals[1, width - 1] = vals[1, width // 2] = 9.0  # tie: the lower index
+    lg = aexq.new_activation(rows, width, dtype, layout)
+    stride = lg.numel() // rows
+    lg.view(rows, stride)[:, :width] = vals.cuda()
+    am = torch.full((rows,), -2, dtype=torch.int32, device="cuda")
+    gap = torch.full((rows,), -2.0, dtype=torch.float32, device="cuda")
+    ctx.argmax(aexq.describe(lg, rows, width, layout), am, gap)
+    torch.cuda.synchronize()
+    ref = vals.float().numpy()
+    want = _expect(orc, ref)
+    got = (am.cpu().numpy(), gap.cpu().numpy())
+    assert np.array_equal(got[0], want[0]), (got[0], want[0])
+    for r in range(rows):
+        if np.isnan(want[1][r]):
+            assert np.isnan(got[1][r])
+        else:
+            assert got[1][r] == np.float32(want[1][r]), (r, got[1][r], want[1][r])
+    assert got[0][0] == 0
+    if rows > 1:
+        assert got[0][1] == width // 2 and got[1][1] == 0.0

@@ -131,7 +131,7 @@ def test_tied_alias_embedding_and_lm_head(ctx, aexq, orc):
 
 # the refused capture below launches nothing, so torch warns that its graph is empty
 @pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
-def test_graph_replays_after_scratch_growth(ctx, aexq, orc):
+def test_graph_replays_after_scratch_growth(ctx, aexq, orc, monkeypatch):
     _announce("graph replay after the context's scratch grows; growth under capture refused")
     from aiimage_amd import _abi, synth
     c2 = aexq.Context(0)
@@ -150,15 +150,18 @@ def test_graph_replays_after_scratch_growth(ctx, aexq, orc):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
             c2.lmhead_argmax(w, aexq.describe(x1, 1, k), None, am1)
-        # an argmax over [64][151936] logits takes 38 partials per row (2432),
-        # more than the M = 1 LM head's one per workgroup: the partial buffers
-        # grow, and the captured graph still names the old ones
+        # an argmax over [64][151936] logits at 32 workgroups per CU takes 149
+        # partials per row, 4768 per launch of 32 rows: more than the M = 1 LM
+        # head's one per workgroup (1024), so the partial buffer grows, and the
+        # captured graph still names the old one
         rows, width = 64, 151936
         lg = torch.randn(rows, width, device="cuda", dtype=torch.float32)
         am64 = torch.zeros(rows, dtype=torch.int32, device="cuda")
+        monkeypatch.setenv("AEXQ_ARGMAX_WG_PER_CU", "32")
         with torch.cuda.stream(stream):
             c2.argmax(aexq.describe(lg.reshape(-1), rows, width), am64)
         stream.synchronize()
+        monkeypatch.delenv("AEXQ_ARGMAX_WG_PER_CU")
         assert np.array_equal(am64.cpu().numpy(), np.argmax(lg.cpu().numpy(), axis=1))
         for i in range(3):
             am1.fill_(-1)
