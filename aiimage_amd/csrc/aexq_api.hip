@@ -1303,14 +1303,19 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     // persistent grid: every wave resident, each owning a contiguous tile range
     // Workgroups queued beyond the resident count stream best: Q4 16 of 4
     // waves per CU (config 2, against 6, 8, 12, 20, 24 and 32), Q8 12 (config
-    // 1, against the resident count, 8 and 16).  Argmax launches stay at the
-    // resident count (config 5, M = 1: 34.0 us against 36.0 at 8 per CU and
-    // 46.5 at 16): their waves split the vocabulary by rows, and queued
-    // workgroups would each pay the prologue and the partial store.
+    // 1, against the resident count, 8 and 16).  Argmax launches take two
+    // workgroups per CU, fewer than the resident four (config 5, M = 1: 33.9
+    // us against 34.1-34.4 at four, 36.0 at 8 and 46.5 at 16): their waves
+    // split the vocabulary by rows, and every workgroup pays its prologue and
+    // partial store.
     int per_cu = qmv_blocks_per_cu(plan->entry);
     const bool fused_argmax = plan->entry->cfg.argmax;
-    const int queued = fused_argmax ? per_cu : (fmt == kQ4 ? 16 : 12);
-    if (per_cu < queued) per_cu = queued;
+    if (fused_argmax) {
+      if (per_cu > 2) per_cu = 2;
+    } else {
+      const int queued = fmt == kQ4 ? 16 : 12;
+      if (per_cu < queued) per_cu = queued;
+    }
     const char* env = getenv("AEXQ_QMV_BLOCKS_PER_CU");
     if (env && atoi(env) > 0) per_cu = atoi(env);
     const long long need = ((long long)tiles_total + kWaves - 1) / kWaves;

@@ -67,6 +67,22 @@
 
 namespace aexq {
 
+// Phase timing (built only with -DAEXQ_STEP_STAMPS, the instrumented library
+// bench.py --decode-phases loads): the store wave of every workgroup records
+// s_memrealtime (100 MHz) when its compute waves have finished a phase and
+// again after the phase's workgroup barrier, 10 stamps per layer, into
+// g_step_stamps[(layer * 10 + k) * grid + workgroup] (layers < 64, grid <= 256);
+// aexq_step_stamps copies them out.  The store wave only stores, so the stamps
+// add no wait to any role.
+#ifdef AEXQ_STEP_STAMPS
+__device__ unsigned long long g_step_stamps[64 * 10 * 256];
+#define AEXQ_STAMP(l, k, lane, b)                                                          \
+  if ((lane) == 0 && (l) < 64)                                                             \
+  g_step_stamps[((l) * 10 + (k)) * gridDim.x + (b)] = __builtin_amdgcn_s_memrealtime()
+#else
+#define AEXQ_STAMP(l, k, lane, b) ((void)0)
+#endif
+
 namespace {
 
 constexpr int kSt = kStepThreads;
@@ -842,11 +858,13 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       // P1: q/k/v rows
       {
         sw_wait(&s_done, done_target, err, broken);
+        AEXQ_STAMP(l, 0, lane, b);
         const int r0 = b * p.rows_qkv;
         const int n = nqkv - r0 < p.rows_qkv ? nqkv - r0 : p.rows_qkv;
         if (n > 0) sw_copy(p.qkv_t + r0, s_out, n, lane);
       }
       __syncthreads();
+      AEXQ_STAMP(l, 1, lane, b);
       // P2: the K/V append, the split partials, the merged attention slice
       {
         if (has_new) {
@@ -857,6 +875,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
           vc[lane] = ((const uint32_t*)s_vn)[lane];
         }
         sw_wait(&s_done, done_target, err, broken);
+        AEXQ_STAMP(l, 2, lane, b);
         if (attn_wg) {
 #pragma unroll
           for (int h = 0; h < GQ; ++h)
@@ -870,25 +889,31 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         }
       }
       __syncthreads();
+      AEXQ_STAMP(l, 3, lane, b);
       // P3: rows after attention
       {
         sw_wait(&s_done, done_target, err, broken);
+        AEXQ_STAMP(l, 4, lane, b);
         const int r0 = b * p.rows_hid;
         const int n = hid - r0 < p.rows_hid ? hid - r0 : p.rows_hid;
         if (n > 0) sw_copy(p.xb_t + r0, s_out, n, lane);
       }
       __syncthreads();
+      AEXQ_STAMP(l, 5, lane, b);
       // P4: SwiGLU rows
       {
         sw_wait(&s_done, done_target, err, broken);
+        AEXQ_STAMP(l, 6, lane, b);
         const int r0 = b * p.rows_inter;
         const int n = inter - r0 < p.rows_inter ? inter - r0 : p.rows_inter;
         if (n > 0) sw_copy(p.h_t + r0, s_out, n, lane);
       }
       __syncthreads();
+      AEXQ_STAMP(l, 7, lane, b);
       // P5: the layer's output rows (and the step's output after the last layer)
       {
         sw_wait(&s_done, done_target, err, broken);
+        AEXQ_STAMP(l, 8, lane, b);
         const int r0 = b * p.rows_hid;
         const int n = hid - r0 < p.rows_hid ? hid - r0 : p.rows_hid;
         if (n > 0) {
@@ -898,6 +923,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         }
       }
       __syncthreads();
+      AEXQ_STAMP(l, 9, lane, b);
     }
     if (b == 0 && lane == 0) st_word(p.epoch, e0 + 6u * (uint32_t)nl);
   } else {
@@ -1071,6 +1097,15 @@ hipError_t decode_layers_occupancy(int fmt, int gmode, int* per_cu) {
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, AEXQ_STEP_Q4(kG16), kSt, 0);
   return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, AEXQ_STEP_Q4(kG32), kSt, 0);
 }
+
+#ifdef AEXQ_STEP_STAMPS
+// The phase stamps of the last launch (n words) into host memory.
+extern "C" int aexq_step_stamps(void* host, long long n) {
+  if (n > 64LL * 10 * 256) n = 64LL * 10 * 256;
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_step_stamps), (size_t)n * 8, 0,
+                                  hipMemcpyDeviceToHost);
+}
+#endif
 
 hipError_t decode_layers_launch(const StepParams& p, int grid, hipStream_t stream) {
   const int ce = p.fmt == kQ8 ? 16 : 32;

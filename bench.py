@@ -60,6 +60,9 @@ def parse():
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the config-3 decode step timing and print its JSON (for "
                          "profiling that step); not the benchmark line")
+    ap.add_argument("--decode-phases", action="store_true",
+                    help="per-phase times of the fused decode step from the phase-stamped "
+                         "library (aiimage_amd/libaexq_stamps.so; built if missing)")
     ap.add_argument("--config4-only", action="store_true",
                     help="run only the config-4 timings (M in {16, 64, 512}, Q4 and Q8; batched "
                          "copies and single layers) and print their JSON (for profiling those "
@@ -645,6 +648,66 @@ def cpu_baseline(seconds: float):
     return out
 
 
+def decode_phases(torch, steps: int = 10):
+    """Per-phase times of the fused decode step (config 3 shapes, 2048 cached
+    positions) for the benchmark's Q4 and the reference's Q4-g16 and Q8
+    formats, from the phase-stamped build of the library: per workgroup and
+    layer, the compute time of each phase (barrier to the compute waves' last
+    output) and its hand-over (to the next workgroup barrier, which waits for
+    the grid's outputs the next phase polls); medians over workgroups and
+    layers 1..L-1 (layer 0 includes the launch prologue)."""
+    import ctypes
+    import numpy as np
+    from aiimage_amd import _abi, build as hip_build
+    if not os.path.exists(hip_build.LIB_STAMPS):
+        hip_build.build(stamps=True)
+    lib = _abi.load(hip_build.LIB_STAMPS)
+    lib.aexq_step_stamps.argtypes = [ctypes.c_void_p, ctypes.c_longlong]
+    from aiimage_amd import aexq, decoder
+    ctx = aexq.Context(0)
+    names = ["P1 q/k/v", "P2 attention splits + split merge", "P3 o_proj + residual",
+             "P4 gate/up + SwiGLU", "P5 down + residual"]
+    out = {"library": os.path.basename(hip_build.LIB_STAMPS), "formats": {}}
+    for mk in (decoder.ModelConfig, decoder.ModelConfig.reference_q4,
+               decoder.ModelConfig.reference_q8):
+        cfg = mk()
+        sess = decoder.DecodeSession(ctx, cfg, fused=True)
+        grid = sess.fused.info()["workgroups"]
+        sess.token.fill_(1)
+        sess.set_position(cfg.capacity - 1)
+        for _ in range(3):
+            sess.step(check=False)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            sess.step(check=False)
+        e1.record()
+        torch.cuda.synchronize()
+        sess.check_fused()
+        n = cfg.layers * 10 * grid
+        buf = (ctypes.c_ulonglong * n)()
+        if lib.aexq_step_stamps(buf, n) != 0:
+            raise RuntimeError("aexq_step_stamps failed")
+        st = np.frombuffer(buf, dtype=np.uint64).astype(np.int64).reshape(cfg.layers, 10, grid) * 10
+        rows = []
+        for ph in range(5):
+            prev = st[:-1, 9, :] if ph == 0 else st[1:, 2 * ph - 1, :]
+            comp = (st[1:, 2 * ph, :] - prev) / 1e3
+            hand = (st[1:, 2 * ph + 1, :] - st[1:, 2 * ph, :]) / 1e3
+            rows.append({"phase": names[ph], "compute_us": round(float(np.median(comp)), 2),
+                         "compute_us_p90": round(float(np.percentile(comp, 90)), 2),
+                         "handover_us": round(float(np.median(hand)), 2),
+                         "handover_us_p90": round(float(np.percentile(hand, 90)), 2)})
+        layer = np.diff(st[:, 9, :], axis=0) / 1e3
+        out["formats"][cfg.format_name] = {
+            "ms_per_step_eager": round(e0.elapsed_time(e1) / steps, 4), "workgroups": grid,
+            "layers": cfg.layers, "layer_us": round(float(np.median(layer)), 2), "phases": rows}
+        del sess
+        torch.cuda.synchronize()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -654,6 +717,12 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.decode_phases:
+        if not torch.cuda.is_available():
+            print("bench.py needs a GPU", file=sys.stderr)
+            sys.exit(2)
+        print(json.dumps(decode_phases(torch)), flush=True)
+        return
     from aiimage_amd import aexq, synth
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
