@@ -150,14 +150,12 @@ __device__ __forceinline__ void argmax_wave_reduce(float& bv, int& bi, float& bs
 // previous merging launch left, plus one, never 0 (the words of a scratch
 // buffer start at tag 0).  Every workgroup reads it before its partial store;
 // the merging workgroup stores it back only after every partial of the launch
-// carries it, so the whole grid reads the same value.  The word changes only
-// between launches (stored through at the previous launch's end, and launch
-// boundaries write back and invalidate the caches), so a plain load reads it:
-// agent-coherent loads of one word by the whole grid queue on its line (a
-// 1024-workgroup argmax launch measured 10.9 us with them).
+// carries it, so the whole grid reads the same value.  An agent-coherent
+// load: the previous launch's last workgroup, on any XCD, stored the word, and
+// another XCD's L2 may still hold the line from an earlier read.
 __device__ __forceinline__ uint32_t argmax_tag(const QmvParams& p) {
   if (!p.am_tagged) return 0;
-  const uint32_t e = *p.am_epoch;
+  const uint32_t e = __hip_atomic_load(p.am_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return e == 0xffffffffu ? 1u : e + 1u;
 }
 
