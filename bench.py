@@ -277,9 +277,20 @@ def extras(torch, aexq, synth, ctx):
         for _ in range(8):
             call()
         avg, med = time_launches(torch, call, 24)
+        # the same calls back to back between one pair of events (as a decode
+        # loop issues the LM head behind the layer kernel): no per-call event gap
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(24):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        stream_ms = e0.elapsed_time(e1) / 24
         b = n * k + n * 2 + m * k * 2 + m * n * 4
         out[f"config5_lmhead_m{m}"] = {"bytes": b, "ms_per_call": avg,
                                        "GBps": b / (avg * 1e-3) / 1e9,
+                                       "ms_per_call_back_to_back": stream_ms,
+                                       "GBps_back_to_back": b / (stream_ms * 1e-3) / 1e9,
                                        "note": ("one launch: " + ("streaming matvec" if m == 1
                                                                   else "MFMA matvec") +
                                                 ", logits and argmax, the tagged partials "
