@@ -687,8 +687,13 @@ static aexq_status view_tensor(const aexq_tensor* t, const char* op, const char*
   if (t->dtype != AEXQ_DTYPE_F16 && t->dtype != AEXQ_DTYPE_F32)
     return fail(AEXQ_ERR_UNSUPPORTED, op, "%s dtype=%d | rejectedFallback=dtype", name, t->dtype);
   const aexq_shape& L = t->logical;
-  const int W = L.w > 1 ? L.w : 1;
-  const int H = L.dims >= 2 ? (L.h > 1 ? L.h : 1) : 1;
+  // an empty matrix (no columns, or no rows of a 2-D shape) is refused, never
+  // launched as one row
+  if (L.dims < 1 || L.w <= 0 || (L.dims >= 2 && L.h <= 0))
+    return fail(AEXQ_ERR_SHAPE, op, "%s logical {%d,%d,%d,%d,%d} is empty", name, L.dims, L.w,
+                L.h, L.d, L.c);
+  const int W = L.w;
+  const int H = L.dims >= 2 ? L.h : 1;
   v->rows = H;
   v->width = W;
   v->dtype = t->dtype;

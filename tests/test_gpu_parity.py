@@ -367,6 +367,20 @@ def test_strict_plan_rejects_without_fallback(ctx, aexq):
     with pytest.raises(_abi.ArgumentError):       # Q8 direct upload with block != K
         ctx.weight(aexq.QuantizedTensor(n * k, 256, words, scales, bits=8), n, k)
     assert "one scale per output channel" in _abi.last_error()
+    # empty matrices (no rows, no columns) are refused before anything launches
+    no_rows = aexq.describe(x, 1, k)
+    no_rows.logical = _abi.Shape(2, k, 0, 1, 1)
+    no_cols = aexq.describe(y, 1, n, aexq.LAYOUT_PACK4_LINEAR)
+    no_cols.logical = _abi.Shape(2, 0, 1, 1, 1)
+    am = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+    for call in (lambda: ctx.linear(w, no_rows, yd), lambda: ctx.linear(w, xd, no_cols),
+                 lambda: ctx.lmhead_argmax(w, no_rows, None, am),
+                 lambda: ctx.argmax(no_cols, am)):
+        with pytest.raises(_abi.InvalidOperationError):
+            call()
+        assert "is empty" in _abi.last_error()
+    torch.cuda.synchronize()
+    assert int(am.item()) == -7
 
 
 # ------------------------------------------------------------------ LM head + argmax
