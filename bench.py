@@ -63,6 +63,9 @@ def parse():
     ap.add_argument("--decode-phases", action="store_true",
                     help="per-phase times of the fused decode step from the phase-stamped "
                          "library (aiimage_amd/libaexq_stamps.so; built if missing)")
+    ap.add_argument("--lmhead-only", action="store_true",
+                    help="config 5 only (the LM head with the fused argmax, M = 1 and 8) and "
+                         "the logits-only matvec of the same head")
     ap.add_argument("--config4-only", action="store_true",
                     help="run only the config-4 timings (M in {16, 64, 512}, Q4 and Q8; batched "
                          "copies and single layers) and print their JSON (for profiling those "
@@ -257,7 +260,17 @@ def extras(torch, aexq, synth, ctx):
                                       "GBps": copies * bytes1 / (avg * 1e-3) / 1e9}
     stack.release()
     del y
-    # config 5: LM head Q8 K=1024 N=151936 with fused argmax, M=1 and M=8.
+    out.update(config5(torch, aexq, synth, ctx))
+    return out
+
+
+def config5(torch, aexq, synth, ctx, plain: bool = False):
+    """Config 5: the LM head (Q8 per-row, K=1024, N=151,936) with the argmax
+    fused, M = 1 and 8, eight rotated copies so every call is cold; each call
+    between its own events and the same calls back to back.  plain: also the
+    logits-only matvec of the same head (fp16 logits, no argmax) for
+    comparison."""
+    out = {}
     n, k = synth.VOCAB, synth.HIDDEN
     words, scales, _ = synth.q8_weights(n, k, synth.SEED_BASE + 5)
     heads = [ctx.weight(aexq.QuantizedTensor(n * k, k, words, scales, bits=8), n, k)
@@ -295,6 +308,24 @@ def extras(torch, aexq, synth, ctx):
                                                                   else "MFMA matvec") +
                                                 ", logits and argmax, the tagged partials "
                                                 "merged by the last workgroup")}
+    if plain:
+        for m in (1, 8):
+            xm = torch.as_tensor(synth.activations(m, k, 9)).cuda()
+            xmd = aexq.describe(xm, m, k)
+            y16 = aexq.new_activation(m, n, torch.float16, aexq.LAYOUT_PACK4_LINEAR)
+            yd = aexq.describe(y16, m, n, aexq.LAYOUT_PACK4_LINEAR)
+            it = [0]
+
+            def lin():
+                ctx.linear(heads[it[0] % 8], xmd, yd)
+                it[0] += 1
+            for _ in range(8):
+                lin()
+            avg, _ = time_launches(torch, lin, 24)
+            b = n * k + n * 2 + m * k * 2 + m * n * 2
+            out[f"config5_plain_matvec_m{m}"] = {"bytes": b, "ms_per_call": avg,
+                                                 "GBps": b / (avg * 1e-3) / 1e9,
+                                                 "note": "logits only (fp16), no argmax"}
     for h in heads:
         h.release()
     return out
@@ -741,6 +772,9 @@ def main():
     ctx = aexq.Context(0)
     if args.decode_only:
         print(json.dumps(config3(torch, aexq, ctx, steps=max(args.steps, 10))), flush=True)
+        return
+    if args.lmhead_only:
+        print(json.dumps(config5(torch, aexq, synth, ctx, plain=True)), flush=True)
         return
     if args.config4_only:
         res = config4(torch, aexq, synth, ctx)
