@@ -14,6 +14,7 @@
 
 #include "../../include/aexq.h"
 #include "aexq_internal.hpp"
+#include "aexq_step.hpp"
 
 using namespace aexq;
 
@@ -1990,8 +1991,8 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
   if (grid < hkv || splits < 1 || sp > kStepMaxSplitPos || merge < 1 || merge > kStepMaxMerge ||
       kStepHeadDim % merge || merge * grid != hq * kStepHeadDim || merge % 8 ||
       splits * (merge / 8) > 64 || rq > 4 * kStepComputeWaves || rh > kStepComputeWaves ||
-      ri > 4 * kStepComputeWaves || rq > kStepOutWords || ri > kStepOutWords ||
-      (hq / hkv) * kStepPartStride > kStepOutWords)
+      ri > 4 * kStepComputeWaves || rq > kStepOutWords || ri > kStepOutWords || rq > 64 ||
+      ri > 64 || rh < 1 || merge > 64 || (hq / hkv) * kStepPartStride > kStepOutWords)
     return fail(AEXQ_ERR_UNSUPPORTED, op,
                 "capacity=%d on %d workgroups: %d splits of %d positions, %d merged dims, rows "
                 "%d/%d/%d per workgroup | rejectedFallback=per-operator step",
@@ -2019,14 +2020,21 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
     table[l].kc = (uint16_t*)L.k_cache;
     table[l].vc = (uint16_t*)L.v_cache;
   }
-  const long long words[8] = {hid, qw + 2 * kvw, (long long)hq * splits * kStepPartStride, qw, hid,
-                              inter, 1, 1};
+  // the polled vectors in kStepReplicas copies of whole 4 KB pages each, every
+  // buffer on a 4 KB boundary (the allocation is over-sized by a page to align)
+  const int rs[8] = {step_replica_stride(hid), step_replica_stride(qw + 2 * kvw), 0,
+                     step_replica_stride(qw), step_replica_stride(hid), step_replica_stride(inter),
+                     0, 0};
+  const long long words[8] = {(long long)kStepReplicas * rs[0], (long long)kStepReplicas * rs[1],
+                              (long long)hq * splits * kStepPartStride,
+                              (long long)kStepReplicas * rs[3], (long long)kStepReplicas * rs[4],
+                              (long long)kStepReplicas * rs[5], 1, 1};
   long long off[9];
-  off[0] = round_up((long long)count * sizeof(StepLayer), 256);
-  for (int i = 0; i < 8; ++i) off[i + 1] = off[i] + round_up(words[i] * 4, 256);
+  off[0] = round_up((long long)count * sizeof(StepLayer), 4096);
+  for (int i = 0; i < 8; ++i) off[i + 1] = off[i] + round_up(words[i] * 4, 4096);
   aexq_decoder* d = new aexq_decoder();
-  hipError_t e = hipMalloc(&d->mem, (size_t)off[8]);
-  if (e == hipSuccess) e = hipMemset(d->mem, 0, (size_t)off[8]);
+  hipError_t e = hipMalloc(&d->mem, (size_t)off[8] + 4096);
+  if (e == hipSuccess) e = hipMemset(d->mem, 0, (size_t)off[8] + 4096);
   if (e == hipSuccess)
     e = hipMemcpy(d->mem, table.data(), (size_t)count * sizeof(StepLayer), hipMemcpyHostToDevice);
   if (e != hipSuccess) {
@@ -2034,9 +2042,12 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
     delete d;
     return hip_fail(e, op, "decoder buffers");
   }
-  char* base = (char*)d->mem;
+  // the layer table at the allocation's start; the buffers at offsets from its
+  // first 4 KB boundary (off[0] >= the table's bytes, so they never overlap it)
+  char* const table_at = (char*)d->mem;
+  char* const base = (char*)(uintptr_t)round_up((long long)(uintptr_t)table_at, 4096);
   StepParams& p = d->p;
-  p.layers = (const StepLayer*)base;
+  p.layers = (const StepLayer*)table_at;
   p.nlayers = count;
   p.hidden = hid;
   p.qw = qw;
@@ -2062,6 +2073,11 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
   p.attn_t = (uint32_t*)(base + off[3]);
   p.xb_t = (uint32_t*)(base + off[4]);
   p.h_t = (uint32_t*)(base + off[5]);
+  p.xa_rs = rs[0];
+  p.qkv_rs = rs[1];
+  p.attn_rs = rs[3];
+  p.xb_rs = rs[4];
+  p.h_rs = rs[5];
   p.epoch = (uint32_t*)(base + off[6]);
   p.err = (int*)(base + off[7]);
   p.rows_qkv = rq;

@@ -28,7 +28,12 @@
 // rewritten in every layer, so a stale word is at most a few epochs old and
 // never carries the current tag.  Each phase reads all of its predecessor's
 // outputs, or (P2a, P2b) those of its kv head, so a buffer is never
-// rewritten while a slower workgroup still reads it.  Spins are bounded: a
+// rewritten while a slower workgroup still reads it.  The vectors that every
+// workgroup polls (q/k/v, the merged attention, x after attention, the SwiGLU
+// output, the layer output) are written in kStepReplicas copies on separate
+// 4 KB pages and workgroup b polls copy b % kStepReplicas: a grid polling one
+// 4-14 KB vector otherwise meets on the few memory channels holding it, and
+// its polls delay the producers' stores there.  Spins are bounded: a
 // wait that exceeds kSpinLimit sets the error word and gives up (the launch
 // still ends; the host reports the error).
 //
@@ -64,6 +69,7 @@
 #include <math.h>
 
 #include "aexq_device.hpp"
+#include "aexq_step.hpp"
 
 namespace aexq {
 
@@ -367,6 +373,30 @@ __device__ __forceinline__ void sw_wait_count(int* ctr, int target, int* err, bo
 // Store wave: n tagged words from LDS to device memory.
 __device__ __forceinline__ void sw_copy(uint32_t* dst, const uint32_t* src, int n, int lane) {
   for (int i = lane; i < n; i += 64) st_word(dst + i, src[i]);
+}
+// The store wave's lanes over (copy, word) pairs of a replicated vector for a
+// workgroup's n <= 64 words of one phase: a store instruction covers 64 / n
+// copies.  Computed once per launch (it divides).
+struct RepLanes {
+  int copy;  // the lane's first copy
+  int word;  // the lane's word (64: none)
+  int step;  // copies per store instruction
+};
+__device__ __forceinline__ RepLanes rep_lanes(int n, int lane) {
+  RepLanes m;
+  m.step = 64 / n;
+  m.copy = lane / n;
+  m.word = m.copy < m.step ? lane - m.copy * n : 64;
+  return m;
+}
+// Store wave: n tagged words from LDS into every copy of a replicated vector
+// (copies `stride` words apart).
+__device__ __forceinline__ void sw_copy_rep(uint32_t* dst, int stride, const uint32_t* src, int n,
+                                            const RepLanes& m) {
+  if (m.word < n) {
+    const uint32_t v = src[m.word];
+    for (int r = m.copy; r < kStepReplicas; r += m.step) st_word(dst + r * stride + m.word, v);
+  }
 }
 
 // Scale words a lane holds per row slot: one per row (Q8), one per 32-code
@@ -853,6 +883,8 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
   } else if (store) {
     __syncthreads();
     const int lane = opaque_tid() & 63;
+    const RepLanes rl_qkv = rep_lanes(p.rows_qkv, lane), rl_attn = rep_lanes(per, lane),
+                   rl_hid = rep_lanes(p.rows_hid, lane), rl_inter = rep_lanes(p.rows_inter, lane);
     for (int l = 0; l < nl; ++l) {
       const StepLayer& L = s_layers[l];
       // P1: q/k/v rows
@@ -861,7 +893,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         AEXQ_STAMP(l, 0, lane, b);
         const int r0 = b * p.rows_qkv;
         const int n = nqkv - r0 < p.rows_qkv ? nqkv - r0 : p.rows_qkv;
-        if (n > 0) sw_copy(p.qkv_t + r0, s_out, n, lane);
+        if (n > 0) sw_copy_rep(p.qkv_t + r0, p.qkv_rs, s_out, n, rl_qkv);
       }
       __syncthreads();
       AEXQ_STAMP(l, 1, lane, b);
@@ -885,7 +917,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         if (mwg) {
           merge_target += 1;
           sw_wait_count(&s_merge, merge_target, err, broken);
-          sw_copy(p.attn_t + mh * kHd + md0, s_mout, per, lane);
+          sw_copy_rep(p.attn_t + mh * kHd + md0, p.attn_rs, s_mout, per, rl_attn);
         }
       }
       __syncthreads();
@@ -896,7 +928,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         AEXQ_STAMP(l, 4, lane, b);
         const int r0 = b * p.rows_hid;
         const int n = hid - r0 < p.rows_hid ? hid - r0 : p.rows_hid;
-        if (n > 0) sw_copy(p.xb_t + r0, s_out, n, lane);
+        if (n > 0) sw_copy_rep(p.xb_t + r0, p.xb_rs, s_out, n, rl_hid);
       }
       __syncthreads();
       AEXQ_STAMP(l, 5, lane, b);
@@ -906,7 +938,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         AEXQ_STAMP(l, 6, lane, b);
         const int r0 = b * p.rows_inter;
         const int n = inter - r0 < p.rows_inter ? inter - r0 : p.rows_inter;
-        if (n > 0) sw_copy(p.h_t + r0, s_out, n, lane);
+        if (n > 0) sw_copy_rep(p.h_t + r0, p.h_rs, s_out, n, rl_inter);
       }
       __syncthreads();
       AEXQ_STAMP(l, 7, lane, b);
@@ -917,7 +949,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         const int r0 = b * p.rows_hid;
         const int n = hid - r0 < p.rows_hid ? hid - r0 : p.rows_hid;
         if (n > 0) {
-          sw_copy(p.xa_t + r0, s_out, n, lane);
+          sw_copy_rep(p.xa_t + r0, p.xa_rs, s_out, n, rl_hid);
           if (l + 1 == nl)
             for (int i = lane; i < n; i += 64) p.out[r0 + i] = (uint16_t)(s_out[i] & 0xffffu);
         }
@@ -928,6 +960,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
     if (b == 0 && lane == 0) st_word(p.epoch, e0 + 6u * (uint32_t)nl);
   } else {
     const int lane = opaque_tid() & 63;
+    const int rc = b % kStepReplicas;  // the copy of every polled vector this workgroup reads
     if (pw == 0) {
       f32x4 g[4];
       pw_gamma_issue(lds_ptr(&s_layers[0].g_attn), hid, g, lane);
@@ -957,7 +990,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         for (int i = 0; i < NQ; ++i) off[i] = ag * GQ * kHd + (lane + 64 * i) * 4;
         off[NQ] = lane < 32 ? qw + ag * kHd + lane * 4 : qw + kvw + ag * kHd + (lane - 32) * 4;
         u32x4 v[NQ + 1];
-        pw_wait<NQ + 1>(p.qkv_t, nqkv, off, tg, 16, 0xffffu, v, err, broken);
+        pw_wait<NQ + 1>(p.qkv_t + rc * p.qkv_rs, nqkv, off, tg, 16, 0xffffu, v, err, broken);
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
           uint32_t a, c;
@@ -1046,11 +1079,12 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         cw_signal(&s_merge, lane);
       }
       // the attention output of the whole grid (the merges of every workgroup)
-      pw_vec_pairs<kStepMaxQ / 256 / kPW, kPairs>(p.attn_t, qw, tg + 2, s_at, lane, pw, err, broken);
+      pw_vec_pairs<kStepMaxQ / 256 / kPW, kPairs>(p.attn_t + rc * p.attn_rs, qw, tg + 2, s_at, lane,
+                                                  pw, err, broken);
       __syncthreads();
       // during P3: x after attention and its RMSNorm-in; the next layer's gamma
       if (pw == 0) {
-        pw_vec_plain<kStepMaxHidden / 256>(p.xb_t, hid, tg + 3, s_xb, lane, err, broken);
+        pw_vec_plain<kStepMaxHidden / 256>(p.xb_t + rc * p.xb_rs, hid, tg + 3, s_xb, lane, err, broken);
         __asm__ volatile("" ::: "memory");
         pw_rms<kPairs>(s_xb, s_gm, s_xn, hid, p.eps, lane);
       } else if (l + 1 < nl) {
@@ -1060,12 +1094,12 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       }
       __syncthreads();
       // during P4: the SwiGLU output
-      pw_vec_pairs<kStepMaxInter / 256 / kPW, kPairs>(p.h_t, inter, tg + 4, s_h, lane, pw, err,
-                                                      broken);
+      pw_vec_pairs<kStepMaxInter / 256 / kPW, kPairs>(p.h_t + rc * p.h_rs, inter, tg + 4, s_h, lane,
+                                                      pw, err, broken);
       __syncthreads();
       // during P5: the next layer's input and its RMSNorm-in
       if (pw == 0 && l + 1 < nl) {
-        pw_vec_plain<kStepMaxHidden / 256>(p.xa_t, hid, tg + 5, s_xa, lane, err, broken);
+        pw_vec_plain<kStepMaxHidden / 256>(p.xa_t + rc * p.xa_rs, hid, tg + 5, s_xa, lane, err, broken);
         __asm__ volatile("" ::: "memory");
         pw_rms<kPairs>(s_xa, s_ga, s_xn, hid, p.eps, lane);
       }
