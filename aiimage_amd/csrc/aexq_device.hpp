@@ -84,17 +84,43 @@ __device__ __forceinline__ float dpp(float v) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// DPP broadcast across rows into the rows enabled in ROWS (the others read
+// `old`): row_bcast:15 (0x142) gives rows 1 and 3 lane 15 of rows 0 and 2,
+// row_bcast:31 (0x143) gives rows 2 and 3 lane 31.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_rows(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, v), CTRL,
+                                                               ROWS, 0xF, false));
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
 // Sum over aligned groups of LPR lanes (16, 32 or 64); every lane of a group
 // receives the group total.  Within a 16-lane DPP row: rotate by 8 and 4, then
-// quad swaps; across rows: lane shuffles.
+// quad swaps.  Across rows (no LDS round trip): rows 1 and 3 add lane 15 of
+// rows 0 and 2 by row_bcast:15, rows 2 and 3 then add lane 31 by row_bcast:31,
+// and the totals are read from lanes 31 and 63.  Lane 63 holds
+// (S3 + S2) + (S1 + S0) for row sums S0..S3, the same value (addition
+// commutes) as the pairwise (S0 + S1) + (S2 + S3) of a butterfly.  Needs every
+// lane active, like the row steps.
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
   v += dpp<0x128>(v);  // row_ror:8
   v += dpp<0x124>(v);  // row_ror:4
   v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
-  if constexpr (LPR >= 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (LPR >= 64) v += __shfl_xor(v, 32, 64);
+  if constexpr (LPR >= 32) {
+    v += dpp_rows<0x142, 0xA>(0.0f, v);  // rows 1, 3: S1 + S0, S3 + S2
+    if constexpr (LPR == 32) {
+      const float lo = lane_value(v, 31), hi = lane_value(v, 63);
+      return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) < 32 ? lo : hi;
+    } else {
+      v += dpp_rows<0x143, 0xC>(0.0f, v);  // row 3: (S3 + S2) + (S1 + S0)
+      return lane_value(v, 63);
+    }
+  }
   return v;
 }
 
@@ -106,8 +132,9 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<0x124>(v));  // row_ror:4
   v = fmaxf(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]
   v = fmaxf(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  v = fmaxf(v, dpp_rows<0x142, 0xA>(v, v));
+  v = fmaxf(v, dpp_rows<0x143, 0xC>(v, v));
+  return lane_value(v, 63);
 }
 
 // Argmax order of the reference scan (MM:645-686: element 0 first, then any

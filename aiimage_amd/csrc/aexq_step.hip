@@ -13,7 +13,8 @@
 //                                    positions: scores, softmax statistics,
 //                                    P.V partials
 //   P2b split merge                  (q head, slice of dims) per workgroup, on
-//                                    the poll wave that received the partials
+//                                    the poll wave that received the partials,
+//                                    which also stores the merged slice
 //   P3  o_proj + residual            rows of Wo
 //   P4  gate/up + SwiGLU             rows of the gate/up pair
 //   P5  down + residual              rows of Wdown
@@ -51,8 +52,9 @@
 // share one vector-memory counter, which counts in issue order and, once both
 // kinds are in flight, makes any wait a wait for everything: so the compute
 // waves issue only loads (a use of a register loaded two phases ago waits for
-// exactly that load), the poll waves only loads, and the store wave only
-// stores.
+// exactly that load) and the store wave only stores.  The poll waves load,
+// and the merging one also stores its merged slice: its next wait is for its
+// next poll, which waits for everything before it in any case.
 //
 // The layer weights are Q4 with one scale per 32 codes (the benchmark's
 // format), Q4 with one per 16 (the reference's shipping archives, Q8A:116-139)
@@ -108,6 +110,12 @@ constexpr int kNoOff = 0x7ffffff0;
 
 __device__ __forceinline__ void st_word(uint32_t* p, uint32_t w) {
   __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 bytes of tagged words at byte offset `off` of the buffer `rs`, written
+// with the same agent coherence as st_word; every word carries its own tag, so
+// a reader never needs the four words to land together.
+__device__ __forceinline__ void st_quad(__amdgpu_buffer_rsrc_t rs, int off, const u32x4& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kCoh);
 }
 __device__ __forceinline__ uint32_t ld_word(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -356,24 +364,6 @@ __device__ __forceinline__ void sw_wait(int* ctr, int& target, int* err, bool& b
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
-// Store wave: waits until the LDS counter reaches target.
-__device__ __forceinline__ void sw_wait_count(int* ctr, int target, int* err, bool& broken) {
-  for (int spin = 0;; ++spin) {
-    if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target || broken)
-      break;
-    if (spin >= kSpinLimit) {
-      atomicOr(err, 1);
-      broken = true;
-      break;
-    }
-    __builtin_amdgcn_s_sleep(0);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-// Store wave: n tagged words from LDS to device memory.
-__device__ __forceinline__ void sw_copy(uint32_t* dst, const uint32_t* src, int n, int lane) {
-  for (int i = lane; i < n; i += 64) st_word(dst + i, src[i]);
-}
 // The store wave's lanes over (copy, word) pairs of a replicated vector for a
 // workgroup's n <= 64 words of one phase: a store instruction covers 64 / n
 // copies.  Computed once per launch (it divides).
@@ -575,8 +565,6 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
   __shared__ StepLayer s_layers[kStepMaxLayers];        // the layer table
   __shared__ __align__(16) uint32_t s_out[kStepOutWords];  // this phase's tagged outputs
   __shared__ int s_done;                               // compute waves done with s_out
-  __shared__ __align__(16) uint32_t s_mout[kStepMaxMerge];  // the merged attention slice
-  __shared__ int s_merge;                              // merges written to s_mout
   __shared__ int s_cbar;
   __shared__ uint32_t s_e0;
 
@@ -593,7 +581,6 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
   bool broken = false;
   int cbar_target = 0;
   int done_target = 0;
-  int merge_target = 0;
 
   int pos = *p.pos;
   pos = pos < 0 ? 0 : (pos >= p.cap ? p.cap - 1 : pos);
@@ -682,7 +669,6 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
     if (threadIdx.x == 0) {
       s_cbar = 0;
       s_done = 0;
-      s_merge = 0;
       s_e0 = ld_word(p.epoch);
     }
   }
@@ -883,8 +869,8 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
   } else if (store) {
     __syncthreads();
     const int lane = opaque_tid() & 63;
-    const RepLanes rl_qkv = rep_lanes(p.rows_qkv, lane), rl_attn = rep_lanes(per, lane),
-                   rl_hid = rep_lanes(p.rows_hid, lane), rl_inter = rep_lanes(p.rows_inter, lane);
+    const RepLanes rl_qkv = rep_lanes(p.rows_qkv, lane), rl_hid = rep_lanes(p.rows_hid, lane),
+                   rl_inter = rep_lanes(p.rows_inter, lane);
     for (int l = 0; l < nl; ++l) {
       const StepLayer& L = s_layers[l];
       // P1: q/k/v rows
@@ -908,16 +894,17 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         }
         sw_wait(&s_done, done_target, err, broken);
         AEXQ_STAMP(l, 2, lane, b);
-        if (attn_wg) {
+        if (attn_wg && lane < kStepPartStride / 4) {
+          // the split's partial of each head, 16 bytes a lane: every LDS read
+          // first, then the stores (one LDS round trip)
+          u32x4 pv[GQ];
+#pragma unroll
+          for (int h = 0; h < GQ; ++h) pv[h] = *(const u32x4*)(s_out + h * kStepPartStride + 4 * lane);
+          const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+              (void*)p.part_t, (short)0, p.hq * S * kStepPartStride * 4, kBufferRsrcWord3);
 #pragma unroll
           for (int h = 0; h < GQ; ++h)
-            sw_copy(p.part_t + ((long long)(ag * GQ + h) * S + as) * kStepPartStride,
-                    s_out + h * kStepPartStride, kStepPartStride, lane);
-        }
-        if (mwg) {
-          merge_target += 1;
-          sw_wait_count(&s_merge, merge_target, err, broken);
-          sw_copy_rep(p.attn_t + mh * kHd + md0, p.attn_rs, s_mout, per, rl_attn);
+            st_quad(pr, (((ag * GQ + h) * S + as) * kStepPartStride + 4 * lane) * 4, pv[h]);
         }
       }
       __syncthreads();
@@ -1028,23 +1015,23 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         pw_gamma_store(gm, s_gm, hid, lane);
       } else if (mwg) {
         // the split merge of (q head mh, dims md0 .. md0 + per), MM:420-544's
-        // softmax over all positions: lane = split s = lane / lps, dims
-        // md0 + 8 (lane % lps) .. + 8; the split's first lane also reads its
-        // (max, sum) header
-        const int lps = per / 8, s = lane / lps, q8 = lane % lps;
+        // softmax over all positions: lps groups of 8 dims, each held by
+        // sl = 64 / lps lanes, lane = group q8 * sl + split s; every lane
+        // reads its split's (max, sum) header.  A group's lanes sum over the
+        // splits with group_sum (no LDS round trip), and its first
+        // kStepReplicas lanes write the merged 8 dims into the copies of the
+        // attention output themselves.
+        static_assert(kStepReplicas <= 16, "a group has at least 16 lanes");
+        const int lps = per / 8, sl = 64 / lps, q8 = lane / sl, s = lane % sl;
         const bool in = s < S;
         const int rb = (mh * S + (in ? s : 0)) * kStepPartStride;
         int off[3] = {in ? rb + 4 + md0 + 8 * q8 : -1, in ? rb + 4 + md0 + 8 * q8 + 4 : -1,
-                      in && q8 == 0 ? rb : -1};
+                      in ? rb : -1};
         u32x4 v[3];
         pw_wait<3>(p.part_t, p.hq * S * kStepPartStride, off, tg + 1, 0, 0xffu, v, err, broken);
-        // the split's (max, sum) to all its lanes; absent splits are neutral
-        float ms = __shfl(as_f32(v[2][0] & ~0xffu), lane - q8, 64);
-        float ls = __shfl(as_f32(v[2][1] & ~0xffu), lane - q8, 64);
-        if (!in) {
-          ms = kNegBig;
-          ls = 0.0f;
-        }
+        // absent splits are neutral
+        const float ms = in ? as_f32(v[2][0] & ~0xffu) : kNegBig;
+        const float ls = in ? as_f32(v[2][1] & ~0xffu) : 0.0f;
         const float M = wave_max(ms);
         const float f = __expf(ms - M);
         const float lsum = wave_sum(q8 == 0 ? ls * f : 0.0f);
@@ -1054,29 +1041,30 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
           a[e] = in ? as_f32(v[0][e] & ~0xffu) * f : 0.0f;
           a[4 + e] = in ? as_f32(v[1][e] & ~0xffu) * f : 0.0f;
         }
-        // the sum over splits (lanes lps apart): rotations within each row of
-        // 16 lanes by DPP, then the four rows
+        if (sl == 64) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float x = a[e];
-          if (lps == 1) x += dppf<0x121>(x);  // row_ror:1
-          if (lps <= 2) x += dppf<0x122>(x);  // row_ror:2
-          if (lps <= 4) x += dppf<0x124>(x);  // row_ror:4
-          if (lps <= 8) x += dppf<0x128>(x);  // row_ror:8
-          a[e] = x;
+          for (int e = 0; e < 8; ++e) a[e] = group_sum<64>(a[e]);
+        } else if (sl == 32) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[e] = group_sum<32>(a[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[e] = group_sum<16>(a[e]);
         }
-        if (lps <= 16) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) a[e] += __shfl_xor(a[e], 16, 64);
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] += __shfl_xor(a[e], 32, 64);
-        if (lane < lps) {
+        if (s < kStepReplicas) {
           const float inv_l = 1.0f / fmaxf(lsum, 1e-20f);
+          u32x4 w0, w1;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) s_mout[8 * q8 + e] = tag_f16((f16)(a[e] * inv_l), tg + 2);
+          for (int e = 0; e < 4; ++e) {
+            w0[e] = tag_f16((f16)(a[e] * inv_l), tg + 2);
+            w1[e] = tag_f16((f16)(a[4 + e] * inv_l), tg + 2);
+          }
+          const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+              (void*)p.attn_t, (short)0, kStepReplicas * p.attn_rs * 4, kBufferRsrcWord3);
+          const int o = (s * p.attn_rs + mh * kHd + md0 + 8 * q8) * 4;
+          st_quad(ar, o, w0);
+          st_quad(ar, o + 16, w1);
         }
-        cw_signal(&s_merge, lane);
       }
       // the attention output of the whole grid (the merges of every workgroup)
       pw_vec_pairs<kStepMaxQ / 256 / kPW, kPairs>(p.attn_t + rc * p.attn_rs, qw, tg + 2, s_at, lane,
