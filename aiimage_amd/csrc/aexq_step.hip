@@ -42,8 +42,9 @@
 // the compute waves run phase p, the poll waves wait for phase p's outputs of
 // the whole grid (the inputs of phase p + 1) and leave them in LDS, ready at
 // the next workgroup barrier; they also do the work between a poll and the
-// next linear: RMSNorm-in (bit-exact with the streaming kernel's staged path),
-// RoPE of q and the new k row, and the RMSNorm gammas.  The compute waves load
+// next linear: RMSNorm-in (bit-exact with the streaming kernel's staged path,
+// split between the two waves), RoPE of q and the new k row, the split merge
+// and the RMSNorm gammas.  The compute waves load
 // each phase's weights (and the split's cached K/V rows) one to three phases
 // ahead into registers, issuing them at the start of a phase so that the
 // grid-wide burst drains while they compute, before the phase's outputs are
@@ -60,12 +61,14 @@
 // format), Q4 with one per 16 (the reference's shipping archives, Q8A:116-139)
 // or Q8 with one scale per row (Q8A:94-114), scales fp16 or fp32; the format
 // is a template parameter of the kernel.  Arithmetic of the linears follows
-// the streaming kernel (aexq_qmv.hpp) for the same format and shapes (lanes
-// per row, chunks per lane): the same RMSNorm-in
+// the streaming kernel (aexq_qmv.hpp) for the same format: the same RMSNorm-in
 // (sums of squares over 8-element slices, DPP wave sums, four partials in
 // order; fp16(x * inv * gamma)), the same per-chunk dot-product order and
-// group-scale fmaf, the same DPP row reduction and epilogue, so each linear's
-// outputs are bit-identical to those of aexq_linear at M = 1.  Attention
+// group-scale fmaf, the same DPP row reduction and epilogue.  q/k/v, gate/up
+// and down use the streaming kernel's lanes per row and chunks per lane, so
+// their outputs are bit-identical to those of aexq_linear at M = 1; o_proj
+// takes 64 lanes per row (one row per wave, eight waves busy instead of four
+// at half the chunks per lane), so its sums are grouped differently.  Attention
 // follows MM:420-544 (scale, max-subtracted softmax, sum floored at 1e-20)
 // with positions split over workgroups and waves.
 #include <math.h>
@@ -148,6 +151,16 @@ __device__ __forceinline__ int opaque_tid() {
   __asm__ volatile("" : "+v"(t));
   return t;
 }
+// The compute waves' thread index.  Q4: the plain index, so the per-lane
+// offsets of every prefetch are computed once and held across the layer loop
+// (the kernels then take 157-165 VGPRs): each phase's loads issue without
+// their address arithmetic, which is what delays a wave's start on its dot
+// products.  Q8: hidden, since its twice-wider weight registers leave no room
+// for the offsets (they would spill).
+template <int FMT>
+__device__ __forceinline__ int cw_tid() {
+  return FMT == kQ8 ? opaque_tid() : (int)threadIdx.x;
+}
 
 // A pointer of the layer table staged in LDS, made wave-uniform (SGPRs): the
 // buffer resources built from it need no waterfall loop, and reading it
@@ -193,27 +206,6 @@ __device__ __forceinline__ void pw_wait(const uint32_t* src, int words, const in
 __device__ __forceinline__ void halves(const u32x4& v, uint32_t& a, uint32_t& b) {
   a = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);
   b = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
-}
-
-// Poll wave: a tagged fp16 vector of `count` words (count % 4 == 0, count <=
-// 256 * NV) into dst in plain order.
-template <int NV>
-__device__ __forceinline__ void pw_vec_plain(const uint32_t* src, int count, uint32_t tag, f16* dst,
-                                             int lane, int* err, bool& broken) {
-  int off[NV];
-#pragma unroll
-  for (int i = 0; i < NV; ++i) off[i] = (lane + 64 * i) * 4 < count ? (lane + 64 * i) * 4 : -1;
-  u32x4 v[NV];
-  pw_wait<NV>(src, count, off, tag, 16, 0xffffu, v, err, broken);
-#pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (off[i] >= 0) {
-      uint32_t a, b;
-      halves(v[i], a, b);
-      uint32_t* d = (uint32_t*)(dst + off[i]);
-      d[0] = a;
-      d[1] = b;
-    }
 }
 
 // Poll wave pw of kPW: its share of a tagged fp16 vector of `count` words
@@ -292,6 +284,100 @@ __device__ __forceinline__ void pw_rms(const f16* x, const float* gamma, f16* ou
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const f16x2 h = as_h2(xv[v][e]);
+        const float a = (float)h[0] * inv, b = (float)h[1] * inv;
+        const f16x2 r = {(f16)(a * g[2 * e]), (f16)(b * g[2 * e + 1])};
+        o[e] = as_u(r);
+      }
+      uint32_t xp[4];
+      if constexpr (PAIRS) {
+        q4_xpairs(o[0], o[1], o[2], o[3], xp);
+      } else {
+        xp[0] = o[0];
+        xp[1] = o[1];
+        xp[2] = o[2];
+        xp[3] = o[3];
+      }
+      *(u32x4*)(out + e0) = u32x4{xp[0], xp[1], xp[2], xp[3]};
+    }
+  }
+}
+
+// Both poll waves: the tagged fp16 vector of k <= 1024 words at src into
+// plain (LDS, plain order) and its RMSNorm-in into out (LDS, nibble-pair order
+// for Q4 weights), the two waves splitting pw_rms's work: wave pw polls,
+// squares and normalises the 8-element slices (lane + 64 v) of v = pw and
+// pw + 2, and the four wave sums meet in s_part, where both waves add them in
+// pw_rms's order, so the result is bit-exact with it.  `count` is the LDS
+// counter the two waves meet on; `target` advances by 2 per call.
+template <bool PAIRS>
+__device__ __forceinline__ void pw_vec_rms2(const uint32_t* src, int k, uint32_t tag, f16* plain,
+                                            const float* gamma, f16* out, float eps, int lane,
+                                            int pw, float* s_part, int* count, int& target,
+                                            int* err, bool& broken) {
+  int off[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e0 = (lane + 64 * (pw + 2 * j)) * 8;
+    off[2 * j] = e0 < k ? e0 : -1;
+    off[2 * j + 1] = e0 < k ? e0 + 4 : -1;
+  }
+  u32x4 t[4];
+  pw_wait<4>(src, k, off, tag, 16, 0xffffu, t, err, broken);
+  u32x4 xv[2];
+  float part[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    xv[j] = u32x4{0u, 0u, 0u, 0u};
+    if (off[2 * j] >= 0) {
+      uint32_t a, b, c, d;
+      halves(t[2 * j], a, b);
+      halves(t[2 * j + 1], c, d);
+      xv[j] = u32x4{a, b, c, d};
+      *(u32x4*)(plain + off[2 * j]) = xv[j];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const f16x2 h = as_h2(xv[j][e]);
+      const float a = (float)h[0], b = (float)h[1];
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+    part[j] = wave_sum(ss);
+  }
+  if (lane == 0) {
+    s_part[pw] = part[0];
+    s_part[pw + 2] = part[1];
+  }
+  target += 2;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if (lane == 0) __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  for (int spin = 0;; ++spin) {
+    if (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target || broken)
+      break;
+    if (spin >= kSpinLimit) {
+      atomicOr(err, 1);
+      broken = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(0);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  float tot = 0.0f;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) tot += s_part[v];
+  const float inv = rsqrtf(fmaxf(tot / (float)k + eps, 1e-20f));
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e0 = off[2 * j];
+    if (e0 >= 0) {
+      const f32x4 g0 = *(const f32x4*)(gamma + e0);
+      const f32x4 g1 = *(const f32x4*)(gamma + e0 + 4);
+      const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 h = as_h2(xv[j][e]);
         const float a = (float)h[0] * inv, b = (float)h[1] * inv;
         const f16x2 r = {(f16)(a * g[2 * e]), (f16)(b * g[2 * e + 1])};
         o[e] = as_u(r);
@@ -521,6 +607,78 @@ __device__ __forceinline__ float row_dot(const u32x4 (&w)[CPL],
   return v;
 }
 
+// row_dot of a gate/up pair of row slots against one read of the activation
+// chunks: each row's sums in row_dot's order (bit-identical to two row_dots).
+template <int LPR, int CPL, int FMT, int GM>
+__device__ __forceinline__ void row_dot2(const u32x4 (&w)[2][CPL],
+                                         const uint32_t (&s)[2][slot_scales<FMT, GM, CPL>()],
+                                         const f16* xl, int chunks, int row, bool sf16, int t,
+                                         float& out0, float& out1) {
+  const int sub = (t & 63) % LPR;
+  const int sb = sf16 ? 2 : 4;
+  constexpr int XW = FMT == kQ8 ? 8 : 16;  // activation dwords per chunk
+  float acc[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ci = sub + c * LPR;
+    uint32_t xr[XW];
+    if (ci < chunks) {
+      const u32x4* src = (const u32x4*)(xl + ci * (2 * XW));
+#pragma unroll
+      for (int v = 0; v < XW / 4; ++v) {
+        const u32x4 t4 = src[v];
+        xr[4 * v + 0] = t4[0];
+        xr[4 * v + 1] = t4[1];
+        xr[4 * v + 2] = t4[2];
+        xr[4 * v + 3] = t4[3];
+      }
+    } else {
+#pragma unroll
+      for (int d = 0; d < XW; ++d) xr[d] = 0u;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if constexpr (FMT == kQ8) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          uint32_t lo, hi;
+          q8_pairs(w[h][c][d], lo, hi);
+          acc[h] = dot2(hi, xr[2 * d + 1], dot2(lo, xr[2 * d], acc[h]));
+        }
+      } else {
+        constexpr int SPC = GM == kG16 ? 2 : 1;
+        float part[SPC];
+#pragma unroll
+        for (int g = 0; g < SPC; ++g) part[g] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          uint32_t q[4];
+          q4_pairs(w[h][c][d], q);
+          const int g = GM == kG16 ? (d >> 1) : 0;
+          float tt = part[g];
+          tt = dot2(q[0], xr[4 * d + 0], tt);
+          tt = dot2(q[1], xr[4 * d + 1], tt);
+          tt = dot2(q[2], xr[4 * d + 2], tt);
+          tt = dot2(q[3], xr[4 * d + 3], tt);
+          part[g] = tt;
+        }
+#pragma unroll
+        for (int g = 0; g < SPC; ++g)
+          acc[h] = fmaf(part[g],
+                        scale_at(s[h][SPC * c + g], (row * SPC * chunks + SPC * ci + g) * sb, sf16),
+                        acc[h]);
+      }
+    }
+  }
+  float v0 = group_sum<LPR>(acc[0]), v1 = group_sum<LPR>(acc[1]);
+  if constexpr (FMT == kQ8) {
+    v0 *= scale_at(s[0][0], row * sb, sf16);
+    v1 *= scale_at(s[1][0], row * sb, sf16);
+  }
+  out0 = v0;
+  out1 = v1;
+}
+
 // Rows of one phase for this workgroup and compute wave: [row0 + wave * slots, +slots).
 struct WaveRows {
   int r0;     // first row of the wave (in the phase's row space)
@@ -566,6 +724,8 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
   __shared__ __align__(16) uint32_t s_out[kStepOutWords];  // this phase's tagged outputs
   __shared__ int s_done;                               // compute waves done with s_out
   __shared__ int s_cbar;
+  __shared__ float s_rpart[4];                         // the RMSNorm's four wave sums
+  __shared__ int s_rms;                                // RMSNorm halves done (both poll waves)
   __shared__ uint32_t s_e0;
 
   const int b = blockIdx.x;
@@ -668,6 +828,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       ((uint32_t*)s_layers)[i] = ((const uint32_t*)p.layers)[i];
     if (threadIdx.x == 0) {
       s_cbar = 0;
+      s_rms = 0;
       s_done = 0;
       s_e0 = ld_word(p.epoch);
     }
@@ -681,7 +842,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
   // the compiler's vector-memory wait counts of each role exact.
   if (compute) {
     {
-      const int t = opaque_tid();
+      const int t = cw_tid<FMT>();
       issue_qkv(0, t);
       issue_kv(0, t, true, true);
     }
@@ -691,7 +852,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       const uint32_t tg = e0 + 1 + 6u * (uint32_t)l;  // tags of P1..P5 are tg .. tg + 5
       // ---------------- P1: q/k/v
       {
-        const int t = opaque_tid(), lane = t & 63;
+        const int t = cw_tid<FMT>(), lane = t & 63;
         issue_o(l, t);
         if constexpr (FMT != kQ8) issue_d(l, t);
         if (w1.live) {
@@ -708,7 +869,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       __syncthreads();
       // ---------------- P2: attention splits
       {
-        const int t = opaque_tid(), lane = t & 63, wave = t >> 6;
+        const int t = cw_tid<FMT>(), lane = t & 63, wave = t >> 6;
         issue_gu(l, t);
         if (attn_wg) {
           const int pl = t >> 3, j = t & 7;  // position pl of the split, dims 16 j .. 16 j + 15
@@ -817,7 +978,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       __syncthreads();
       // ---------------- P3: o_proj + residual
       {
-        const int t = opaque_tid(), lane = t & 63;
+        const int t = cw_tid<FMT>(), lane = t & 63;
         if constexpr (FMT == kQ8) {
           issue_d(l, t);
         } else {
@@ -834,17 +995,17 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       __syncthreads();
       // ---------------- P4: gate/up + SwiGLU-out
       {
-        const int t = opaque_tid(), lane = t & 63;
+        const int t = cw_tid<FMT>(), lane = t & 63;
         if constexpr (FMT == kQ8) {
           if (l + 1 < nl) issue_qkv(l + 1, t);
         }
         if (l + 1 < nl) issue_kv(l + 1, t, true, false);
         if (w4.live) {
           const int row = w4.r0 + lane / L1;
-          const float g =
-              0.0f + row_dot<L1, C1, FMT, GM>(wgu.w[0], wgu.s[0], s_xn, ch1, row, sf16, t);
-          const float u =
-              0.0f + row_dot<L1, C1, FMT, GM>(wgu.w[1], wgu.s[1], s_xn, ch1, row, sf16, t);
+          float g, u;
+          row_dot2<L1, C1, FMT, GM>(wgu.w, wgu.s, s_xn, ch1, row, sf16, t, g, u);
+          g += 0.0f;
+          u += 0.0f;
           const float v = silu(g) * u;
           if (lane % L1 == 0 && row < inter)
             s_out[row - b * p.rows_inter] = tag_f16((f16)v, tg + 4);
@@ -854,7 +1015,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       __syncthreads();
       // ---------------- P5: down + residual
       {
-        const int t = opaque_tid(), lane = t & 63;
+        const int t = cw_tid<FMT>(), lane = t & 63;
         if (l + 1 < nl) issue_kv(l + 1, t, false, true);
         if (w5.live) {
           const int row = w5.r0 + lane / L3;
@@ -948,6 +1109,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
   } else {
     const int lane = opaque_tid() & 63;
     const int rc = b % kStepReplicas;  // the copy of every polled vector this workgroup reads
+    int rms_target = 0;
     if (pw == 0) {
       f32x4 g[4];
       pw_gamma_issue(lds_ptr(&s_layers[0].g_attn), hid, g, lane);
@@ -1070,38 +1232,35 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       pw_vec_pairs<kStepMaxQ / 256 / kPW, kPairs>(p.attn_t + rc * p.attn_rs, qw, tg + 2, s_at, lane,
                                                   pw, err, broken);
       __syncthreads();
-      // during P3: x after attention and its RMSNorm-in; the next layer's gamma
-      if (pw == 0) {
-        pw_vec_plain<kStepMaxHidden / 256>(p.xb_t + rc * p.xb_rs, hid, tg + 3, s_xb, lane, err, broken);
-        __asm__ volatile("" ::: "memory");
-        pw_rms<kPairs>(s_xb, s_gm, s_xn, hid, p.eps, lane);
-      } else if (l + 1 < nl) {
+      // during P3: x after attention and its RMSNorm-in (both poll waves); the
+      // next layer's gamma
+      if (pw == 1 && l + 1 < nl) {
         f32x4 ga[4];
         pw_gamma_issue(lds_ptr(&s_layers[l + 1].g_attn), hid, ga, lane);
         pw_gamma_store(ga, s_ga, hid, lane);
       }
+      pw_vec_rms2<kPairs>(p.xb_t + rc * p.xb_rs, hid, tg + 3, s_xb, s_gm, s_xn, p.eps, lane, pw,
+                          s_rpart, &s_rms, rms_target, err, broken);
       __syncthreads();
       // during P4: the SwiGLU output
       pw_vec_pairs<kStepMaxInter / 256 / kPW, kPairs>(p.h_t + rc * p.h_rs, inter, tg + 4, s_h, lane,
                                                       pw, err, broken);
       __syncthreads();
-      // during P5: the next layer's input and its RMSNorm-in
-      if (pw == 0 && l + 1 < nl) {
-        pw_vec_plain<kStepMaxHidden / 256>(p.xa_t + rc * p.xa_rs, hid, tg + 5, s_xa, lane, err, broken);
-        __asm__ volatile("" ::: "memory");
-        pw_rms<kPairs>(s_xa, s_ga, s_xn, hid, p.eps, lane);
-      }
+      // during P5: the next layer's input and its RMSNorm-in (both poll waves)
+      if (l + 1 < nl)
+        pw_vec_rms2<kPairs>(p.xa_t + rc * p.xa_rs, hid, tg + 5, s_xa, s_ga, s_xn, p.eps, lane, pw,
+                            s_rpart, &s_rms, rms_target, err, broken);
       __syncthreads();
     }
   }
 }
 
-// The instantiations: Q4 (groups of 32 or 16) at the streaming kernel's
-// shapes for rows of 17..32 / 33..64 / 65..128 chunks (16 x 2, 32 x 2, 64 x 2
-// lanes x chunks), Q8 at those for 33..64 / 65..128 / 129..256 chunks (16 x 4,
-// 32 x 4, 64 x 4), four q heads per kv head.
-#define AEXQ_STEP_Q4(GM) decode_layers_kernel<kQ4, GM, 4, 16, 2, 32, 2, 64, 2>
-#define AEXQ_STEP_Q8 decode_layers_kernel<kQ8, kGRow, 4, 16, 4, 32, 4, 64, 4>
+// The instantiations (lanes x chunks per row of the hidden-width, q-width and
+// intermediate-width inputs): Q4 (groups of 32 or 16) for rows of 17..32 /
+// 33..64 / 65..128 chunks, 16 x 2, 64 x 1, 64 x 2; Q8 for 33..64 / 65..128 /
+// 129..256 chunks, 16 x 4, 64 x 2, 64 x 4; four q heads per kv head.
+#define AEXQ_STEP_Q4(GM) decode_layers_kernel<kQ4, GM, 4, 16, 2, 64, 1, 64, 2>
+#define AEXQ_STEP_Q8 decode_layers_kernel<kQ8, kGRow, 4, 16, 4, 64, 2, 64, 4>
 
 bool decode_layers_supported(int fmt, int gmode, int gq, int ch1, int ch2, int ch3) {
   if (gq != 4) return false;
