@@ -375,10 +375,15 @@ class DecodeSession:
         if advance:
             ctx.decode_advance(self.pos, self.token, self.next_token, self.history)
 
-    def capture(self, warmup: int = 2, advance: bool = False) -> torch.cuda.CUDAGraph:
-        """Captures step(advance) into a HIP graph on a side stream.  The warm-up
-        steps (which do not advance) size the context's scratch first, so
-        nothing allocates while capturing."""
+    def capture(self, warmup: int = 2, advance: bool = False, steps: int = 1) -> torch.cuda.CUDAGraph:
+        """Captures `steps` consecutive step(advance) calls into one HIP graph on
+        a side stream (with `advance` each step feeds its argmax to the next on
+        the device, so a replay decodes `steps` tokens; a graph launch costs the
+        device about 8 us of idle time between replays, which this spreads over
+        the steps).  The warm-up steps (which do not advance) size the context's
+        scratch first, so nothing allocates while capturing."""
+        if steps < 1:
+            raise ValueError(f"steps={steps}")
         stream = torch.cuda.Stream()
         old = self.ctx.stream
         self.ctx.set_stream(stream)
@@ -391,29 +396,33 @@ class DecodeSession:
             self.check_fused()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
-                self.step(advance=advance, check=False)
+                for _ in range(steps):
+                    self.step(advance=advance, check=False)
         finally:
             self.ctx.set_stream(old)
         torch.cuda.synchronize()
         return g
 
     def generate(self, start_token: int, position: int, count: int,
-                 graph: torch.cuda.CUDAGraph = None) -> list:
+                 graph: torch.cuda.CUDAGraph = None, graph_steps: int = 1) -> list:
         """Greedy decoding of `count` tokens from `start_token` at `position`
         (Qwen35DecoderSession.Generate, DEC:1160-1237): each step's argmax is the
-        next step's input.  With `graph` (from capture(advance=True)) every
-        token is one replay of the same graph; otherwise eager steps.  Returns
-        the generated token ids."""
+        next step's input.  With `graph` (from capture(advance=True,
+        steps=graph_steps)) each replay decodes graph_steps tokens and the
+        remainder of count runs as eager steps; otherwise every token is an
+        eager step.  Returns the generated token ids."""
+        if graph_steps < 1:
+            raise ValueError(f"graph_steps={graph_steps}")
         if count < 0 or position + count > self.cfg.capacity:
             raise ValueError(f"{count} tokens from position {position} exceed the cache "
                              f"capacity {self.cfg.capacity}")
         self.token.fill_(start_token)
         self.set_position(position)
-        for _ in range(count):
-            if graph is not None:
-                graph.replay()
-            else:
-                self.step(advance=True, check=False)
+        replays = count // graph_steps if graph is not None else 0
+        for _ in range(replays):
+            graph.replay()
+        for _ in range(count - replays * graph_steps):
+            self.step(advance=True, check=False)
         torch.cuda.synchronize()
         self.check_fused()
         self.position = position + count

@@ -476,7 +476,10 @@ def config3(torch, aexq, ctx, steps: int = 30):
     one (every decoder layer in one persistent launch, aexq_decoder_run) and
     the per-operator one (five launches per layer); each eager, as a replayed
     HIP graph, and as the Generate loop (one graph per token that feeds the
-    argmax back and advances the device position)."""
+    argmax back and advances the device position).  The fused form also as
+    graphs of 8 steps (a graph launch leaves the device idle for about 8 us
+    between replays): the same step replayed, and the Generate loop decoding 8
+    tokens per replay."""
     from aiimage_amd import decoder
     cfg = decoder.ModelConfig()
     t0 = time.time()
@@ -492,7 +495,7 @@ def config3(torch, aexq, ctx, steps: int = 30):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps
 
-    def measure():
+    def measure(multi=False):
         sess.token.fill_(1)
         sess.set_position(cfg.capacity - 1)     # attends over all 2048 positions
         for _ in range(2):
@@ -513,13 +516,41 @@ def config3(torch, aexq, ctx, steps: int = 30):
         gen_ms = timed(ga.replay)
         assert int(sess.pos.item()) == cfg.capacity
         del g, ga
-        return eager_ms, graph_ms, gen_ms, start
+        if not multi:
+            return eager_ms, graph_ms, gen_ms, start, None, None
+        # 8 steps per graph: the same step (4 replays, 32 steps), and 8 tokens
+        # per replay of the Generate loop over the same last 24 positions
+        g8 = sess.capture(steps=8)
+        sess.token.fill_(1)
+        sess.set_position(cfg.capacity - 1)
+        g8.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(4):
+            g8.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        graph8_ms = e0.elapsed_time(e1) / 32
+        ga8 = sess.capture(advance=True, steps=8)
+        sess.generate(1, cfg.capacity - 48, 16, graph=ga8, graph_steps=8)   # warm replays
+        sess.token.fill_(1)
+        sess.set_position(cfg.capacity - 24)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(3):
+            ga8.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        gen8_ms = e0.elapsed_time(e1) / 24
+        assert int(sess.pos.item()) == cfg.capacity
+        del g8, ga8
+        return eager_ms, graph_ms, gen_ms, start, graph8_ms, gen8_ms
 
-    eager_ms, graph_ms, gen_ms, start = measure()
+    eager_ms, graph_ms, gen_ms, start, graph8_ms, gen8_ms = measure(multi=True)
     err = sess.fused.error()
     assert err == 0, "the fused step gave up a bounded wait"
     keep, sess.fused = sess.fused, None
-    p_eager, p_graph, p_gen, _ = measure()
+    p_eager, p_graph, p_gen, _, _, _ = measure()
     sess.fused = keep
     b = cfg.bytes_per_token(cfg.capacity)
     roof = HBM_PEAK_GBS * 1e9 / b["total"]
@@ -534,6 +565,9 @@ def config3(torch, aexq, ctx, steps: int = 30):
         "tokens_per_s_eager": tps(eager_ms), "ms_per_token_eager": round(eager_ms, 4),
         "tokens_per_s_generate": tps(gen_ms), "ms_per_token_generate": round(gen_ms, 4),
         "generate_positions": [start, cfg.capacity - 1],
+        "tokens_per_s_graph8": tps(graph8_ms), "ms_per_token_graph8": round(graph8_ms, 4),
+        "tokens_per_s_generate8": tps(gen8_ms), "ms_per_token_generate8": round(gen8_ms, 4),
+        "generate8_positions": [cfg.capacity - 24, cfg.capacity - 1],
         "generate_frac_of_roofline": round(b_gen / (gen_ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
         "bytes_per_token": b, "roofline_tokens_per_s": round(roof, 1),
         "roofline_tokens_per_s_8kv_heads": round(roof8, 1),

@@ -4,8 +4,9 @@
     the reference root, DEC = Packages/com.aexis/Samples/AIImageApplicationExample/
     Runtime/Scripts/Qwen35DecoderSession.cs): each step's greedy argmax is the
     next step's input at the next position.  The position lives in device
-    memory, so one captured graph is replayed once per token; the tokens must
-    equal those of eager steps bit for bit, and those of the oracle
+    memory, so one captured graph is replayed once per token, or decodes
+    several tokens per replay when several steps are captured in it; the
+    tokens must equal those of eager steps bit for bit, and those of the oracle
     composition until the first near-tie (top-2 gap below 1e-3).
   * Config 3 at its real size (24 layers, 2048 cached positions): graph replay
     equal to the eager step bit for bit, the final hidden state within 5e-3 of
@@ -83,6 +84,32 @@ def test_generate_graph_replays_match_eager_and_oracle(ctx, aexq, orc):
         tok = want
     else:
         assert normwise(x_eager.cpu().numpy(), x_ref) <= 5e-3
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_generate_multistep_graph_matches_eager(ctx, aexq, fused):
+    """capture(advance=True, steps=4): one replay decodes four tokens, the
+    argmax of each step fed to the next on the device; 11 tokens are two
+    replays plus three eager steps, and must equal 11 eager steps bit for bit
+    (tokens, final hidden state, device position)."""
+    _announce(f"generate 11 tokens with a 4-step graph (fused={fused}, 2 layers, 64 positions)")
+    from aiimage_amd import decoder
+    cfg = decoder.ModelConfig(layers=2, capacity=64)
+    sess = decoder.DecodeSession(ctx, cfg, fused=fused)
+    start, pos0, count = 777, 17, 11
+    eager = sess.generate(start, pos0, count)
+    x_eager = sess.xa.clone()
+    g = sess.capture(advance=True, steps=4)
+    for rep in range(2):
+        sess.xa.zero_()
+        sess.history.fill_(-1)
+        got = sess.generate(start, pos0, count, graph=g, graph_steps=4)
+        assert got == eager, (rep, got, eager)
+        assert torch.equal(sess.xa, x_eager), rep
+        assert int(sess.pos.item()) == pos0 + count
+        assert int(sess.token.item()) == eager[-1]
+    with pytest.raises(ValueError):
+        sess.capture(steps=0)
 
 
 def test_generate_rejects_past_capacity(ctx, aexq):
