@@ -42,9 +42,11 @@
 // the compute waves run phase p, the poll waves wait for phase p's outputs of
 // the whole grid (the inputs of phase p + 1) and leave them in LDS, ready at
 // the next workgroup barrier; they also do the work between a poll and the
-// next linear: RMSNorm-in (bit-exact with the streaming kernel's staged path,
-// split between the two waves), RoPE of q and the new k row, the split merge
-// and the RMSNorm gammas.  The compute waves load
+// next linear: the RMSNorm-in (for layer 0's input, in the prologue, bit-exact
+// with the streaming kernel's staged path; for every later one, gamma x in
+// fp16 before the barrier and 1 / rms after it, which the compute waves apply
+// to each row's sum), RoPE of q and the new k row, the split merge and the
+// RMSNorm gammas.  The compute waves load
 // each phase's weights (and the split's cached K/V rows) one to three phases
 // ahead into registers, issuing them at the start of a phase so that the
 // grid-wide burst drains while they compute, before the phase's outputs are
@@ -66,9 +68,13 @@
 // order; fp16(x * inv * gamma)), the same per-chunk dot-product order and
 // group-scale fmaf, the same DPP row reduction and epilogue.  q/k/v, gate/up
 // and down use the streaming kernel's lanes per row and chunks per lane, so
-// their outputs are bit-identical to those of aexq_linear at M = 1; o_proj
-// takes 64 lanes per row (one row per wave, eight waves busy instead of four
-// at half the chunks per lane), so its sums are grouped differently.  Attention
+// layer 0's q/k/v outputs are bit-identical to those of aexq_linear at M = 1;
+// o_proj takes 64 lanes per row (one row per wave, eight waves busy instead of
+// four at half the chunks per lane), so its sums are grouped differently; and
+// after layer 0 the RMSNorm-in's 1 / rms multiplies each row's sum of
+// W (fp16(gamma x)) rather than each element before its fp16 rounding, the
+// same product rounded differently, so the barrier before a linear does not
+// wait for the vector's sum of squares.  Attention
 // follows MM:420-544 (scale, max-subtracted softmax, sum floored at 1e-20)
 // with positions split over workgroups and waves.
 #include <math.h>
@@ -302,18 +308,17 @@ __device__ __forceinline__ void pw_rms(const f16* x, const float* gamma, f16* ou
   }
 }
 
-// Both poll waves: the tagged fp16 vector of k <= 1024 words at src into
-// plain (LDS, plain order) and its RMSNorm-in into out (LDS, nibble-pair order
-// for Q4 weights), the two waves splitting pw_rms's work: wave pw polls,
-// squares and normalises the 8-element slices (lane + 64 v) of v = pw and
-// pw + 2, and the four wave sums meet in s_part, where both waves add them in
-// pw_rms's order, so the result is bit-exact with it.  `count` is the LDS
-// counter the two waves meet on; `target` advances by 2 per call.
+// Both poll waves: the tagged fp16 vector x of k <= 1024 words at src into
+// plain (LDS, plain order) and fp16(x * gamma) into out (LDS, nibble-pair
+// order for Q4 weights): the RMSNorm-in without its 1 / rms factor, which the
+// compute waves apply to each row's sum (y = W (gamma x) / rms(x)) once
+// pw_inv_publish has formed it, so the workgroup barrier does not wait for
+// the sum of squares.  Wave pw takes the 8-element slices (lane + 64 v) of
+// v = pw and pw + 2 and keeps them in xv for pw_inv_publish.
 template <bool PAIRS>
-__device__ __forceinline__ void pw_vec_rms2(const uint32_t* src, int k, uint32_t tag, f16* plain,
-                                            const float* gamma, f16* out, float eps, int lane,
-                                            int pw, float* s_part, int* count, int& target,
-                                            int* err, bool& broken) {
+__device__ __forceinline__ void pw_vec_gx(const uint32_t* src, int k, uint32_t tag, f16* plain,
+                                          const float* gamma, f16* out, int lane, int pw,
+                                          u32x4 (&xv)[2], int* err, bool& broken) {
   int off[4];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -323,18 +328,51 @@ __device__ __forceinline__ void pw_vec_rms2(const uint32_t* src, int k, uint32_t
   }
   u32x4 t[4];
   pw_wait<4>(src, k, off, tag, 16, 0xffffu, t, err, broken);
-  u32x4 xv[2];
-  float part[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     xv[j] = u32x4{0u, 0u, 0u, 0u};
-    if (off[2 * j] >= 0) {
+    const int e0 = off[2 * j];
+    if (e0 >= 0) {
       uint32_t a, b, c, d;
       halves(t[2 * j], a, b);
       halves(t[2 * j + 1], c, d);
       xv[j] = u32x4{a, b, c, d};
-      *(u32x4*)(plain + off[2 * j]) = xv[j];
+      *(u32x4*)(plain + e0) = xv[j];
+      const f32x4 g0 = *(const f32x4*)(gamma + e0);
+      const f32x4 g1 = *(const f32x4*)(gamma + e0 + 4);
+      const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 h = as_h2(xv[j][e]);
+        const f16x2 r = {(f16)((float)h[0] * g[2 * e]), (f16)((float)h[1] * g[2 * e + 1])};
+        o[e] = as_u(r);
+      }
+      uint32_t xp[4];
+      if constexpr (PAIRS) {
+        q4_xpairs(o[0], o[1], o[2], o[3], xp);
+      } else {
+        xp[0] = o[0];
+        xp[1] = o[1];
+        xp[2] = o[2];
+        xp[3] = o[3];
+      }
+      *(u32x4*)(out + e0) = u32x4{xp[0], xp[1], xp[2], xp[3]};
     }
+  }
+}
+
+// Both poll waves, after the workgroup barrier that released the compute
+// waves: 1 / rms of the vector pw_vec_gx left in xv, with pw_rms's arithmetic
+// (sums of squares over 8-element slices, four wave sums meeting in s_part and
+// added in order), into *inv; *done advances by one once it is there.
+// `count` is the LDS counter the two waves meet on (target advances by 2).
+__device__ __forceinline__ void pw_inv_publish(const u32x4 (&xv)[2], int k, float eps, int lane,
+                                               int pw, float* s_part, int* count, int& target,
+                                               float* inv, int* done, int* err, bool& broken) {
+  float part[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -363,36 +401,13 @@ __device__ __forceinline__ void pw_vec_rms2(const uint32_t* src, int k, uint32_t
     __builtin_amdgcn_s_sleep(0);
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  float tot = 0.0f;
+  if (pw == 0) {
+    float tot = 0.0f;
 #pragma unroll
-  for (int v = 0; v < 4; ++v) tot += s_part[v];
-  const float inv = rsqrtf(fmaxf(tot / (float)k + eps, 1e-20f));
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int e0 = off[2 * j];
-    if (e0 >= 0) {
-      const f32x4 g0 = *(const f32x4*)(gamma + e0);
-      const f32x4 g1 = *(const f32x4*)(gamma + e0 + 4);
-      const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
-      uint32_t o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const f16x2 h = as_h2(xv[j][e]);
-        const float a = (float)h[0] * inv, b = (float)h[1] * inv;
-        const f16x2 r = {(f16)(a * g[2 * e]), (f16)(b * g[2 * e + 1])};
-        o[e] = as_u(r);
-      }
-      uint32_t xp[4];
-      if constexpr (PAIRS) {
-        q4_xpairs(o[0], o[1], o[2], o[3], xp);
-      } else {
-        xp[0] = o[0];
-        xp[1] = o[1];
-        xp[2] = o[2];
-        xp[3] = o[3];
-      }
-      *(u32x4*)(out + e0) = u32x4{xp[0], xp[1], xp[2], xp[3]};
-    }
+    for (int v = 0; v < 4; ++v) tot += s_part[v];
+    if (lane == 0) *inv = rsqrtf(fmaxf(tot / (float)k + eps, 1e-20f));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0) __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
 
@@ -428,6 +443,24 @@ __device__ __forceinline__ void cbar(int* ctr, int& target, int lane, int* err, 
     __builtin_amdgcn_s_sleep(0);
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Compute waves: the 1 / rms pw_inv_publish forms for this phase's input,
+// once *done has reached target (bounded like the other waits).
+__device__ __forceinline__ float cw_inv(const float* inv, int* done, int target, int* err,
+                                        bool& broken) {
+  for (int spin = 0;; ++spin) {
+    if (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target || broken)
+      break;
+    if (spin >= kSpinLimit) {
+      atomicOr(err, 1);
+      broken = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(0);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  return *inv;
 }
 
 // Compute waves: this wave's writes to s_out are done.
@@ -726,6 +759,8 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
   __shared__ int s_cbar;
   __shared__ float s_rpart[4];                         // the RMSNorm's four wave sums
   __shared__ int s_rms;                                // RMSNorm halves done (both poll waves)
+  __shared__ float s_inv;                              // 1 / rms of the phase's RMSNorm-in input
+  __shared__ int s_invc;                               // 1 / rms values published
   __shared__ uint32_t s_e0;
 
   const int b = blockIdx.x;
@@ -829,6 +864,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
     if (threadIdx.x == 0) {
       s_cbar = 0;
       s_rms = 0;
+      s_invc = 0;
       s_done = 0;
       s_e0 = ld_word(p.epoch);
     }
@@ -859,8 +895,11 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
           const uint32_t* w; const void* s; int n, lr;
           qkv_mat(L, w1.r0, w, s, n, lr);
           const int row = lr + lane / L1;
-          const float v =
-              0.0f + row_dot<L1, C1, FMT, GM>(wqkv.w[0], wqkv.s[0], s_xn, ch1, row, sf16, t);
+          float v = row_dot<L1, C1, FMT, GM>(wqkv.w[0], wqkv.s[0], s_xn, ch1, row, sf16, t);
+          // layer 0's input is normalised whole (the prologue); later layers'
+          // rows take 1 / rms here
+          if (l > 0) v *= cw_inv(&s_inv, &s_invc, 2 * l, err, broken);
+          v += 0.0f;
           if (lane % L1 == 0 && row < n)
             s_out[w1.r0 + lane / L1 - b * p.rows_qkv] = tag_f16((f16)v, tg);
         }
@@ -1004,8 +1043,9 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
           const int row = w4.r0 + lane / L1;
           float g, u;
           row_dot2<L1, C1, FMT, GM>(wgu.w, wgu.s, s_xn, ch1, row, sf16, t, g, u);
-          g += 0.0f;
-          u += 0.0f;
+          const float inv = cw_inv(&s_inv, &s_invc, 2 * l + 1, err, broken);
+          g = g * inv + 0.0f;
+          u = u * inv + 0.0f;
           const float v = silu(g) * u;
           if (lane % L1 == 0 && row < inter)
             s_out[row - b * p.rows_inter] = tag_f16((f16)v, tg + 4);
@@ -1110,6 +1150,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
     const int lane = opaque_tid() & 63;
     const int rc = b % kStepReplicas;  // the copy of every polled vector this workgroup reads
     int rms_target = 0;
+    u32x4 xa_g[2];  // the next layer's input slices (pw_vec_gx), for its 1 / rms
     if (pw == 0) {
       f32x4 g[4];
       pw_gamma_issue(lds_ptr(&s_layers[0].g_attn), hid, g, lane);
@@ -1128,7 +1169,11 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
     for (int l = 0; l < nl; ++l) {
       const StepLayer& L = s_layers[l];
       const uint32_t tg = e0 + 1 + 6u * (uint32_t)l;
-      // during P1: q/k/v of the kv head, RoPE of q and the new k row
+      // during P1: 1 / rms of the layer's input (layers after the first); q/k/v
+      // of the kv head, RoPE of q and the new k row
+      if (l > 0)
+        pw_inv_publish(xa_g, hid, p.eps, lane, pw, s_rpart, &s_rms, rms_target, &s_inv, &s_invc,
+                       err, broken);
       if (attn_wg && pw == 0) {
         // this position's RoPE row (DEC:1660-1675 tables), entry `lane`
         const float cs = p.cos_t[(long long)pos * kHalf + lane];
@@ -1232,24 +1277,28 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       pw_vec_pairs<kStepMaxQ / 256 / kPW, kPairs>(p.attn_t + rc * p.attn_rs, qw, tg + 2, s_at, lane,
                                                   pw, err, broken);
       __syncthreads();
-      // during P3: x after attention and its RMSNorm-in (both poll waves); the
-      // next layer's gamma
+      // during P3: x after attention, and gamma x for the next linear (both
+      // poll waves); the next layer's gamma
       if (pw == 1 && l + 1 < nl) {
         f32x4 ga[4];
         pw_gamma_issue(lds_ptr(&s_layers[l + 1].g_attn), hid, ga, lane);
         pw_gamma_store(ga, s_ga, hid, lane);
       }
-      pw_vec_rms2<kPairs>(p.xb_t + rc * p.xb_rs, hid, tg + 3, s_xb, s_gm, s_xn, p.eps, lane, pw,
-                          s_rpart, &s_rms, rms_target, err, broken);
+      u32x4 xb_g[2];
+      pw_vec_gx<kPairs>(p.xb_t + rc * p.xb_rs, hid, tg + 3, s_xb, s_gm, s_xn, lane, pw, xb_g, err,
+                        broken);
       __syncthreads();
-      // during P4: the SwiGLU output
+      // during P4: 1 / rms of x after attention; the SwiGLU output
+      pw_inv_publish(xb_g, hid, p.eps, lane, pw, s_rpart, &s_rms, rms_target, &s_inv, &s_invc,
+                     err, broken);
       pw_vec_pairs<kStepMaxInter / 256 / kPW, kPairs>(p.h_t + rc * p.h_rs, inter, tg + 4, s_h, lane,
                                                       pw, err, broken);
       __syncthreads();
-      // during P5: the next layer's input and its RMSNorm-in (both poll waves)
+      // during P5: the next layer's input, and gamma x for its q/k/v (both
+      // poll waves)
       if (l + 1 < nl)
-        pw_vec_rms2<kPairs>(p.xa_t + rc * p.xa_rs, hid, tg + 5, s_xa, s_ga, s_xn, p.eps, lane, pw,
-                            s_rpart, &s_rms, rms_target, err, broken);
+        pw_vec_gx<kPairs>(p.xa_t + rc * p.xa_rs, hid, tg + 5, s_xa, s_ga, s_xn, lane, pw, xa_g, err,
+                          broken);
       __syncthreads();
     }
   }
