@@ -2028,7 +2028,7 @@ extern "C" aexq_status aexq_decoder_create(aexq_ctx* ctx, const aexq_decoder_con
   const long long words[8] = {(long long)kStepReplicas * rs[0], (long long)kStepReplicas * rs[1],
                               (long long)hq * splits * kStepPartStride,
                               (long long)kStepReplicas * rs[3], (long long)kStepReplicas * rs[4],
-                              (long long)kStepReplicas * rs[5], 1, 1};
+                              (long long)kStepReplicasH * rs[5], 1, 1};
   long long off[9];
   off[0] = round_up((long long)count * sizeof(StepLayer), 4096);
   for (int i = 0; i < 8; ++i) off[i + 1] = off[i] + round_up(words[i] * 4, 4096);

@@ -13,8 +13,8 @@
 //                                    positions: scores, softmax statistics,
 //                                    P.V partials
 //   P2b split merge                  (q head, slice of dims) per workgroup, on
-//                                    the poll wave that received the partials,
-//                                    which also stores the merged slice
+//                                    the two poll waves (half of the dims each),
+//                                    which also store the merged slice
 //   P3  o_proj + residual            rows of Wo
 //   P4  gate/up + SwiGLU             rows of the gate/up pair
 //   P5  down + residual              rows of Wdown
@@ -499,12 +499,12 @@ __device__ __forceinline__ RepLanes rep_lanes(int n, int lane) {
   return m;
 }
 // Store wave: n tagged words from LDS into every copy of a replicated vector
-// (copies `stride` words apart).
+// (`copies` copies, `stride` words apart).
 __device__ __forceinline__ void sw_copy_rep(uint32_t* dst, int stride, const uint32_t* src, int n,
-                                            const RepLanes& m) {
+                                            const RepLanes& m, int copies = kStepReplicas) {
   if (m.word < n) {
     const uint32_t v = src[m.word];
-    for (int r = m.copy; r < kStepReplicas; r += m.step) st_word(dst + r * stride + m.word, v);
+    for (int r = m.copy; r < copies; r += m.step) st_word(dst + r * stride + m.word, v);
   }
 }
 
@@ -1126,7 +1126,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         AEXQ_STAMP(l, 6, lane, b);
         const int r0 = b * p.rows_inter;
         const int n = inter - r0 < p.rows_inter ? inter - r0 : p.rows_inter;
-        if (n > 0) sw_copy_rep(p.h_t + r0, p.h_rs, s_out, n, rl_inter);
+        if (n > 0) sw_copy_rep(p.h_t + r0, p.h_rs, s_out, n, rl_inter, kStepReplicasH);
       }
       __syncthreads();
       AEXQ_STAMP(l, 7, lane, b);
@@ -1220,57 +1220,50 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
         f32x4 gm[4];
         pw_gamma_issue(lds_ptr(&L.g_mlp), hid, gm, lane);
         pw_gamma_store(gm, s_gm, hid, lane);
-      } else if (mwg) {
+      }
+      if (mwg) {
         // the split merge of (q head mh, dims md0 .. md0 + per), MM:420-544's
-        // softmax over all positions: lps groups of 8 dims, each held by
-        // sl = 64 / lps lanes, lane = group q8 * sl + split s; every lane
-        // reads its split's (max, sum) header.  A group's lanes sum over the
-        // splits with group_sum (no LDS round trip), and its first
-        // kStepReplicas lanes write the merged 8 dims into the copies of the
-        // attention output themselves.
-        static_assert(kStepReplicas <= 16, "a group has at least 16 lanes");
-        const int lps = per / 8, sl = 64 / lps, q8 = lane / sl, s = lane % sl;
+        // softmax over all positions, on both poll waves: wave pw merges dims
+        // md0 + hp pw .. + hp (hp = per / 2) in lq quads of 4 dims, each held by
+        // sl = 64 / lq lanes, lane = quad q4 * sl + split s; every lane reads
+        // its split's (max, sum) header.  A quad's lanes sum over the splits with
+        // group_sum (no LDS round trip), and its first kStepReplicas lanes write
+        // the merged 4 dims into the copies of the attention output themselves.
+        static_assert(kStepReplicas <= 16, "a quad has at least 16 lanes");
+        const int hp = per / 2, lq = hp / 4, sl = 64 / lq, q4 = lane / sl, s = lane % sl;
+        const int d0 = md0 + hp * pw + 4 * q4;
         const bool in = s < S;
         const int rb = (mh * S + (in ? s : 0)) * kStepPartStride;
-        int off[3] = {in ? rb + 4 + md0 + 8 * q8 : -1, in ? rb + 4 + md0 + 8 * q8 + 4 : -1,
-                      in ? rb : -1};
-        u32x4 v[3];
-        pw_wait<3>(p.part_t, p.hq * S * kStepPartStride, off, tg + 1, 0, 0xffu, v, err, broken);
+        int off[2] = {in ? rb + 4 + d0 : -1, in ? rb : -1};
+        u32x4 v[2];
+        pw_wait<2>(p.part_t, p.hq * S * kStepPartStride, off, tg + 1, 0, 0xffu, v, err, broken);
         // absent splits are neutral
-        const float ms = in ? as_f32(v[2][0] & ~0xffu) : kNegBig;
-        const float ls = in ? as_f32(v[2][1] & ~0xffu) : 0.0f;
+        const float ms = in ? as_f32(v[1][0] & ~0xffu) : kNegBig;
+        const float ls = in ? as_f32(v[1][1] & ~0xffu) : 0.0f;
         const float M = wave_max(ms);
         const float f = __expf(ms - M);
-        const float lsum = wave_sum(q8 == 0 ? ls * f : 0.0f);
-        float a[8];
+        const float lsum = wave_sum(q4 == 0 ? ls * f : 0.0f);
+        float a[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          a[e] = in ? as_f32(v[0][e] & ~0xffu) * f : 0.0f;
-          a[4 + e] = in ? as_f32(v[1][e] & ~0xffu) * f : 0.0f;
-        }
+        for (int e = 0; e < 4; ++e) a[e] = in ? as_f32(v[0][e] & ~0xffu) * f : 0.0f;
         if (sl == 64) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) a[e] = group_sum<64>(a[e]);
+          for (int e = 0; e < 4; ++e) a[e] = group_sum<64>(a[e]);
         } else if (sl == 32) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) a[e] = group_sum<32>(a[e]);
+          for (int e = 0; e < 4; ++e) a[e] = group_sum<32>(a[e]);
         } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) a[e] = group_sum<16>(a[e]);
+          for (int e = 0; e < 4; ++e) a[e] = group_sum<16>(a[e]);
         }
         if (s < kStepReplicas) {
           const float inv_l = 1.0f / fmaxf(lsum, 1e-20f);
-          u32x4 w0, w1;
+          u32x4 w0;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            w0[e] = tag_f16((f16)(a[e] * inv_l), tg + 2);
-            w1[e] = tag_f16((f16)(a[4 + e] * inv_l), tg + 2);
-          }
+          for (int e = 0; e < 4; ++e) w0[e] = tag_f16((f16)(a[e] * inv_l), tg + 2);
           const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
               (void*)p.attn_t, (short)0, kStepReplicas * p.attn_rs * 4, kBufferRsrcWord3);
-          const int o = (s * p.attn_rs + mh * kHd + md0 + 8 * q8) * 4;
-          st_quad(ar, o, w0);
-          st_quad(ar, o + 16, w1);
+          st_quad(ar, (s * p.attn_rs + mh * kHd + d0) * 4, w0);
         }
       }
       // the attention output of the whole grid (the merges of every workgroup)
@@ -1291,7 +1284,7 @@ __global__ __launch_bounds__(kSt) void decode_layers_kernel(const StepParams p) 
       // during P4: 1 / rms of x after attention; the SwiGLU output
       pw_inv_publish(xb_g, hid, p.eps, lane, pw, s_rpart, &s_rms, rms_target, &s_inv, &s_invc,
                      err, broken);
-      pw_vec_pairs<kStepMaxInter / 256 / kPW, kPairs>(p.h_t + rc * p.h_rs, inter, tg + 4, s_h, lane,
+      pw_vec_pairs<kStepMaxInter / 256 / kPW, kPairs>(p.h_t + (b % kStepReplicasH) * p.h_rs, inter, tg + 4, s_h, lane,
                                                       pw, err, broken);
       __syncthreads();
       // during P5: the next layer's input, and gamma x for its q/k/v (both

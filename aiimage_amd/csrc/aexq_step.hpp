@@ -23,6 +23,10 @@ constexpr int kStepPartStride = 132;    // words per (q head, split) partial: m,
 // workgroup b polls copy b % kStepReplicas, so the grid's polls of one vector
 // spread over that many 4 KB pages (memory channels) instead of meeting on one.
 constexpr int kStepReplicas = 8;
+// The SwiGLU output (28 words per workgroup at the benchmark's shapes) in 4
+// copies: its producers' stores of 8 copies take four store instructions, and
+// 4 copies measured faster.
+constexpr int kStepReplicasH = 4;
 // Words between two copies of a vector of `words` words: whole 4 KB pages, an
 // odd count of them (3 for 12 KB, 5 for 14 KB), so that the copies' first
 // pages do not all fall on pages of one parity.
@@ -57,13 +61,14 @@ struct StepParams {
   const float* cos_t;       // [cap][64]
   const float* sin_t;
   // exchange buffers of tagged words (see aexq_step.hip); the vectors every
-  // workgroup polls are kStepReplicas copies `*_rs` words apart
+  // workgroup polls are kStepReplicas copies (the SwiGLU output
+  // kStepReplicasH) `*_rs` words apart
   uint32_t* xa_t;           // [kStepReplicas][xa_rs >= hidden]
   uint32_t* qkv_t;          // [kStepReplicas][qkv_rs >= qw + 2 kvw]
   uint32_t* part_t;         // [hq][splits][kStepPartStride] (one copy)
   uint32_t* attn_t;         // [kStepReplicas][attn_rs >= qw]
   uint32_t* xb_t;           // [kStepReplicas][xb_rs >= hidden]
-  uint32_t* h_t;            // [kStepReplicas][h_rs >= inter]
+  uint32_t* h_t;            // [kStepReplicasH][h_rs >= inter]
   int xa_rs, qkv_rs, attn_rs, xb_rs, h_rs;
   uint32_t* epoch;          // launch epoch counter
   int* err;                 // set when a wait exceeded its spin bound
