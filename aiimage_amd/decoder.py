@@ -401,16 +401,32 @@ class DecodeSession:
         finally:
             self.ctx.set_stream(old)
         torch.cuda.synchronize()
+        # what generate() needs to know about a replay
+        g.aexq_steps = steps
+        g.aexq_advance = advance
         return g
 
     def generate(self, start_token: int, position: int, count: int,
-                 graph: torch.cuda.CUDAGraph = None, graph_steps: int = 1) -> list:
+                 graph: torch.cuda.CUDAGraph = None, graph_steps: int = None) -> list:
         """Greedy decoding of `count` tokens from `start_token` at `position`
         (Qwen35DecoderSession.Generate, DEC:1160-1237): each step's argmax is the
-        next step's input.  With `graph` (from capture(advance=True,
-        steps=graph_steps)) each replay decodes graph_steps tokens and the
-        remainder of count runs as eager steps; otherwise every token is an
-        eager step.  Returns the generated token ids."""
+        next step's input.  With `graph` (from capture(advance=True, steps=K))
+        each replay decodes K tokens and the remainder of count runs as eager
+        steps; otherwise every token is an eager step.  graph_steps defaults to
+        the graph's K and must equal it; a graph captured without advance (its
+        replays do not move the position) is refused.  Returns the generated
+        token ids."""
+        if graph is not None:
+            captured = getattr(graph, "aexq_steps", None)
+            if getattr(graph, "aexq_advance", True) is False:
+                raise ValueError("the graph was captured without advance=True: its replays "
+                                 "do not move the position")
+            if graph_steps is None:
+                graph_steps = captured if captured is not None else 1
+            elif captured is not None and graph_steps != captured:
+                raise ValueError(f"graph_steps={graph_steps} for a graph of {captured} steps")
+        elif graph_steps is None:
+            graph_steps = 1
         if graph_steps < 1:
             raise ValueError(f"graph_steps={graph_steps}")
         if count < 0 or position + count > self.cfg.capacity:

@@ -91,7 +91,8 @@ def test_generate_multistep_graph_matches_eager(ctx, aexq, fused):
     """capture(advance=True, steps=4): one replay decodes four tokens, the
     argmax of each step fed to the next on the device; 11 tokens are two
     replays plus three eager steps, and must equal 11 eager steps bit for bit
-    (tokens, final hidden state, device position)."""
+    (tokens, final hidden state, device position).  generate() refuses a step
+    count other than the graph's and a graph captured without advance."""
     _announce(f"generate 11 tokens with a 4-step graph (fused={fused}, 2 layers, 64 positions)")
     from aiimage_amd import decoder
     cfg = decoder.ModelConfig(layers=2, capacity=64)
@@ -103,13 +104,19 @@ def test_generate_multistep_graph_matches_eager(ctx, aexq, fused):
     for rep in range(2):
         sess.xa.zero_()
         sess.history.fill_(-1)
-        got = sess.generate(start, pos0, count, graph=g, graph_steps=4)
+        # graph_steps given, then taken from the graph
+        got = sess.generate(start, pos0, count, graph=g, graph_steps=4 if rep == 0 else None)
         assert got == eager, (rep, got, eager)
         assert torch.equal(sess.xa, x_eager), rep
         assert int(sess.pos.item()) == pos0 + count
         assert int(sess.token.item()) == eager[-1]
     with pytest.raises(ValueError):
         sess.capture(steps=0)
+    # a step count other than the graph's, and a graph whose replays do not advance
+    with pytest.raises(ValueError):
+        sess.generate(start, pos0, count, graph=g, graph_steps=2)
+    with pytest.raises(ValueError):
+        sess.generate(start, pos0, count, graph=sess.capture(steps=2))
 
 
 def test_generate_rejects_past_capacity(ctx, aexq):
