@@ -130,6 +130,26 @@ def test_decoder_rope_tables_equal_oracle_rows(orc, head_dim, base, capacity):
         assert np.array_equal(ct[p], c) and np.array_equal(st[p], s), p
 
 
+def test_generate_argument_checks():
+    """DecodeSession.generate refuses, before any device work, a graph_steps
+    other than the captured graph's step count, a graph captured without
+    advance, a step count below 1 and a run past the cache capacity (stand-in
+    session and graph objects carry only what the checks read)."""
+    from types import SimpleNamespace
+    from aiimage_amd import decoder
+    gen = decoder.DecodeSession.generate
+    sess = SimpleNamespace(cfg=SimpleNamespace(capacity=64))
+    four = SimpleNamespace(aexq_steps=4, aexq_advance=True)
+    with pytest.raises(ValueError, match="graph of 4 steps"):
+        gen(sess, 1, 0, 8, graph=four, graph_steps=2)
+    with pytest.raises(ValueError, match="without advance"):
+        gen(sess, 1, 0, 8, graph=SimpleNamespace(aexq_steps=2, aexq_advance=False))
+    with pytest.raises(ValueError, match="graph_steps=0"):
+        gen(sess, 1, 0, 8, graph_steps=0)
+    with pytest.raises(ValueError, match="capacity"):
+        gen(sess, 1, 60, 8, graph=four)
+
+
 # ---------------------------------------------------------------- the C# binding
 
 
