@@ -14,7 +14,6 @@ come from torch (HIP); every computation runs in libaexq.so.
 from __future__ import annotations
 
 import ctypes
-import math
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
