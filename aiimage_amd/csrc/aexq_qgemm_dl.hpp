@@ -17,14 +17,18 @@
 // first MFMA K extent and the rest in the second, so a lane's codes for both
 // extents are one 16-byte read, and the activation fragments are read in the
 // same order (the products of K order, summed in another order in fp32).
-// Q4 keeps K order inside each 32-code extent, so that an extent holds one
-// scale group of 32 or two of 16.
+// Q4 with fp16 weight tiles permutes the same way (a lane's two 8-code chunks
+// are one 8-byte read, and both lie in one scale group of 32, or one of 16):
+// read in K order (lane group g taking chunk 4 kk + g of extent kk) the
+// activation fragments meet LDS bank conflicts (1.3 stall cycles per read on
+// gfx950), in this order none.  Exact Q4 keeps K order inside each 32-code
+// extent, so that an extent holds one scale group of 32 or two of 16.
 //
 // Codes become exact fp16 integers in registers.  Q8 accumulates the row in
 // the MFMA and applies its row scale once at the end.  Q4 has two forms:
-//  * fp16 dequantisation (FD, the default): each lane's eight codes of an
-//    MFMA extent share one scale (lane group g holds codes 8 g .. 8 g + 7, so
-//    a group of 16 is lane groups 0-1 or 2-3), and the B fragment is formed as
+//  * fp16 dequantisation (FD, the default): each lane's codes share one scale
+//    (lane group g holds codes 16 g .. 16 g + 15 of the step: scale group
+//    g / 2 of 32, or g of 16), and the B fragment is formed as
 //    fp16(q * s) by one packed fp16 multiply (one rounding; fp32 scales are
 //    rounded to fp16 first), the weight tile dequantised to fp16 as the
 //    benchmark's batched case specifies; the MFMA then accumulates the whole
@@ -110,6 +114,13 @@ __device__ __forceinline__ void bar() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// silu(g) = g / (1 + e^-g) with the division as a reciprocal (v_rcp_f32, 1 ulp)
+// times g: the SwiGLU epilogue of a tile forms it for every output, and the
+// IEEE division's expansion made up most of the epilogue's VALU work.
+__device__ __forceinline__ float silu_rcp(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }
 
 // Eight offset-8 nibbles (n0 in bits 0-3) -> four fp16 pairs of the exact
@@ -257,9 +268,10 @@ struct QGemmDL {
   // Fragments of one step a wave reads from LDS: the activation blocks of one
   // K half and the raw codes (and Q4 scales) of both halves.
   // (Q4: the lane's 8 codes of each MFMA extent and the row's scales of the
-  // step, one per extent or two for groups of 16; FD: the lane's own scale
-  // of each extent)
-  static constexpr int NS = FMT == kQ8 ? 1 : (FD ? 2 : SPR);
+  // step, one per extent or two for groups of 16; FD: the lane's own scale)
+  static constexpr int NS = FMT == kQ8 ? 1 : (FD ? 1 : SPR);
+  // K order permuted as Q8's (lane group g: chunks 2 g and 2 g + 1 of the step)
+  static constexpr bool PERM = FMT == kQ8 || FD;
   struct Frag {
     f16x8 a[TM];
     typename std::conditional<FMT == kQ8, u32x4, u32x2>::type c[TN];
@@ -278,10 +290,13 @@ struct QGemmDL {
     const int f = (l16 & 7) ^ (l16 >> 3);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
-      L.a_off[kk] = l16 * 128 + (((FMT == kQ8 ? 2 * lk + kk : 4 * kk + lk) ^ f) << 4);
-    L.b_off = FMT == kQ8 ? 16 * lane : l16 * 16 + 4 * lk;  // Q4: + 256 kk
-    // FD groups of 16: lane groups 2-3 take the extent's second scale
-    L.s_off = FMT == kQ8 ? 0 : l16 * (SPR * SB) + (FD && G == 16 ? (lk >> 1) * SB : 0);
+      L.a_off[kk] = l16 * 128 + (((PERM ? 2 * lk + kk : 4 * kk + lk) ^ f) << 4);
+    // Q4 codes [half][row] per 16-row block: FD chunks 2 lk, 2 lk + 1 (half
+    // lk / 2, bytes 8 (lk % 2) ..); exact: dword lk of each half (+ 256 kk)
+    L.b_off = FMT == kQ8 ? 16 * lane
+                         : (FD ? (lk >> 1) * 256 + l16 * 16 + (lk & 1) * 8 : l16 * 16 + 4 * lk);
+    // FD: scale group 16 lk / G of the step (lk / 2 for groups of 32, lk for 16)
+    L.s_off = FMT == kQ8 ? 0 : l16 * (SPR * SB) + (FD ? (16 * lk / G) * SB : 0);
     return L;
   }
 
@@ -300,14 +315,15 @@ struct QGemmDL {
         f.c[tn] = *(const u32x4*)(base + A_BYTES + blk * 1024 + L.b_off);
       } else {
         const char* bb = base + A_BYTES + blk * 512 + L.b_off;
-        f.c[tn] = u32x2{*(const uint32_t*)bb, *(const uint32_t*)(bb + 256)};
+        if constexpr (FD)
+          f.c[tn] = *(const u32x2*)bb;  // chunk 2 lk, then 2 lk + 1
+        else
+          f.c[tn] = u32x2{*(const uint32_t*)bb, *(const uint32_t*)(bb + 256)};
         const char* sb = base + A_BYTES + B_BYTES + blk * 16 * (SPR * SB) + L.s_off;
-        // FD: extent kk's scale sits SPR / 2 scales after extent 0's
-        constexpr int SSTEP = FD ? SPR / 2 : 1;
 #pragma unroll
         for (int i = 0; i < NS; ++i)
-          f.s[tn][i] = SF16 ? (uint32_t) * (const uint16_t*)(sb + SB * SSTEP * i)
-                            : *(const uint32_t*)(sb + 4 * SSTEP * i);
+          f.s[tn][i] = SF16 ? (uint32_t) * (const uint16_t*)(sb + SB * i)
+                            : *(const uint32_t*)(sb + 4 * i);
       }
     }
   }
@@ -330,7 +346,7 @@ struct QGemmDL {
         // the MFMA accumulates the row
         uint32_t e[4];
         q4_pairs_seq(f.c[tn][kk], e);
-        const f16 s16 = (f16)scale_of(f.s[tn][kk], SF16);
+        const f16 s16 = (f16)scale_of(f.s[tn][0], SF16);
         const f16x2 s2 = {s16, s16};
 #pragma unroll
         for (int j = 0; j < 4; ++j) e[j] = as_u(as_h2(e[j]) * s2);
@@ -504,7 +520,7 @@ struct QGemmDL {
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             v[j] = a_in * (0.0f + a_out * (g[j] * rs0[j]));
-            if constexpr (PAIR) v[j] = silu(v[j]) * (a_in * (0.0f + a_out * (u[j] * rs1[j])));
+            if constexpr (PAIR) v[j] = silu_rcp(v[j]) * (a_in * (0.0f + a_out * (u[j] * rs1[j])));
             v[j] += res[j];
           }
         } else {
@@ -515,7 +531,7 @@ struct QGemmDL {
             if (n < mn) {
               v[j] = gemm_epilogue(E, mbase + m, n, g[j] * rs0[j]);
               if constexpr (PAIR)
-                v[j] = silu(v[j]) * gemm_epilogue(E, mbase + m, n, u[j] * rs1[j]);
+                v[j] = silu_rcp(v[j]) * gemm_epilogue(E, mbase + m, n, u[j] * rs1[j]);
               v[j] += res[j];
             }
           }
