@@ -39,14 +39,17 @@ struct QmmW {
   using Acc = typename Base::Acc;
   static constexpr int TN = 16 * NT;          // rows of one wave's blocks
   static constexpr int TNG = kWaves * TN;     // rows of a workgroup tile
-  static constexpr int XRS = 512 + 16;        // LDS activation row stride (256 fp16 + pad)
+  // LDS activation row stride (256 fp16 + 32 bytes): MFMA lane (n, kb)'s
+  // 16-byte A reads of rows n = 0..15 fall on distinct 16-byte slots of a
+  // 512-byte bank line (gfx950 serves 32 lanes' 16-byte reads per pass), and
+  // every 32-lane pass of store_x writes one whole row
+  static constexpr int XRS = 512 + 32;
   static constexpr int XSL = 16 * MT * XRS;   // LDS bytes of one activation slice
   static constexpr int XV = 2 * MT;           // 16-byte activation loads per thread per step
   static constexpr int NW = PAIR ? 2 : 1;
   static constexpr int RB = FMT == kQ8 ? 256 : 128;  // code bytes of a row per step
   static constexpr int WI = RB / 64;                 // 16-byte loads per lane per 16-row block
-  static constexpr int RS = RB + 32;                 // LDS row stride (padded against conflicts)
-  static constexpr int BLK = 16 * RS;                // LDS bytes of one 16-row block
+  static constexpr int BLK = 16 * RB;                // LDS bytes of one 16-row block
   static constexpr int LDS_WAVE = NW * NT * BLK;
   static constexpr int SV = FMT == kQ8 ? 0 : (SF16 ? 1 : 2) * (G16 ? 2 : 1);  // 16-byte scale loads per block
 
@@ -152,7 +155,8 @@ struct QmmW {
   }
 
   // The workgroup's activation slice of one step (16 MT rows x 256 codes):
-  // thread t loads 32 bytes of row t / 16 per 16-row tile (rows past M read 0).
+  // thread t loads 16-byte chunk t % 32 of rows t / 32 and t / 32 + 8 per
+  // 16-row tile (rows past M read 0), so 32 lanes cover one row.
   static __device__ __forceinline__ void load_x(const QmvParams& p, const Cursor& cu,
                                                 u32x4 (&xv)[XV]) {
     const QmvMat& mt = p.mat[cu.j];
@@ -161,14 +165,14 @@ struct QmmW {
     const int xnum = (int)(p.m * rs2) - cu.s * 512;
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, xnum, kBufferRsrcWord3);
-    const int row = threadIdx.x >> 4, col = (threadIdx.x & 15) * 32;
+    const int row = threadIdx.x >> 5, col = (threadIdx.x & 31) * 16;
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
       for (int v = 0; v < 2; ++v)
         xv[2 * m + v] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       xr, (16 * m + row) * (int)rs2 + col + 16 * v, 0, 0));
+                       xr, (16 * m + row + 8 * v) * (int)rs2 + col, 0, 0));
   }
 
   // RMSNorm-in inside the kernel (RMSX: launches with one item per workgroup,
@@ -218,15 +222,15 @@ struct QmmW {
   static __device__ __forceinline__ void store_x(uint8_t* xs, const u32x4 (&xv)[XV],
                                                  int step = 0, const float* gs = nullptr,
                                                  const float* inv = nullptr) {
-    const int row = threadIdx.x >> 4, col = (threadIdx.x & 15) * 32;
+    const int row = threadIdx.x >> 5, col = (threadIdx.x & 31) * 16;
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
       for (int v = 0; v < 2; ++v) {
         u32x4 c = xv[2 * m + v];
         if constexpr (RMSX) {
-          const float iv = inv[16 * m + row];
-          const float* g = gs + step * 256 + (col >> 1) + 8 * v;  // col counts bytes
+          const float iv = inv[16 * m + row + 8 * v];
+          const float* g = gs + step * 256 + (col >> 1);  // col counts bytes
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const f16x2 h = as_h2(c[e]);
@@ -240,7 +244,7 @@ struct QmmW {
           q4_xpairs(c[0], c[1], c[2], c[3], xp);
           c = u32x4{xp[0], xp[1], xp[2], xp[3]};
         }
-        *(u32x4*)(xs + (16 * m + row) * XRS + col + 16 * v) = c;
+        *(u32x4*)(xs + (16 * m + row + 8 * v) * XRS + col) = c;
       }
   }
 
@@ -333,9 +337,13 @@ struct QmmW {
                                                  const uint8_t* xs, const Buf& buf, Acc& acc) {
     const int n_l = lane & 15, kb = lane >> 4;
     const int lr = lane >> 3, lc = lane & 7;
-    // LDS: row n, group g, 8-code unit kb at n * RS + kb * (RB / 4) + g * (RB / 32)
-    // (Q4: 4 bytes per unit, Q8: 8), so MFMA lane (n, kb) finds its eight
-    // groups' units contiguous
+    // LDS, per 16-row block: the 16-byte run v of MFMA lane (n, kb) -- its
+    // 8-code unit kb of groups 4 v .. 4 v + 3 (Q4, 4 bytes a unit) or 2 v,
+    // 2 v + 1 (Q8, 8 bytes) -- at v * 1024 + (16 kb + n') * 16, with the row
+    // swizzled (Q4: n' = n ^ 4 v; Q8: n' = n ^ (2 (v & 1) + 4 (kb / 2))): a
+    // lane's runs are 16-byte reads whose 32-lane passes cover 32 distinct
+    // slots of a 512-byte bank line, and the transposing stores (Q4: 4 bytes,
+    // 32 lanes a pass; Q8: 8 bytes, 16 lanes a pass) meet distinct banks
 #pragma unroll
     for (int h = 0; h < NW; ++h)
 #pragma unroll
@@ -349,13 +357,17 @@ struct QmmW {
             // bytes 128 (i >> 1) + 16 lc: group 4 (i >> 1) + lc / 2, units 2 (lc & 1) + {0, 1}
             const int g = 4 * (i >> 1) + (lc >> 1);
             const int u0 = 2 * (lc & 1);
+            const int np = n ^ (2 * (lc >> 2) + 4 * (lc & 1));  // (g / 2) & 1 = lc / 4, kb / 2 = lc & 1
+            uint8_t* d = blk + (g >> 1) * 1024 + (g & 1) * 8;
             typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-            *(u32x2v*)(blk + n * RS + u0 * 64 + g * 8) = u32x2v{c[0], c[1]};
-            *(u32x2v*)(blk + n * RS + (u0 + 1) * 64 + g * 8) = u32x2v{c[2], c[3]};
+            *(u32x2v*)(d + (16 * u0 + np) * 16) = u32x2v{c[0], c[1]};
+            *(u32x2v*)(d + (16 * (u0 + 1) + np) * 16) = u32x2v{c[2], c[3]};
           } else {
             // 16 bytes = group lc, units 0..3
+            const int np = n ^ (4 * (lc >> 2));
+            uint8_t* d = blk + (lc >> 2) * 1024 + (lc & 3) * 4;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) *(uint32_t*)(blk + n * RS + u * 32 + lc * 4) = c[u];
+            for (int u = 0; u < 4; ++u) *(uint32_t*)(d + (16 * u + np) * 16) = c[u];
           }
         }
       }
@@ -367,10 +379,11 @@ struct QmmW {
     for (int h = 0; h < NW; ++h)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const uint8_t* src = lds + (h * NT + nt) * BLK + n_l * RS + kb * (RB / 4);
+        const uint8_t* src = lds + (h * NT + nt) * BLK;
 #pragma unroll
         for (int v = 0; v < 2 * UW; ++v) {
-          const u32x4 t = *(const u32x4*)(src + 16 * v);
+          const int np = FMT == kQ8 ? n_l ^ (2 * (v & 1) + 4 * (kb >> 1)) : n_l ^ (4 * v);
+          const u32x4 t = *(const u32x4*)(src + v * 1024 + (16 * kb + np) * 16);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int d = 4 * v + e;  // dword index in the lane's contiguous run
