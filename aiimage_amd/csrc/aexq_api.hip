@@ -1082,7 +1082,13 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       int bm = M <= 64 ? 64 : 128;
       const char* benv = getenv("AEXQ_QGEMM_BM");  // tuning override: 64 or 128
       if (benv && (atoi(benv) == 64 || atoi(benv) == 128)) bm = atoi(benv);
-      gc = QgemmConfig{fmt, bm, swiglu, sf16, g16, true, fd};
+      // Q4 fp16 tiles at 64-row tiles take 128-wide K steps: a lane's code
+      // load is then a whole 16-byte quarter of a 64-byte row step, half the
+      // code and scale requests per K of 64-wide steps (the M = 64 launches
+      // wait on those requests).  AEXQ_QGEMM_K64 keeps 64-wide steps (tuning).
+      const bool k128 = fmt == kQ4 && fd && bm == 64 && K % 128 == 0 &&
+                        getenv("AEXQ_QGEMM_K64") == nullptr;
+      gc = QgemmConfig{fmt, bm, swiglu, sf16, g16, true, fd, k128};
     }
     plan->gentry = qgemm_find(gc);
     if (plan->gentry) {
@@ -1260,7 +1266,9 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     }
     // (at most 8 chunks for the LDS-direct kernel: single layers at M = 64
     // and 512 measured fastest at 4 to 8, slower at 14 to 28)
-    pick_split((long long)tiles_total * mtiles, K / 64, slots, step_us, wg_us,
+    const int kstep = plan->gentry->cfg.k128 ? 128 : 64;  // K per step of the kernel
+    if (plan->gentry->cfg.k128) step_us *= 2.0;
+    pick_split((long long)tiles_total * mtiles, K / kstep, slots, step_us, wg_us,
                plan->gentry->cfg.direct ? 8 : 1 << 30,
                (double)M * nw * tiles_total * plan->rows_per_tile * 4.0,
                &plan->sk_chunks, &plan->sk_cs);
@@ -1450,10 +1458,10 @@ extern "C" aexq_status aexq_plan_check(aexq_ctx* ctx, const aexq_weight* w, cons
     else if (plan.kind == kPlanGemm)
       snprintf(diag, diag_len,
                "kernel=qgemm bits=%d bm=%d swiglu=%d direct=%d fp16_dequant=%d rms_prepass=%d "
-               "tiles=%d grid=%d splitk=%d",
+               "tiles=%d grid=%d splitk=%d kstep=%d",
                w->bits, plan.gentry->cfg.bm, (int)plan.gentry->cfg.pair,
                (int)plan.gentry->cfg.direct, (int)plan.gentry->cfg.fd, (int)plan.rms_prepass,
-               plan.p.total_tiles, plan.grid, plan.sk_chunks);
+               plan.p.total_tiles, plan.grid, plan.sk_chunks, plan.gentry->cfg.k128 ? 128 : 64);
     else if (plan.kind == kPlanMfma)
       snprintf(diag, diag_len, "kernel=qmm bits=%d mt=%d nt=%d swiglu=%d wide=%d rms_prepass=%d "
                "tiles=%d grid=%d mblock=%d splitk=%d",

@@ -158,6 +158,7 @@ struct QgemmConfig {
   bool g16;    // Q4 with one scale per 16 codes
   bool direct; // LDS-direct pipeline (Q8; Q4 split scales in groups of 16 or 32)
   bool fd;     // Q4 weight tiles dequantised to fp16 (fp16(q * s)) for the MFMA
+  bool k128;   // fd at 64-row tiles: 128-wide K steps (K a multiple of 128)
 };
 typedef void (*QgemmFn)(const QmvParams, int);
 struct QgemmEntry {

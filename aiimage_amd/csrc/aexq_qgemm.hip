@@ -28,8 +28,20 @@ namespace aexq {
   QGDL_PS(kQ8, BM, 0, false), QGDL_PS(kQ4, BM, 32, false), QGDL_PS(kQ4, BM, 16, false), \
       QGDL_PS(kQ4, BM, 32, true), QGDL_PS(kQ4, BM, 16, true)
 
+// Q4 fp16 tiles at 64-row tiles with 128-wide K steps: two LDS stages (25-28
+// KB each), three workgroups per CU where they fit
+#define QGDL128(PAIR, SF16, G)                                                  \
+  QgemmEntry {                                                                 \
+    QgemmConfig{kQ4, 64, PAIR, SF16, G == 16, true, true, true},               \
+        &qgemm_dl_kernel<kQ4, 64, PAIR, SF16, G, true, 3, 128, 2>              \
+  }
+#define QGDL128_G(G)                                                           \
+  QGDL128(false, true, G), QGDL128(false, false, G), QGDL128(true, true, G),   \
+      QGDL128(true, false, G)
+
 static const QgemmEntry kTableG[] = {QGE(false, true), QGE(false, false), QGE(true, true),
-                                     QGE(true, false), QGDL_BM(64), QGDL_BM(128)};
+                                     QGE(true, false), QGDL_BM(64), QGDL_BM(128),
+                                     QGDL128_G(32), QGDL128_G(16)};
 
 static constexpr int kCountG = (int)(sizeof(kTableG) / sizeof(kTableG[0]));
 
@@ -37,7 +49,7 @@ const QgemmEntry* qgemm_find(const QgemmConfig& c) {
   for (int i = 0; i < kCountG; ++i) {
     const QgemmConfig& q = kTableG[i].cfg;
     if (q.fmt == c.fmt && q.bm == c.bm && q.pair == c.pair && q.sf16 == c.sf16 &&
-        q.g16 == c.g16 && q.direct == c.direct && q.fd == c.fd)
+        q.g16 == c.g16 && q.direct == c.direct && q.fd == c.fd && q.k128 == c.k128)
       return &kTableG[i];
   }
   return nullptr;

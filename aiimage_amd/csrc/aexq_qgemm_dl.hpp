@@ -141,20 +141,25 @@ __device__ __forceinline__ void q4_pairs_seq(uint32_t w, uint32_t q[4]) {
   }
 }
 
-template <int FMT, int BM, bool PAIR, bool SF16, int G, bool FD>
+template <int FMT, int BM, bool PAIR, bool SF16, int G, bool FD, int KS = 64>
 struct QGemmDL {
   static_assert(FMT == kQ8 ? G == 0 : (G == 16 || G == 32),
                 "Q8 (row scales) or Q4 in groups of 16 or 32");
   static_assert(!FD || FMT == kQ4, "fp16 dequantisation is a Q4 form");
   static_assert(BM == 64 || BM == 128, "64- or 128-row activation tiles");
+  static_assert(KS == 64 || (KS == 128 && FD), "128-wide K steps are a form of Q4 fp16 tiles");
   static constexpr int BN = 128;                  // weight rows of a tile
-  static constexpr int BK = 64;                   // K per step
+  static constexpr int BK = KS;                   // K per step
+  static constexpr int NE = BK / 32;              // MFMA K extents per step
+  static constexpr int RA = 2 * BK;               // activation bytes per row and step
   static constexpr int NOUT = PAIR ? BN / 2 : BN;  // output columns of a tile
   static constexpr int WR = BN / 4;               // weight rows per wave (32)
   static constexpr int TN = WR / 16;              // 16-row B blocks per wave (2)
   static constexpr int TM = BM / 16;              // 16-row A blocks per wave (every row)
-  static constexpr int CP = FMT == kQ8 ? 64 : 32;  // code bytes per row and step
-  static constexpr int A_BYTES = BM * 128;
+  static constexpr int CP = FMT == kQ8 ? 64 : BK / 2;  // code bytes per row and step
+  // codes read as Q8's: a lane's 16 bytes of a 64-byte row step (Q8, Q4 at KS 128)
+  static constexpr bool C16 = CP == 64;
+  static constexpr int A_BYTES = BM * RA;
   static constexpr int B_BYTES = BN * CP;
   static constexpr int SPR = FMT == kQ8 ? 0 : BK / G;    // Q4 scales per row and step
   static constexpr int SB = SF16 ? 2 : 4;                // bytes per scale
@@ -174,6 +179,18 @@ struct QGemmDL {
     if constexpr (PAIR)
       return (tn >= TN / 2 ? 64 : 0) + wn * (WR / 2) + 16 * (tn % (TN / 2));
     return wn * WR + 16 * tn;
+  }
+
+  // Chunk swizzle of activation row r (16-byte chunk c of the row at slot
+  // c ^ aswz(r)): the fragment reads of 16 rows by four lane quarters then
+  // fall on distinct 16-byte slots of each 512-byte bank line (gfx950 serves
+  // 32 lanes' 16-byte LDS reads per pass).  8 chunks a row (64-wide steps):
+  // (r & 7) ^ ((r >> 3) & 1); 16 chunks (128-wide): ((r >> 1) & 3) + 8 ((r >> 3) & 1).
+  static __device__ __forceinline__ int aswz(int r) {
+    if constexpr (RA == 128)
+      return (r & 7) ^ ((r >> 3) & 1);
+    else
+      return ((r >> 1) & 3) + 8 * ((r >> 3) & 1);
   }
 
   struct Src {
@@ -200,16 +217,24 @@ struct QGemmDL {
     s.xr = __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, mrows * rs2, kBufferRsrcWord3);
 #pragma unroll
     for (int t = 0; t < A_INST; ++t) {
-      const int row = 8 * (wave * A_INST + t) + (lane >> 3);
-      const int c = (lane & 7) ^ ((row & 7) ^ ((row >> 3) & 1));
+      // an instruction covers 1024 / RA rows; chunk slot (lane % CH) of a row
+      // holds chunk slot ^ aswz(row)
+      constexpr int CH = RA / 16;  // 16-byte chunks per activation row and step
+      const int row = (1024 / RA) * (wave * A_INST + t) + lane / CH;
+      const int c = (lane % CH) ^ aswz(row);
       s.oa[t] = row * rs2 + c * 16;
     }
-    if constexpr (FMT == kQ8) {
+    if constexpr (C16) {
 #pragma unroll
       for (int t = 0; t < B_INST; ++t) {
         const int r = 16 * (wave * B_INST + t) + (lane & 15);
         s.ob[t] = (PAIR ? (r & 63) : r) * rb + 16 * (lane >> 4);
       }
+    } else {
+      const int r = 32 * wave + 16 * (lane >> 5) + (lane & 15);
+      s.ob[0] = (PAIR ? (r & 63) : r) * rb + 16 * ((lane >> 4) & 1);
+    }
+    if constexpr (FMT == kQ8) {
       // row scales: wave 0 rows 0-63 (the gate rows of a pair), wave 1 rows
       // 64-127 (the up rows); fp16: lane i fetches rows 2i, 2i + 1 (lanes 32..
       // fall past the rows), fp32: row i
@@ -226,8 +251,6 @@ struct QGemmDL {
                                                kBufferRsrcWord3);
       s.os[0] = 4 * lane;
     } else {
-      const int r = 32 * wave + 16 * (lane >> 5) + (lane & 15);
-      s.ob[0] = (PAIR ? (r & 63) : r) * rb + 16 * ((lane >> 4) & 1);
       // scales: load i of wave w covers rows S_RPI (w S_INST + i) .. (every
       // row's SPR scales of the step); one weight per wave (the up weight of
       // a pair from row 64)
@@ -253,7 +276,7 @@ struct QGemmDL {
   static __device__ __forceinline__ void issue(const Src& s, uint32_t base, int wave, int st) {
 #pragma unroll
     for (int t = 0; t < A_INST; ++t)
-      dma<16>(s.xr, base + (wave * A_INST + t) * 1024, s.oa[t] + st * 128);
+      dma<16>(s.xr, base + (wave * A_INST + t) * 1024, s.oa[t] + st * RA);
 #pragma unroll
     for (int t = 0; t < B_INST; ++t)
       dma<16>(s.wr, base + A_BYTES + (wave * B_INST + t) * 1024, s.ob[t] + st * CP);
@@ -269,17 +292,20 @@ struct QGemmDL {
   // K half and the raw codes (and Q4 scales) of both halves.
   // (Q4: the lane's 8 codes of each MFMA extent and the row's scales of the
   // step, one per extent or two for groups of 16; FD: the lane's own scale)
-  static constexpr int NS = FMT == kQ8 ? 1 : (FD ? 1 : SPR);
-  // K order permuted as Q8's (lane group g: chunks 2 g and 2 g + 1 of the step)
+  // (FD: the scale groups of a lane's chunks of a step: one, or two for groups
+  // of 16 at 128-wide steps)
+  static constexpr int NS = FMT == kQ8 ? 1 : (FD ? (NE * 8 / G > 1 ? NE * 8 / G : 1) : SPR);
+  // K order permuted as Q8's (lane group g: chunks NE g .. NE g + NE - 1 of the
+  // step, one per MFMA extent)
   static constexpr bool PERM = FMT == kQ8 || FD;
   struct Frag {
     f16x8 a[TM];
-    typename std::conditional<FMT == kQ8, u32x4, u32x2>::type c[TN];
+    typename std::conditional<C16, u32x4, u32x2>::type c[TN];
     uint32_t s[TN][NS];
   };
 
   struct Lane {
-    int a_off[2];  // activation fragment offset of K half 0 / 1 (row l16 of block 0)
+    int a_off[NE];  // activation fragment offset of extent 0 .. NE - 1 (row l16 of block 0)
     int b_off;     // code fragment offset inside a 16-row block
     int s_off;     // scale offset (row l16, the lane group's scale group) inside block row 0
   };
@@ -287,16 +313,18 @@ struct QGemmDL {
   static __device__ __forceinline__ Lane lane_offsets(int lane) {
     Lane L;
     const int l16 = lane & 15, lk = lane >> 4;
-    const int f = (l16 & 7) ^ (l16 >> 3);
+    const int f = aswz(l16);
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-      L.a_off[kk] = l16 * 128 + (((PERM ? 2 * lk + kk : 4 * kk + lk) ^ f) << 4);
+    for (int kk = 0; kk < NE; ++kk)
+      L.a_off[kk] = l16 * RA + (((PERM ? NE * lk + kk : 4 * kk + lk) ^ f) << 4);
+    // 16-byte code reads (C16): [quarter][row] per 16-row block, lane l at 16 l.
     // Q4 codes [half][row] per 16-row block: FD chunks 2 lk, 2 lk + 1 (half
     // lk / 2, bytes 8 (lk % 2) ..); exact: dword lk of each half (+ 256 kk)
-    L.b_off = FMT == kQ8 ? 16 * lane
-                         : (FD ? (lk >> 1) * 256 + l16 * 16 + (lk & 1) * 8 : l16 * 16 + 4 * lk);
-    // FD: scale group 16 lk / G of the step (lk / 2 for groups of 32, lk for 16)
-    L.s_off = FMT == kQ8 ? 0 : l16 * (SPR * SB) + (FD ? (16 * lk / G) * SB : 0);
+    L.b_off = C16 ? 16 * lane
+                  : (FD ? (lk >> 1) * 256 + l16 * 16 + (lk & 1) * 8 : l16 * 16 + 4 * lk);
+    // FD: the scale group of chunk NE lk (lk / 2 for groups of 32 at 64-wide
+    // steps, lk for 16 or for 32 at 128-wide, 2 lk for 16 at 128-wide)
+    L.s_off = FMT == kQ8 ? 0 : l16 * (SPR * SB) + (FD ? (NE * lk * 8 / G) * SB : 0);
     return L;
   }
 
@@ -304,14 +332,14 @@ struct QGemmDL {
                                                 f16x8 (&a)[TM]) {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm)
-      a[tm] = *(const f16x8*)(base + 16 * tm * 128 + L.a_off[kk]);
+      a[tm] = *(const f16x8*)(base + 16 * tm * RA + L.a_off[kk]);
   }
 
   static __device__ __forceinline__ void read_b(const char* base, const Lane& L, int wn, Frag& f) {
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
       const int blk = brow(wn, tn) >> 4;
-      if constexpr (FMT == kQ8) {
+      if constexpr (C16) {
         f.c[tn] = *(const u32x4*)(base + A_BYTES + blk * 1024 + L.b_off);
       } else {
         const char* bb = base + A_BYTES + blk * 512 + L.b_off;
@@ -319,6 +347,8 @@ struct QGemmDL {
           f.c[tn] = *(const u32x2*)bb;  // chunk 2 lk, then 2 lk + 1
         else
           f.c[tn] = u32x2{*(const uint32_t*)bb, *(const uint32_t*)(bb + 256)};
+      }
+      if constexpr (FMT == kQ4) {
         const char* sb = base + A_BYTES + B_BYTES + blk * 16 * (SPR * SB) + L.s_off;
 #pragma unroll
         for (int i = 0; i < NS; ++i)
@@ -328,7 +358,7 @@ struct QGemmDL {
     }
   }
 
-  // The MFMAs of K half kk from the activation blocks a and the step's codes.
+  // The MFMAs of K extent kk from the activation blocks a and the step's codes.
   static __device__ __forceinline__ void mfma_half(int kk, const f16x8 (&a)[TM], const Frag& f,
                                                    f32x4 (&acc)[TM][TN]) {
 #pragma unroll
@@ -346,7 +376,7 @@ struct QGemmDL {
         // the MFMA accumulates the row
         uint32_t e[4];
         q4_pairs_seq(f.c[tn][kk], e);
-        const f16 s16 = (f16)scale_of(f.s[tn][0], SF16);
+        const f16 s16 = (f16)scale_of(f.s[tn][kk * NS / NE], SF16);
         const f16x2 s2 = {s16, s16};
 #pragma unroll
         for (int j = 0; j < 4; ++j) e[j] = as_u(as_h2(e[j]) * s2);
@@ -605,10 +635,27 @@ struct QGemmDL {
   }
 };
 
-// One step of the pipeline on LDS stage `cur` (the next step's stage `nxt`,
-// the stage refilled with step st + 3 is `cur` itself): on entry f holds the
-// step's codes and first-half activation blocks; on return, the next step's.
-template <typename G>
+// Waits until the loads of at most min(KMAX, ahead) steps (NL instructions
+// each) are outstanding, the older ones landed; `ahead` is wave-uniform.
+template <int NL, int KMAX>
+__device__ __forceinline__ void wait_steps(int ahead) {
+  if constexpr (KMAX > 0) {
+    if (ahead >= KMAX)
+      wait_vm<KMAX * NL>();
+    else
+      wait_steps<NL, KMAX - 1>(ahead);
+  } else {
+    wait_vm<0>();
+  }
+}
+
+// One step of the pipeline on LDS stage `cur` of an NST-stage ring (the next
+// step's stage `nxt`; the stage refilled with step st + NST is `cur` itself):
+// on entry f holds the step's codes and first-extent activation blocks; on
+// return, the next step's.  The barrier sits before the last extent's MFMAs,
+// which cover the next step's first fragment reads; the MFMAs before it
+// cover the reads of the extents after them and the barrier wait.
+template <typename G, int NST>
 __device__ __forceinline__ void qgemm_dl_step(const typename G::Src& src, const typename G::Lane& L,
                                               char* cur, char* nxt, int wave, int wn,
                                               int st, int s1, typename G::Frag& f,
@@ -617,35 +664,40 @@ __device__ __forceinline__ void qgemm_dl_step(const typename G::Src& src, const 
   G::read_a(cur, L, 1, a1);
   __builtin_amdgcn_sched_barrier(0);  // the reads go out ahead of the MFMAs
   G::mfma_half(0, f.a, f, acc);
+  if constexpr (G::NE == 4) {
+    f16x8 a2[G::TM];
+    G::read_a(cur, L, 2, a2);
+    __builtin_amdgcn_sched_barrier(0);
+    G::mfma_half(1, a1, f, acc);
+    G::read_a(cur, L, 3, a1);
+    __builtin_amdgcn_sched_barrier(0);
+    G::mfma_half(2, a2, f, acc);
+  }
   // this step's fragments are in registers before any wave refills `cur`;
   // step st + 1's loads (the oldest in flight) have landed
   wait_lgkm0();
-  if (st + 2 < s1)
-    wait_vm<G::NL>();
-  else
-    wait_vm<0>();
+  wait_steps<G::NL, NST - 2>(s1 - st - 2);
   bar();
-  if (st + 3 < s1) G::issue(src, lds_addr(cur), wave, st + 3);
+  if (st + NST < s1) G::issue(src, lds_addr(cur), wave, st + NST);
   typename G::Frag g;
   if (st + 1 < s1) {
     G::read_a(nxt, L, 0, g.a);
     G::read_b(nxt, L, wn, g);
   }
   __builtin_amdgcn_sched_barrier(0);
-  G::mfma_half(1, a1, f, acc);
+  G::mfma_half(G::NE - 1, a1, f, acc);
   f = g;
 }
 
-template <int FMT, int BM, bool PAIR, bool SF16, int G, bool FD, int WPE>
+template <int FMT, int BM, bool PAIR, bool SF16, int G, bool FD, int WPE, int KS = 64, int NST = 3>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WPE)))
 void qgemm_dl_kernel(const QmvParams p, int mtiles) {
-  using Q = QGemmDL<FMT, BM, PAIR, SF16, G, FD>;
-  static_assert(Q::C_BYTES <= 3 * Q::STAGE, "the accumulator tile reuses the stages");
-  __shared__ __align__(1024) char lds[3 * Q::STAGE];
+  using Q = QGemmDL<FMT, BM, PAIR, SF16, G, FD, KS>;
+  static_assert(NST == 2 || NST == 3, "a ring of two or three LDS stages");
+  static_assert(Q::C_BYTES <= NST * Q::STAGE, "the accumulator tile reuses the stages");
+  __shared__ __align__(1024) char lds[NST * Q::STAGE];
   __shared__ __align__(16) char qs[FMT == kQ8 ? 1024 : 16];  // Q8 row scales of the tile
-  char* const st0 = lds;
-  char* const st1 = lds + Q::STAGE;
-  char* const st2 = lds + 2 * Q::STAGE;
+  char* const sg[3] = {lds, lds + Q::STAGE, lds + (NST - 1) * Q::STAGE};
   // weight tile tn, row tile tm and K chunk kc of this workgroup (the chunks
   // of a split K sit next to each other on one XCD); readfirstlane keeps the
   // workgroup-uniform coordinates in scalar registers
@@ -683,36 +735,33 @@ void qgemm_dl_kernel(const QmvParams p, int mtiles) {
 #pragma unroll
     for (int c = 0; c < Q::TN; ++c) acc[a][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // prologue: steps s0 .. s0 + 2 in flight, step s0 landed and its first
-  // fragments read
+  // prologue: steps s0 .. s0 + NST - 1 in flight, step s0 landed and its
+  // first fragments read
   // Q8: the tile's row scales go to LDS with the first step (waves 0 and 1:
   // rows 0-63 and 64-127, or the gate and up rows of a pair)
   if constexpr (FMT == kQ8)
     if (S == 1 && wave < 2) dma<4>(src.sr, lds_addr(qs) + wave * 512, src.os[0]);
-  Q::issue(src, lds_addr(st0), wave, s0);
-  if (s0 + 1 < s1) Q::issue(src, lds_addr(st1), wave, s0 + 1);
-  if (s0 + 2 < s1) Q::issue(src, lds_addr(st2), wave, s0 + 2);
-  if (s0 + 2 < s1)
-    wait_vm<2 * Q::NL>();  // (the row scales, issued first, have landed too)
-  else if (s0 + 1 < s1)
-    wait_vm<Q::NL>();
-  else
-    wait_vm<0>();
+#pragma unroll
+  for (int i = 0; i < NST; ++i)
+    if (s0 + i < s1) Q::issue(src, lds_addr(sg[i]), wave, s0 + i);
+  // (the row scales, issued first, have landed with step s0)
+  wait_steps<Q::NL, NST - 1>(s1 - s0 - 1);
   bar();
   typename Q::Frag f;
-  Q::read_a(st0, L, 0, f.a);
-  Q::read_b(st0, L, wn, f);
-  // three steps per iteration: the stages rotate with compile-time names
+  Q::read_a(sg[0], L, 0, f.a);
+  Q::read_b(sg[0], L, wn, f);
+  // NST steps per iteration: the stages rotate with compile-time names
   int st = s0;
-  for (int it = (s1 - s0) / 3; it > 0; --it) {
-    qgemm_dl_step<Q>(src, L, st0, st1, wave, wn, st, s1, f, acc);
-    qgemm_dl_step<Q>(src, L, st1, st2, wave, wn, st + 1, s1, f, acc);
-    qgemm_dl_step<Q>(src, L, st2, st0, wave, wn, st + 2, s1, f, acc);
-    st += 3;
+  for (int it = (s1 - s0) / NST; it > 0; --it) {
+#pragma unroll
+    for (int i = 0; i < NST; ++i)
+      qgemm_dl_step<Q, NST>(src, L, sg[i], sg[(i + 1) % NST], wave, wn, st + i, s1, f, acc);
+    st += NST;
   }
   const int tail = s1 - st;
-  if (tail >= 1) qgemm_dl_step<Q>(src, L, st0, st1, wave, wn, st, s1, f, acc);
-  if (tail >= 2) qgemm_dl_step<Q>(src, L, st1, st2, wave, wn, st + 1, s1, f, acc);
+#pragma unroll
+  for (int i = 0; i < NST - 1; ++i)
+    if (tail > i) qgemm_dl_step<Q, NST>(src, L, sg[i], sg[i + 1], wave, wn, st + i, s1, f, acc);
   wait_lgkm0();  // the last fragments are read before the stages become C
   bar();
   if (S == 1)

@@ -78,6 +78,14 @@ def _splitk(plan):
     raise AssertionError(plan)
 
 
+def _kstep(plan):
+    """K per step of a tiled-GEMM plan (64, or 128 for Q4 fp16 tiles at 64-row tiles)."""
+    for tok in plan.split():
+        if tok.startswith("kstep="):
+            return int(tok[6:])
+    raise AssertionError(plan)
+
+
 # (bits, scale_f16, n, k, m, fp32 out, kernel): a layer's linears at the
 # config-4 row counts, one copy each, plus ragged N and M
 CASES = [
@@ -213,14 +221,14 @@ def test_forced_chunk_counts(ctx, aexq, orc, monkeypatch, chunks, kernel, m):
     _announce(f"splitk forced {chunks} {kernel} m={m}")
     from aiimage_amd import synth
     monkeypatch.setenv("AEXQ_SPLITK", chunks)
-    n, k = 640, 3584   # 14 wide steps, 56 GEMM steps
+    n, k = 640, 3584   # 14 wide steps; 56 GEMM steps of 64, 28 of 128
     w, wf = _weight(ctx, aexq, orc, 4, n, k, 31 + m)
     x16 = synth.activations(m, k, 32)
     y = aexq.new_activation(m, n, torch.float32, aexq.LAYOUT_PACK4_LINEAR)
     xd = aexq.describe(dev(x16), m, k)
     yd = aexq.describe(y, m, n, aexq.LAYOUT_PACK4_LINEAR)
     plan = ctx.plan_check(w, xd, yd)
-    steps = k // (256 if kernel == "qmm" else 64)
+    steps = k // (256 if kernel == "qmm" else _kstep(plan))
     want = min(int(chunks), steps)
     cs = -(-steps // want)
     assert plan.startswith(f"kernel={kernel}") and _splitk(plan) == -(-steps // cs), plan
