@@ -1111,8 +1111,9 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
       if (fmt == kQ8 && mt == 1) wc.nt = nt > 1 ? nt / 2 : 1;
       if (gmode == kG16) wc.nt = nt > 1 ? nt / 2 : 1;  // twice the scales per block
       if (argmax) {
-        // the LM head: argmax partials fused, one 16-row block per wave (more,
-        // shorter workgroups over the vocabulary measured faster).  The plain
+        // the LM head: argmax partials fused, one 16-row block per wave (two
+        // blocks need 208 VGPRs against 150, and ran config 5 at M = 8 in
+        // 57-65 us against 45-56 at grids of 2-6 workgroups per CU).  The plain
         // kernel's logits and an argmax launch over them measured no faster
         // (config 5, M = 8: 46-47 us against 45-47): a second launch costs as
         // much as the fused form's epilogue and merge.
@@ -1291,7 +1292,8 @@ static aexq_status make_plan(aexq_ctx* ctx, int count, const aexq_weight* const*
     const long long need = wide ? items : (items + kWaves - 1) / kWaves;
     // Q8 on the wide kernel streams best with 6 workgroups per CU queued
     // (config 4, M = 16: 5.35 TB/s at the resident 2, 5.71 at 6); Q4 with the
-    // resident count (3.80 at 2, 3.36 at 6)
+    // resident count (3.80 at 2, 3.36 at 6), and so does the fused LM head
+    // (config 5, M = 8: 45 us at the resident 3, 48 at 2, 56 at 4, 53 at 6)
     long long grid_cap = cap;
     if (wide && fmt == kQ8 && !plan->mentry->cfg.argmax && !env && per_cu < 6)
       grid_cap = 6LL * ctx->cus;
@@ -1582,7 +1584,21 @@ static bool lmhead_fused(const Plan& plan) {
 static aexq_status lmhead_fused_launch(aexq_ctx* ctx, Plan& plan, const char* op,
                                        int32_t* argmax, float* top2_gap, const Partials* fixed) {
   const int M = plan.p.m;
-  const int parts = plan.grid;  // one partial per workgroup and row
+  // the wide kernel runs its tiles on any grid: within a fixed scratch it
+  // takes fewer workgroups rather than refuse
+  if (fixed && plan.kind == kPlanMfma && (long long)plan.grid * M + 32LL * M > fixed->cap) {
+    const long long fit = fixed->cap / M - 32;
+    if (fit >= 1 && fit < plan.grid) plan.grid = (int)fit;
+  }
+  const int grid = plan.grid;  // one partial per workgroup and row
+  // a grid of more than 512 workgroups merges in two levels: runs of G = 2^g
+  // >= 32 workgroups, at most 31 run mergers (fewer than one XCD's resident
+  // workgroups even at one per CU), each polling one round of partials;
+  // AEXQ_ARGMAX_ONE_LEVEL keeps the single merge
+  int group = 0;
+  if (grid > 512 && getenv("AEXQ_ARGMAX_ONE_LEVEL") == nullptr)
+    for (group = 5; (grid - 1) >> group > 31;) ++group;
+  const int parts = grid + (group ? (grid - 1) >> group : 0);  // and a group partial per run
   const long long need = (long long)parts * M;
   // the MFMA path launches once per block of mblock rows, each merging its own
   const int rows = plan.kind == kPlanMfma && plan.mblock < M ? plan.mblock : M;
@@ -1593,7 +1609,7 @@ static aexq_status lmhead_fused_launch(aexq_ctx* ctx, Plan& plan, const char* op
   if (fixed) {
     if (need > fixed->cap)
       return fail(AEXQ_ERR_UNSUPPORTED, op,
-                  "%d workgroups x %d rows = %lld argmax partials exceed the fixed scratch of "
+                  "%d partials a row (one per workgroup and merged run) x %d rows = %lld exceed the fixed scratch of "
                   "%lld | rejectedFallback=allocation",
                   parts, M, need, fixed->cap);
     pt = *fixed;
@@ -1603,6 +1619,7 @@ static aexq_status lmhead_fused_launch(aexq_ctx* ctx, Plan& plan, const char* op
   }
   plan.p.parts = parts;
   bind_partials(plan.p, pt, argmax, top2_gap);
+  plan.p.am_group = group;
   if (plan.fast) {
     hipError_t e = qmv_launch(plan.entry, plan.p, plan.grid, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, op, "lm head launch");

@@ -229,11 +229,90 @@ __device__ __forceinline__ void argmax_top2_combine(unsigned long long& k1, unsi
   ks = ks < os ? os : ks;
 }
 
+// Polls n tagged partials from entry e0 of the first plane at `base` (the
+// other two planes `plane` words on), thread gl of a row's gsz threads taking
+// entries gl, gl + gsz, ...; folds each into (k1, k2, ks).  False: a wait ran
+// out.  Addresses are a uniform base plus 32-bit byte offsets (every plane
+// holds fewer than 2^29 words), one register per load rather than a pointer
+// pair, which keeps the poll within the kernel's register budget.
+template <int kB>
+__device__ __forceinline__ bool argmax_poll(const unsigned long long* base, long long plane,
+                                            long long e0, int n, int gl, int gsz, uint32_t tag,
+                                            unsigned long long& k1, unsigned long long& k2,
+                                            uint32_t& ks) {
+  const char* b0 = (const char*)base;
+  const uint32_t o0 = (uint32_t)(e0 * 8), pb = (uint32_t)(plane * 8);
+  auto word = [&](int e, int q) {
+    return __hip_atomic_load((const unsigned long long*)(b0 + (o0 + (uint32_t)e * 8u + q * pb)),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  for (int i0 = gl; i0 < n; i0 += gsz * kB) {
+    unsigned long long a[kB], b[kB], c[kB];
+    bool ok[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      const int e = i0 + j * gsz;
+      ok[j] = e >= n;
+      if (!ok[j]) {
+        a[j] = word(e, 0);
+        b[j] = word(e, 1);
+        c[j] = word(e, 2);
+      }
+    }
+    for (int spin = 0;; ++spin) {
+      bool all = true;
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        if (!ok[j]) {
+          ok[j] = (uint32_t)(a[j] >> 32) == tag && (uint32_t)(b[j] >> 32) == tag &&
+                  (uint32_t)(c[j] >> 32) == tag;
+          all = all && ok[j];
+        }
+      }
+      if (all) break;
+      if (spin >= kArgSpinLimit) return false;
+      __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int e = i0 + j * gsz;
+        if (!ok[j]) {
+          a[j] = word(e, 0);
+          b[j] = word(e, 1);
+          c[j] = word(e, 2);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      if (i0 + j * gsz < n) {
+        const float v = __uint_as_float((uint32_t)a[j]);
+        const float sv = __uint_as_float((uint32_t)c[j]);
+        const uint32_t ix = (uint32_t)b[j];
+        if (!__builtin_isnan(sv)) {
+          const uint32_t o = argmax_ord(sv);
+          ks = ks < o ? o : ks;
+        }
+        if (!__builtin_isnan(v))
+          argmax_top2_insert(k1, k2, ((unsigned long long)argmax_ord(v) << 32) | (uint32_t)~ix);
+        else if (ix == 0)
+          argmax_top2_insert(k1, k2, ~0ull);
+      }
+    }
+  }
+  return true;
+}
+
 // In-kernel merge of the argmax partials (p.am_tagged non-null), called by
 // every thread of every workgroup after its partial stores; only the grid's
-// last workgroup works.  Workgroups are dispatched in index order, so when the
-// last one runs every other has been dispatched and finishes without waiting
-// on anything: the last one's wait ends.
+// last workgroup works, and with p.am_group = g > 0 the last workgroup of each
+// full run of G = 2^g as well.  A merging workgroup waits only on partials of
+// workgroups with lower indices, dispatched before it; those finish or wait
+// in turn only on lower indices, so every wait ends.  (Should dispatch order
+// differ across XCDs, a waiting run merger holds one slot, and the host keeps
+// the run mergers fewer than one XCD's resident slots.)  Two levels keep the
+// merge at one poll round per level when the grid queues thousands of
+// workgroups: a run merger folds its G partials into a group partial of the
+// same three-word form while the rest of the grid still streams.
 //
 // Its threads split into one group per row (a power of two, 256 / rows or
 // less); a thread polls its share of the row's partials (agent-coherent loads,
@@ -249,15 +328,22 @@ __device__ __forceinline__ void argmax_top2_combine(unsigned long long& k1, unsi
 // The top-2 gap is best - max(ks, value of k2): the best of all candidates but
 // the winner, as the sequential scan forms it.  A wait that runs out writes
 // index -1 and a NaN gap for every row.  Then the tag becomes the next
-// launch's epoch.
+// launch's epoch.  A run merger whose wait runs out stores no group partial,
+// so the grid's last workgroup runs out too and reports the failure.
 template <int kB>
 __device__ __forceinline__ void argmax_tail(const QmvParams& p, uint32_t tag) {
-  if (!p.am_tagged || blockIdx.x != gridDim.x - 1) return;
+  if (!p.am_tagged) return;
+  const int parts = p.parts, gs = p.am_group, G = gs > 0 ? 1 << gs : 0;
+  const bool last = blockIdx.x == gridDim.x - 1;
+  if (!last && (gs <= 0 || ((int)blockIdx.x & (G - 1)) != G - 1)) return;
   __shared__ unsigned long long s_k1[kArgMergeRows], s_k2[kArgMergeRows];
   __shared__ uint32_t s_ks[kArgMergeRows];
   __shared__ int s_fail;
   const int rows = p.m;  // <= kArgMergeRows (host-checked)
-  const int parts = p.parts;
+  // full runs before the last workgroup's; their group partials follow the
+  // grid's partials in each row (parts = grid + groups words a row), so the
+  // last workgroup's run and the group partials are one range
+  const int groups = gs > 0 ? ((int)gridDim.x - 1) >> gs : 0;
   int gsz = kThreads;  // threads per row
   while (gsz > 8 && gsz * rows > kThreads) gsz >>= 1;
   const int r = (int)threadIdx.x / gsz, gl = (int)threadIdx.x % gsz;
@@ -267,66 +353,12 @@ __device__ __forceinline__ void argmax_tail(const QmvParams& p, uint32_t tag) {
   uint32_t ks = argmax_ord(-INFINITY);
   bool fail = false;
   if (r < rows) {
-    const long long row0 = (long long)(p.m_base + r) * parts;
-    const unsigned long long* w0 = p.am_tagged + row0;
-    const unsigned long long* w1 = w0 + p.am_plane;
-    const unsigned long long* w2 = w0 + 2 * p.am_plane;
-    for (int i0 = gl; i0 < parts && !fail; i0 += gsz * kB) {
-      unsigned long long a[kB], b[kB], c[kB];
-      bool ok[kB];
-#pragma unroll
-      for (int j = 0; j < kB; ++j) {
-        const int e = i0 + j * gsz;
-        ok[j] = e >= parts;
-        if (!ok[j]) {
-          a[j] = __hip_atomic_load(w0 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          b[j] = __hip_atomic_load(w1 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          c[j] = __hip_atomic_load(w2 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-      for (int spin = 0;; ++spin) {
-        bool all = true;
-#pragma unroll
-        for (int j = 0; j < kB; ++j) {
-          if (!ok[j]) {
-            ok[j] = (uint32_t)(a[j] >> 32) == tag && (uint32_t)(b[j] >> 32) == tag &&
-                    (uint32_t)(c[j] >> 32) == tag;
-            all = all && ok[j];
-          }
-        }
-        if (all) break;
-        if (spin >= kArgSpinLimit) {
-          fail = true;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-#pragma unroll
-        for (int j = 0; j < kB; ++j) {
-          const int e = i0 + j * gsz;
-          if (!ok[j]) {
-            a[j] = __hip_atomic_load(w0 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            b[j] = __hip_atomic_load(w1 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            c[j] = __hip_atomic_load(w2 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < kB; ++j) {
-        if (i0 + j * gsz < parts) {
-          const float v = __uint_as_float((uint32_t)a[j]);
-          const float sv = __uint_as_float((uint32_t)c[j]);
-          const uint32_t ix = (uint32_t)b[j];
-          if (!__builtin_isnan(sv)) {
-            const uint32_t o = argmax_ord(sv);
-            ks = ks < o ? o : ks;
-          }
-          if (!__builtin_isnan(v))
-            argmax_top2_insert(k1, k2, ((unsigned long long)argmax_ord(v) << 32) | (uint32_t)~ix);
-          else if (ix == 0)
-            argmax_top2_insert(k1, k2, ~0ull);
-        }
-      }
-    }
+    const long long row = p.m_base + r;
+    // this workgroup's run: every partial, the last run with the group
+    // partials, or a full run (run merging needs partial i to be workgroup i's)
+    const int first = last ? groups * (G > 0 ? G : 0) : (int)blockIdx.x - (G - 1);
+    fail = !argmax_poll<kB>(p.am_tagged, p.am_plane, row * parts + first,
+                            last ? parts - first : G, gl, gsz, tag, k1, k2, ks);
   }
   // combine within each group (aligned lanes of one wave), then per wave
   const int span = gsz < 64 ? gsz : 64;
@@ -359,12 +391,21 @@ __device__ __forceinline__ void argmax_tail(const QmvParams& p, uint32_t tag) {
     float bs = argmax_unord(bks);
     if (b2) bs = fmaxf(bs, argmax_unord((uint32_t)(b2 >> 32)));
     const bool bad = s_fail != 0;
-    p.am_out[p.m_base + threadIdx.x] = bad ? -1 : bi;
-    if (p.am_gap)
-      p.am_gap[p.m_base + threadIdx.x] =
-          bad ? __builtin_nanf("") : (bs == -INFINITY ? INFINITY : bv - bs);
+    if (!last) {
+      // the run's group partial (an empty run: NaN at index 0x7fffffff, which
+      // never wins; a NaN at index 0 keeps index 0)
+      if (!bad)
+        argmax_partial_store(p, (long long)(p.m_base + threadIdx.x) * parts + (int)gridDim.x +
+                                    ((int)blockIdx.x >> gs),
+                             bv, b1 ? bi : 0x7fffffff, bs, tag);
+    } else {
+      p.am_out[p.m_base + threadIdx.x] = bad ? -1 : bi;
+      if (p.am_gap)
+        p.am_gap[p.m_base + threadIdx.x] =
+            bad ? __builtin_nanf("") : (bs == -INFINITY ? INFINITY : bv - bs);
+    }
   }
-  if (threadIdx.x == 0)
+  if (last && threadIdx.x == 0)
     __hip_atomic_store(p.am_epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -81,9 +81,15 @@ struct QmvParams {
   // launch's epoch, am_epoch[0] + 1 (0 skipped), read by every workgroup at
   // its start.  The last workgroup of the grid polls the words until all
   // carry the tag, merges them, writes the index / top-2 gap per row and
-  // stores the tag back into am_epoch[0].
+  // stores the tag back into am_epoch[0].  With am_group = g > 0 the merge
+  // has two levels: the last workgroup of each full run of G = 2^g (index % G ==
+  // G - 1, the grid's last excepted), groups = (grid - 1) / G runs, merges
+  // its run into a group partial at r * parts + grid + run (parts = grid +
+  // groups), and the grid's last workgroup merges its own run's partials and
+  // the group partials, one contiguous range of each row.
   unsigned long long* am_tagged;
   long long am_plane;
+  int am_group;
   unsigned* am_epoch;
   int32_t* am_out;
   float* am_gap;

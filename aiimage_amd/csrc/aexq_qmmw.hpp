@@ -485,15 +485,15 @@ void qmmw_kernel(const QmvParams p) {
   const int t0 = (int)((i0 / S) * steps + (i0 % S) * cs);
   const int t1 = i1 > i0 ? (int)(((i1 - 1) / S) * steps + min((int)((i1 - 1) % S + 1) * cs, steps))
                          : t0;
-  const uint32_t tag = ARGMAX ? argmax_tag(p) : 0u;
   if (t0 >= t1) {  // the whole workgroup: no barrier is left waiting
     if constexpr (ARGMAX) {
+      const uint32_t tag = argmax_tag(p);
       // an empty partial for each row (it never wins the merge)
       const int row = threadIdx.x;
       if (row < 16 * MT && row < p.m)
         argmax_partial_store(p, (long long)(p.m_base + row) * p.parts + blockIdx.x,
                              __builtin_nanf(""), 0x7fffffff, -INFINITY, tag);
-      argmax_tail<16>(p, tag);
+      argmax_tail<4>(p, tag);
     }
     return;
   }
@@ -581,8 +581,12 @@ void qmmw_kernel(const QmvParams p) {
     sl ^= 1;
   }
   if constexpr (ARGMAX) {
+    // the launch's tag, read only now: issued at the start, it would sit
+    // ahead of the weight loads in the memory counter, and the first wait for
+    // them would wait for this agent-coherent round trip too
+    const uint32_t tag = argmax_tag(p);
     Q::best_write(p, lane, wave, best, tag);
-    argmax_tail<16>(p, tag);
+    argmax_tail<4>(p, tag);
   }
 }
 

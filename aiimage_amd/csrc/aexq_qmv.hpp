@@ -587,7 +587,6 @@ void qmv_kernel(const QmvParams p) {
   const int t0 = ARGMAX ? 0 : (int)((long long)gw * p.total_tiles / nw);
   const int t1 = ARGMAX ? (wr1 - wr0 + Q::RW - 1) / Q::RW
                         : (int)((long long)(gw + 1) * p.total_tiles / nw);
-  const uint32_t tag = ARGMAX ? argmax_tag(p) : 0u;
 
   float bv[MMAX], bs[MMAX];
   int bi[MMAX];
@@ -704,6 +703,10 @@ void qmv_kernel(const QmvParams p) {
         }
       }
     }
+    // the launch's tag, read only now: a load issued at the start would sit
+    // ahead of the weight loads in the memory counter, and the first wait
+    // for them would wait for this agent-coherent round trip too
+    const uint32_t tag = argmax_tag(p);
     if (threadIdx.x < MMAX && (int)threadIdx.x < p.m) {
       const int m = threadIdx.x;
       float v = lv[m][0], s = ls[m][0];
@@ -712,7 +715,7 @@ void qmv_kernel(const QmvParams p) {
       for (int w = 1; w < kWaves; ++w) argmax_merge(v, i, s, lv[m][w], li[m][w], ls[m][w]);
       argmax_partial_store(p, (long long)m * p.parts + blockIdx.x, v, i, s, tag);
     }
-    argmax_tail<8>(p, tag);
+    argmax_tail<4>(p, tag);
   }
 }
 
