@@ -182,6 +182,29 @@ def test_merge_grids_shrink_and_grow(ctx, aexq, orc, monkeypatch, m, k):
     w.release()
 
 
+def test_merge_one_and_two_levels(ctx, aexq, orc, monkeypatch):
+    """A grid of 2048 workgroups merged in two levels (runs of 64, 31 run
+    mergers, then the grid's last workgroup) and in one: the same index and
+    the same gap bits, both the oracle's."""
+    from aiimage_amd import synth
+    m, k = 4, 1024
+    _announce(f"lm head merge one and two levels m={m} k={k} grid 8 per CU")
+    words, scales, _ = synth.q8_weights(N, k, 0xAE1E3200)
+    w = ctx.weight(aexq.QuantizedTensor(N * k, k, words, scales, bits=8), N, k)
+    deq = orc.dequant_q8(words, scales, N, k, scale_dtype=orc.SCALE_F16)
+    x16 = synth.activations(m, k, 0xAE1E3201)
+    wi, wg = _expect(orc, orc.gemm_gpu_semantics(x16.astype(np.float32), deq))
+    monkeypatch.setenv("AEXQ_QMM_BLOCKS_PER_CU", "8")
+    two = _run(ctx, aexq, w, x16, m, k)
+    monkeypatch.setenv("AEXQ_ARGMAX_ONE_LEVEL", "1")
+    one = _run(ctx, aexq, w, x16, m, k)
+    _check(two, (wi, wg))
+    _check(one, (wi, wg))
+    assert np.array_equal(two[0], one[0]), (two[0], one[0])
+    assert np.array_equal(two[1].view(np.uint32), one[1].view(np.uint32)), (two[1], one[1])
+    w.release()
+
+
 @pytest.mark.parametrize("dtype,rows,width,packed", [
     (torch.float32, 40, 151936, False),   # two launches of up to 32 rows, 16-byte loads
     (torch.float32, 3, 100003, False),    # odd row stride: element loads
