@@ -260,12 +260,14 @@ aexq_status aexq_lmhead_argmax_ex(aexq_ctx* ctx, const aexq_weight* w, const aex
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  No counterpart in the reference: it exists for those
  * callers only.  It allocates nothing: the argmax partials go to a fixed
- * device array of the library (3 x 32768 partial entries and the merge's
- * arrival counters, about 400 KiB per GPU, held until the process ends)
+ * device array of the library (3 x 16384 tagged 64-bit partial words and the
+ * merge's epoch word, about 384 KiB per GPU, held until the process ends)
  * instead of the context's growing scratch.  Only the
  * fused-argmax launches qualify (K a multiple of 16 at M = 1, of 128 above);
- * a launch needing more than 32768 (workgroup, row) partials, or the separate
- * logits pass, returns AEXQ_ERR_UNSUPPORTED.  Every call on one GPU shares the
+ * the wide MFMA launch (M >= 2) takes fewer workgroups where its partials
+ * would not fit; a launch that still needs more than 16384 (workgroup, row)
+ * partials, or the separate logits pass, returns AEXQ_ERR_UNSUPPORTED.  Every
+ * call on one GPU shares the
  * array: calls that overlap on a GPU (other streams or contexts) race.
  * Results equal aexq_lmhead_argmax's. */
 aexq_status aexq_lmhead_argmax_noalloc(aexq_ctx* ctx, const aexq_weight* w, const aexq_tensor* x,
